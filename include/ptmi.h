@@ -1,0 +1,152 @@
+/*
+ * libptmi — MI355X (gfx950) projection hot path for pitorch-style LLaMA-2.
+ *
+ * A C-ABI shared library: plain pointers and sizes, no C++ or torch types.
+ * Every entry point that can fail returns a ptmi status (0 = PTMI_OK) and
+ * leaves a message in ptmi_last_error().  Entry points whose reference
+ * counterpart returns void (the pt_matvec_fn drop-in) report failure the
+ * way the reference does — a panic: message on stderr, then abort().
+ *
+ * Threading: one library state per process, bound to one GPU and one HIP
+ * stream; calls are not re-entrant (the reference is single-threaded bare
+ * metal, pitorch/pt.c:19, pitorch/runtime/arena.c:5-8).
+ *
+ * Reference paths are relative to masonwang025/pitorch.
+ */
+#ifndef PTMI_H
+#define PTMI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    PTMI_OK = 0,
+    PTMI_ERR_ARG = 1,        /* bad shape / pointer / size                */
+    PTMI_ERR_OOM = 2,        /* device allocation failed                  */
+    PTMI_ERR_HIP = 3,        /* HIP runtime error                         */
+    PTMI_ERR_STATE = 4,      /* not initialised, or wrong object state    */
+    PTMI_ERR_NODEV = 5       /* no GPU visible                            */
+};
+
+/* ── library lifetime ─────────────────────────────────────────────────
+ * Replaces the VideoCore bring-up in pt_pi_init (pitorch/pt.c:38-44:
+ * qpu_enable, perf_init, gpu_arena_init).  ptmi_init selects the device
+ * and creates the library's stream; it is implied by every other entry
+ * point (device 0) if not called first.                                */
+int         ptmi_init(int device);
+void        ptmi_shutdown(void);
+const char *ptmi_last_error(void);
+int         ptmi_last_status(void);
+void       *ptmi_stream(void);          /* hipStream_t of all launches */
+int         ptmi_sync(void);            /* wait for the stream         */
+
+/* ── weight residency ─────────────────────────────────────────────────
+ * Register a llama2.c .bin blob (header + tensors, pitorch/model/
+ * llama2.c:9-70; size per pt_file_size, llama2.c:21-47).  The tensors are
+ * copied once into HBM in the device layout (per layer [wq;wk;wv] and
+ * row-interleaved [w1|w3]); afterwards any host pointer into the blob's
+ * weight tensors passed to ptmi_matvec resolves to its device copy.
+ * Replaces: the Pi's weights-in-ARM-RAM read through the TMU bus alias
+ * (pitorch/ops/matvec/matvec.c:13-30).                                 */
+int ptmi_register_weights(const void *blob, size_t bytes);
+/* Re-upload [ptr, ptr+bytes) of a registered blob after host writes
+ * (pitorch/train/pt_train.c:870-896 mutates W in place).               */
+int ptmi_invalidate(const void *ptr, size_t bytes);
+int ptmi_unregister_weights(const void *blob);
+
+/* ── matvec: y[out_dim] = W[out_dim, in_dim] . x[in_dim] ──────────────
+ * ptmi_matvec has exactly the pt_matvec_fn signature
+ * (pitorch/model/llama2.h:73-75) and replaces matvec_gpu/smatvec_tmu
+ * (pitorch/pt.c:21-25, pitorch/ops/matvec/matvec.c:13-86).  Host pointers;
+ * W is resolved through the residency map, else uploaded for the call.
+ * y is fully overwritten.  Unlike smatvec_tmu there is no out_dim%16
+ * constraint (matvec.c:15-16).  Panics (stderr + abort) on error, as the
+ * reference's demand() does.                                           */
+void ptmi_matvec(const float *W, const float *x, float *y, int out_dim, int in_dim);
+/* Same, returning a status instead of panicking. */
+int  ptmi_matvec_checked(const float *W, const float *x, float *y, int out_dim, int in_dim);
+/* Device pointers, enqueued on `stream` (NULL = the library stream), no
+ * synchronisation.  ld = row stride of W in floats (>= in_dim).        */
+int  ptmi_matvec_dev(const float *dW, long ld, const float *dx, float *dy,
+                     int out_dim, int in_dim, void *stream);
+
+/* ── training GEMMs (fp32, MFMA) ──────────────────────────────────────
+ * C[M,N] (+)= A[M,K] . B[K,N], all row-major.  Replaces sgemm_rect_tmu
+ * (pitorch/ops/gemm/gemm_rect.h:24-26; the num_qpus argument has no
+ * meaning here and is dropped) and sgemm_cpu (gemm.h:19-20, accumulate=0).
+ * Host pointers.                                                        */
+int ptmi_sgemm_rect(const float *A, const float *B, float *C,
+                    int M, int K, int N, int accumulate);
+/* dW[out,in] += sum_t dY[t,out] * X[t,in]  (TN GEMM, no host transpose).
+ * Same arguments as matmul_backward_weight_batched
+ * (pitorch/train/pt_train.c:475-477).  Host pointers.                   */
+int ptmi_matmul_backward_weight_batched(float *d_W, const float *d_y_all,
+                                        const float *x_all, int out_dim,
+                                        int in_dim, int T);
+/* dX[T,in] (+)= dY[T,out] . W[out,in]  (NN GEMM).  The batched form of
+ * backward_input_pretrans/matmul_backward_input (pt_train.c:442-453,
+ * pt_backward_ops.c:32-41) without the host transpose.  Host pointers. */
+int ptmi_matmul_backward_input_batched(float *d_x_all, const float *W,
+                                       const float *d_y_all, int out_dim,
+                                       int in_dim, int T, int accumulate);
+/* Device-pointer forms.  op: 0 = NN  C(+)=A.B,      A[M,K]  B[K,N]
+ *                            1 = TN  C(+)=A^T.B,    A[K,M]  B[K,N]
+ *                            2 = NT  C(+)=A.B^T,    A[M,K]  B[N,K]
+ * lda/ldb/ldc are row strides in floats.                                */
+int ptmi_gemm_dev(int op, const float *dA, long lda, const float *dB, long ldb,
+                  float *dC, long ldc, int M, int N, int K, int accumulate,
+                  void *stream);
+
+/* ── device-resident model (decode + training) ────────────────────────
+ * One registered blob plus device state: KV cache, activations and, when
+ * max_T > 0, training buffers and gradients.  Replaces pt_host_init /
+ * pt_pi_init (pitorch/pt.c:38-114, 232-248).                            */
+typedef struct ptmi_model ptmi_model_t;
+int  ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **out);
+void ptmi_model_destroy(ptmi_model_t *m);
+int  ptmi_model_config(const ptmi_model_t *m, int cfg7[7]);
+/* pt_reset_kv (pitorch/pt.c:273-280): zero the KV cache, pos = 0. */
+int  ptmi_model_reset_kv(ptmi_model_t *m);
+/* pt_forward_step (pitorch/pt.c:267-271): forward `token` at the current
+ * position through one graph launch, pos += 1, *next = argmax(logits).  */
+int  ptmi_model_forward_step(ptmi_model_t *m, int token, int *next);
+/* Copy the last step's logits [vocab] to host memory. */
+int  ptmi_model_logits(ptmi_model_t *m, float *out);
+int  ptmi_model_pos(const ptmi_model_t *m);
+/* Greedy pt_generate over token ids (pitorch/text/pt_text.c:314-361 with
+ * temperature 0): zero the KV cache, force prompt[1..n_prompt-1] during
+ * prefill, then argmax.  All steps run back to back on the device; the
+ * host waits once.  out[i] = token chosen after position i;
+ * *n_out = positions run (stops after a sampled 1 or 2 when stop_on_eos). */
+int  ptmi_model_generate(ptmi_model_t *m, const int *prompt, int n_prompt,
+                         int max_tokens, int stop_on_eos, int *out, int *n_out);
+/* Enqueue `n_steps` greedy decode steps from the current position without
+ * waiting (benchmark form of the loop above; tokens stay on the device). */
+int  ptmi_model_decode_async(ptmi_model_t *m, int first_token, int n_steps);
+/* Kernel timing: run `n_steps` decode steps eagerly (no graph) with HIP
+ * events around every launch, from the current position.  role_ms[i] is
+ * the summed kernel time and role_launches[i] the launch count of role i:
+ * 0 QKV matvec, 1 attention, 2 Wo matvec, 3 w1|w3 matvec, 4 w2 matvec,
+ * 5 classifier matvec, 6 argmax.  Takes the place of the reference's
+ * per-matvec V3D counters (pitorch/profiler/profiler.h:6-28).           */
+int  ptmi_model_profile(ptmi_model_t *m, int first_token, int n_steps,
+                        float role_ms[7], int role_launches[7]);
+/* pt_train_step (pitorch/pt.c:339-364): zero grads, forward (loss),
+ * backward, SGD on the device copy of the weights.                     */
+int  ptmi_model_train_step(ptmi_model_t *m, const int *tokens, int T, float lr,
+                           float *loss);
+/* Copy the device weights back into a host blob of the same layout
+ * (file order, pitorch/model/llama2.c:49-70).                           */
+int  ptmi_model_read_weights(ptmi_model_t *m, void *blob, size_t bytes);
+/* Copy the gradient buffer (pt_grads_t order, pitorch/train/
+ * pt_train.c:342-370) of the last train step to host memory.           */
+int  ptmi_model_read_grads(ptmi_model_t *m, float *out, size_t n_floats);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,475 @@
+// Device-resident decode step (pt_forward_step, pitorch/pt.c:267-271 over
+// pt_forward, pitorch/model/llama2.c:127-206) captured once as a hipGraph.
+//
+// Per layer, five launches:
+//   1. QKV matvec   : RMSNorm prologue (+ embedding gather on layer 0),
+//                     RoPE epilogue, K/V written straight into the cache
+//   2. attention    : (head, 64-position chunk) workgroups, partial softmax;
+//                     the last chunk of each head to finish combines them
+//   3. Wo matvec    : residual-add epilogue
+//   4. w1|w3 matvec : RMSNorm prologue, rows interleaved, SwiGLU epilogue
+//   5. w2 matvec    : residual-add epilogue
+// then the classifier matvec (final RMSNorm prologue) and one argmax
+// workgroup that also advances the position and picks the next input token.
+#include "ptmi_model.h"
+
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+namespace ptmi {
+
+namespace {
+
+struct AttnParams {
+    const float *q;         // [D] post-RoPE query
+    const float *kc, *vc;   // this layer's caches [seq_len, kv_dim]
+    float *out;             // [D] attention output (xb)
+    float *part_o;          // [n_heads, n_chunks, head_dim]
+    float *part_ml;         // [n_heads, n_chunks, 2]  (max, sum)
+    unsigned *cnt;          // [n_heads] arrival counters, zero between launches
+    const DecodeCtl *ctl;
+    int head_dim, kv_dim, kv_mul, n_chunks;
+    float scale;
+};
+
+// llama2.c:153-177, split over position chunks (flash-decoding).  Scores
+// use the reference's exponential (pt_math.c:8-25) at every rescale.
+__global__ __launch_bounds__(256) void k_attn_decode(AttnParams a) {
+    __shared__ float qs[kMaxHeadDim];
+    __shared__ float es[kAttnChunk];
+    __shared__ float red[4][kMaxHeadDim];
+    __shared__ float ml[2];
+    __shared__ int last;
+
+    const int h = blockIdx.y, c = blockIdx.x, tid = threadIdx.x;
+    const int pos = a.ctl->pos;
+    const int n_active = pos / kAttnChunk + 1;
+    if (c >= n_active) return;                    // uniform per block
+    const int hd = a.head_dim;
+    const int t0 = c * kAttnChunk;
+    const long ko = (long)(h / a.kv_mul) * hd;
+
+    if (tid < hd) qs[tid] = a.q[h * hd + tid];
+    __syncthreads();
+
+    // scores: 4 lanes per position, strided dims
+    {
+        const int p = tid >> 2, part = tid & 3;
+        const int t = t0 + p;
+        float s = 0.0f;
+        if (t <= pos) {
+            const float *kt = a.kc + (long)t * a.kv_dim + ko;
+            for (int i = part; i < hd; i += 4) s = fmaf(qs[i], kt[i], s);
+        }
+        s = group_sum<4>(s);
+        if (part == 0) es[p] = s * a.scale;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const bool valid = t0 + tid <= pos;
+        const float s = valid ? es[tid] : -INFINITY;
+        const float m = group_max<64>(s);
+        const float e = valid ? d_expf(s - m) : 0.0f;
+        const float l = group_sum<64>(e);
+        es[tid] = e;
+        if (tid == 0) { ml[0] = m; ml[1] = l; }
+    }
+    __syncthreads();
+    // o[i] = sum_p e_p v_p[i]: 4 position groups x 64 dims
+    {
+        const int i = tid & 63, grp = tid >> 6;
+        if (i < hd) {
+            float o = 0.0f;
+            for (int p = grp; p < kAttnChunk && t0 + p <= pos; p += 4)
+                o = fmaf(es[p], a.vc[(long)(t0 + p) * a.kv_dim + ko + i], o);
+            red[grp][i] = o;
+        }
+        if (hd > 64) {   // second column block for head_dim in (64, 128]
+            const int i2 = i + 64;
+            if (i2 < hd) {
+                float o = 0.0f;
+                for (int p = grp; p < kAttnChunk && t0 + p <= pos; p += 4)
+                    o = fmaf(es[p], a.vc[(long)(t0 + p) * a.kv_dim + ko + i2], o);
+                red[grp][i2] = o;
+            }
+        }
+    }
+    __syncthreads();
+    const long slot = (long)h * a.n_chunks + c;
+    if (tid < hd) a.part_o[slot * hd + tid] = red[0][tid] + red[1][tid] + red[2][tid] + red[3][tid];
+    if (tid == 0) { a.part_ml[2 * slot] = ml[0]; a.part_ml[2 * slot + 1] = ml[1]; }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned prev = atomicAdd(&a.cnt[h], 1u);
+        last = (prev == (unsigned)(n_active - 1));
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    // combine the n_active partials of head h
+    if (tid < hd) {
+        const float *pm = a.part_ml + 2 * (long)h * a.n_chunks;
+        const float *po = a.part_o + (long)h * a.n_chunks * hd;
+        float M = -INFINITY;
+        for (int k = 0; k < n_active; k++) M = fmaxf(M, pm[2 * k]);
+        float num = 0.0f, den = 0.0f;
+        for (int k = 0; k < n_active; k++) {
+            const float f = d_expf(pm[2 * k] - M);
+            num = fmaf(po[(long)k * hd + tid], f, num);
+            den = fmaf(pm[2 * k + 1], f, den);
+        }
+        a.out[h * hd + tid] = num / den;
+    }
+    if (tid == 0) a.cnt[h] = 0u;
+}
+
+// argmax (pt_ops.c:65-70: first index of the maximum) + step bookkeeping
+// (pt.c:269 pos++, pt_text.c:344-350 prefill forcing).
+__global__ __launch_bounds__(1024) void k_argmax_step(const float *logits, int n, DecodeCtl *ctl,
+                                                      const int *prompt, int *out_tokens) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = tid; i < n; i += 1024) {
+        const float v = logits[i];
+        if (v > bv) { bv = v; bi = i; }      // ascending i: keeps the first max
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const float ov = __shfl_xor(bv, m);
+        const int oi = __shfl_xor(bi, m);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; w++)
+            if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
+        if (bi == 0x7fffffff) bi = 0;        // all NaN: the reference returns 0
+        const int pos = ctl->pos;
+        const int next = (pos < ctl->n_prompt - 1) ? prompt[pos + 1] : bi;
+        ctl->next = bi;
+        ctl->tok_in = next;
+        ctl->pos = pos + 1;
+        if (out_tokens) out_tokens[pos] = next;
+    }
+}
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// att_scale = 1/pt_sqrtf(head_dim) (llama2.c:137), evaluated on the host
+// with the reference's seed + 3 Newton steps (pt_math.c:92-102).
+float host_att_scale(int head_dim) {
+    const float x = (float)head_dim;
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    u = 0x1fbd1df5u + (u >> 1);
+    float y;
+    memcpy(&y, &u, 4);
+    for (int i = 0; i < 3; i++) y = 0.5f * (y + x / y);
+    return 1.0f / y;
+}
+
+// Optional per-launch HIP events (eager profiling runs only).
+struct StepTimer {
+    std::vector<hipEvent_t> ev;     // 2 per launch
+    std::vector<int> role;
+    size_t used = 0;
+    int begin(hipStream_t s, int r) {
+        if (used + 2 > ev.size()) {
+            hipEvent_t a, b;
+            PTMI_HIP(hipEventCreate(&a));
+            PTMI_HIP(hipEventCreate(&b));
+            ev.push_back(a);
+            ev.push_back(b);
+            role.push_back(0);
+        }
+        role[used / 2] = r;
+        PTMI_HIP(hipEventRecord(ev[used], s));
+        return PTMI_OK;
+    }
+    int end(hipStream_t s) {
+        PTMI_HIP(hipEventRecord(ev[used + 1], s));
+        used += 2;
+        return PTMI_OK;
+    }
+    ~StepTimer() {
+        for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+    }
+};
+
+#define TIMED(role_, launch_)                                   \
+    do {                                                        \
+        if (tm && (st = tm->begin(s, role_))) return st;        \
+        launch_;                                                \
+        if (tm && (st = tm->end(s))) return st;                 \
+    } while (0)
+
+// Enqueue one decode step on s (used both for capture and eager runs).
+int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
+    const Config &c = m->c;
+    const Resident *r = m->res;
+    const long D = c.dim, H = c.hidden, KV = c.kv_dim, S = c.seq_len;
+    int st = PTMI_OK;
+    for (int l = 0; l < c.n_layers; l++) {
+        float *kc = m->kc + (long)l * S * KV, *vc = m->vc + (long)l * S * KV;
+        MatvecParams p = {};
+        p.W = r->wqkv + (long)l * (D + 2 * KV) * D; p.ld = D; p.rows = (int)(D + 2 * KV); p.n = (int)D;
+        p.pro = l == 0 ? PRO_EMBED_RMSNORM : PRO_RMSNORM;
+        p.x = l == 0 ? r->emb : m->x;
+        p.token = &m->ctl->tok_in; p.x_out = m->x;
+        p.norm_w = r->rms_att + l * D;
+        p.y = m->q; p.epi = EPI_QKV_ROPE; p.pos = &m->ctl->pos;
+        p.q_rows = (int)D; p.kv_rows = (int)KV; p.head_dim = c.head_dim; p.k_cache = kc; p.v_cache = vc;
+        TIMED(0, if ((st = launch_matvec(p, s))) return st);
+
+        AttnParams a = {};
+        a.q = m->q; a.kc = kc; a.vc = vc; a.out = m->xb; a.part_o = m->part_o; a.part_ml = m->part_ml;
+        a.cnt = m->attn_cnt; a.ctl = m->ctl; a.head_dim = c.head_dim; a.kv_dim = (int)KV;
+        a.kv_mul = c.n_heads / c.n_kv_heads; a.n_chunks = m->n_chunks;
+        a.scale = host_att_scale(c.head_dim);
+        TIMED(1, hipLaunchKernelGGL(k_attn_decode, dim3(m->n_chunks, c.n_heads), dim3(256), 0, s, a));
+        PTMI_HIP(hipGetLastError());
+
+        p = MatvecParams{};
+        p.W = r->wo + (long)l * D * D; p.ld = D; p.rows = (int)D; p.n = (int)D;
+        p.x = m->xb; p.y = m->x; p.pro = PRO_NONE; p.epi = EPI_RESIDUAL;
+        TIMED(2, if ((st = launch_matvec(p, s))) return st);
+
+        p = MatvecParams{};
+        p.W = r->w13 + (long)l * 2 * H * D; p.ld = D; p.rows = (int)(2 * H); p.n = (int)D;
+        p.x = m->x; p.pro = PRO_RMSNORM; p.norm_w = r->rms_ffn + l * D;
+        p.y = m->hb; p.epi = EPI_SWIGLU;
+        TIMED(3, if ((st = launch_matvec(p, s))) return st);
+
+        p = MatvecParams{};
+        p.W = r->w2 + (long)l * D * H; p.ld = H; p.rows = (int)D; p.n = (int)H;
+        p.x = m->hb; p.y = m->x; p.pro = PRO_NONE; p.epi = EPI_RESIDUAL;
+        TIMED(4, if ((st = launch_matvec(p, s))) return st);
+    }
+    MatvecParams p = {};
+    p.W = r->wcls; p.ld = D; p.rows = c.vocab; p.n = (int)D;
+    p.x = m->x; p.pro = PRO_RMSNORM; p.norm_w = r->rms_final; p.y = m->logits; p.epi = EPI_STORE;
+    TIMED(5, if ((st = launch_matvec(p, s))) return st);
+    TIMED(6, hipLaunchKernelGGL(k_argmax_step, dim3(1), dim3(1024), 0, s, m->logits, c.vocab, m->ctl,
+                                m->prompt, m->out_tokens));
+    PTMI_HIP(hipGetLastError());
+    return PTMI_OK;
+}
+#undef TIMED
+
+int build_graph(ptmi_model *m) {
+    hipStream_t s = lib_stream();
+    PTMI_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int st = enqueue_step(m, s);
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &graph);
+    if (st) { if (graph) (void)hipGraphDestroy(graph); return st; }
+    if (e != hipSuccess) return hip_check(e, "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) { (void)hipGraphDestroy(graph); return hip_check(e, "hipGraphInstantiate"); }
+    m->graph = graph;
+    m->exec = exec;
+    return PTMI_OK;
+}
+
+int set_ctl(ptmi_model *m, int tok, int pos, int n_prompt) {
+    DecodeCtl h = {tok, pos, n_prompt, 0};
+    PTMI_HIP(hipMemcpyAsync(m->ctl, &h, sizeof(h), hipMemcpyHostToDevice, lib_stream()));
+    return PTMI_OK;
+}
+
+int zero_kv(ptmi_model *m) {
+    const size_t n = (size_t)m->c.n_layers * m->c.seq_len * m->c.kv_dim * sizeof(float);
+    PTMI_HIP(hipMemsetAsync(m->kc, 0, n, lib_stream()));
+    PTMI_HIP(hipMemsetAsync(m->vc, 0, n, lib_stream()));
+    return PTMI_OK;
+}
+
+}  // namespace
+
+}  // namespace ptmi
+
+using namespace ptmi;
+
+extern "C" {
+
+int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **out) {
+    if (!out) return set_error(PTMI_ERR_ARG, "ptmi_model_create: out is NULL");
+    *out = nullptr;
+    int st = PTMI_OK;
+    Resident *r = register_blob(blob, bytes, &st);
+    if (!r) return st;
+    const Config &c = r->c;
+    if (c.dim % 4 || c.hidden % 4 || c.head_dim % 2 || c.head_dim > kMaxHeadDim || c.kv_dim % 2)
+        return set_error(PTMI_ERR_ARG, "unsupported shape: dim=%d hidden=%d head_dim=%d", c.dim, c.hidden,
+                         c.head_dim);
+    if (max_T < 0 || max_T > c.seq_len) return set_error(PTMI_ERR_ARG, "max_T=%d outside [0, seq_len]", max_T);
+    ptmi_model *m = new ptmi_model();
+    m->res = r;
+    m->c = c;
+    m->max_T = max_T;
+    m->n_chunks = (c.seq_len + kAttnChunk - 1) / kAttnChunk;
+    const size_t D = c.dim, H = c.hidden, V = c.vocab, S = c.seq_len, KV = c.kv_dim, L = c.n_layers;
+    const size_t NH = c.n_heads, NC = m->n_chunks, hd = c.head_dim;
+    size_t sizes[] = {D, D, D, H, V, L * S * KV, L * S * KV, NH * NC * hd, NH * NC * 2};
+    float **dst[] = {&m->x, &m->xb, &m->q, &m->hb, &m->logits, &m->kc, &m->vc, &m->part_o, &m->part_ml};
+    size_t total = 0;
+    for (size_t s : sizes) total += align_up(s, 64);
+    const size_t ints = align_up(NH, 64) + align_up(sizeof(DecodeCtl) / 4, 64) + 2 * align_up(S, 64);
+    total += ints;
+    hipError_t e = hipMalloc(&m->mem, total * sizeof(float));
+    if (e != hipSuccess) { delete m; return hip_check(e, "hipMalloc(decode state)"); }
+    size_t o = 0;
+    for (int i = 0; i < 9; i++) { *dst[i] = m->mem + o; o += align_up(sizes[i], 64); }
+    m->attn_cnt = (unsigned *)(m->mem + o); o += align_up(NH, 64);
+    m->ctl = (DecodeCtl *)(m->mem + o); o += align_up(sizeof(DecodeCtl) / 4, 64);
+    m->prompt = (int *)(m->mem + o); o += align_up(S, 64);
+    m->out_tokens = (int *)(m->mem + o);
+    hipStream_t s = lib_stream();
+    e = hipMemsetAsync(m->mem, 0, total * sizeof(float), s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) { (void)hipFree(m->mem); delete m; return hip_check(e, "zero decode state"); }
+    if ((st = build_graph(m))) { (void)hipFree(m->mem); delete m; return st; }
+    if (max_T > 0 && (st = train_create(m))) {
+        (void)hipGraphExecDestroy(m->exec); (void)hipGraphDestroy(m->graph); (void)hipFree(m->mem);
+        delete m;
+        return st;
+    }
+    *out = m;
+    return PTMI_OK;
+}
+
+void ptmi_model_destroy(ptmi_model_t *m) {
+    if (!m) return;
+    (void)hipStreamSynchronize(lib_stream());
+    train_destroy(m);
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    (void)hipFree(m->mem);
+    delete m;
+}
+
+int ptmi_model_config(const ptmi_model_t *m, int cfg7[7]) {
+    if (!m || !cfg7) return set_error(PTMI_ERR_ARG, "ptmi_model_config: NULL");
+    const Config &c = m->c;
+    int v[7] = {c.dim, c.hidden, c.n_layers, c.n_heads, c.n_kv_heads, c.vocab, c.seq_len};
+    memcpy(cfg7, v, sizeof(v));
+    return PTMI_OK;
+}
+
+int ptmi_model_reset_kv(ptmi_model_t *m) {
+    if (!m) return set_error(PTMI_ERR_ARG, "NULL model");
+    int st;
+    if ((st = zero_kv(m)) || (st = set_ctl(m, 0, 0, 0))) return st;
+    PTMI_HIP(hipStreamSynchronize(lib_stream()));
+    m->host_pos = 0;
+    return PTMI_OK;
+}
+
+int ptmi_model_pos(const ptmi_model_t *m) { return m ? m->host_pos : -1; }
+
+int ptmi_model_forward_step(ptmi_model_t *m, int token, int *next) {
+    if (!m) return set_error(PTMI_ERR_ARG, "NULL model");
+    if (token < 0 || token >= m->c.vocab) return set_error(PTMI_ERR_ARG, "token %d outside [0, %d)", token, m->c.vocab);
+    if (m->host_pos >= m->c.seq_len)
+        return set_error(PTMI_ERR_STATE, "position %d: KV cache full (seq_len %d)", m->host_pos, m->c.seq_len);
+    hipStream_t s = lib_stream();
+    int st;
+    if ((st = set_ctl(m, token, m->host_pos, 0))) return st;
+    PTMI_HIP(hipGraphLaunch(m->exec, s));
+    DecodeCtl h;
+    PTMI_HIP(hipMemcpyAsync(&h, m->ctl, sizeof(h), hipMemcpyDeviceToHost, s));
+    PTMI_HIP(hipStreamSynchronize(s));
+    m->host_pos++;
+    if (next) *next = h.next;
+    return PTMI_OK;
+}
+
+int ptmi_model_logits(ptmi_model_t *m, float *out) {
+    if (!m || !out) return set_error(PTMI_ERR_ARG, "NULL argument");
+    hipStream_t s = lib_stream();
+    PTMI_HIP(hipMemcpyAsync(out, m->logits, (size_t)m->c.vocab * sizeof(float), hipMemcpyDeviceToHost, s));
+    PTMI_HIP(hipStreamSynchronize(s));
+    return PTMI_OK;
+}
+
+int ptmi_model_generate(ptmi_model_t *m, const int *prompt, int n_prompt, int max_tokens, int stop_on_eos,
+                        int *out, int *n_out) {
+    if (!m || !prompt || !out || !n_out || n_prompt < 1)
+        return set_error(PTMI_ERR_ARG, "ptmi_model_generate: bad arguments");
+    const Config &c = m->c;
+    if (max_tokens > c.seq_len) max_tokens = c.seq_len;          // pt_text.c:321-322
+    if (n_prompt > c.seq_len) return set_error(PTMI_ERR_ARG, "prompt longer than seq_len");
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= c.vocab) return set_error(PTMI_ERR_ARG, "prompt[%d]=%d out of range", i, prompt[i]);
+    *n_out = 0;
+    if (max_tokens <= 0) return PTMI_OK;
+    hipStream_t s = lib_stream();
+    int st;
+    if ((st = zero_kv(m))) return st;
+    PTMI_HIP(hipMemcpyAsync(m->prompt, prompt, (size_t)n_prompt * sizeof(int), hipMemcpyHostToDevice, s));
+    if ((st = set_ctl(m, prompt[0], 0, n_prompt))) return st;
+    for (int i = 0; i < max_tokens; i++) PTMI_HIP(hipGraphLaunch(m->exec, s));
+    PTMI_HIP(hipMemcpyAsync(out, m->out_tokens, (size_t)max_tokens * sizeof(int), hipMemcpyDeviceToHost, s));
+    PTMI_HIP(hipStreamSynchronize(s));
+    m->host_pos = max_tokens;
+    int n = max_tokens;
+    if (stop_on_eos)                                               // pt_text.c:354
+        for (int i = n_prompt - 1; i < max_tokens; i++)
+            if (out[i] == 1 || out[i] == 2) { n = i + 1; break; }
+    *n_out = n;
+    return PTMI_OK;
+}
+
+int ptmi_model_decode_async(ptmi_model_t *m, int first_token, int n_steps) {
+    if (!m) return set_error(PTMI_ERR_ARG, "NULL model");
+    if (first_token < 0 || first_token >= m->c.vocab) return set_error(PTMI_ERR_ARG, "token out of range");
+    if (n_steps < 0 || m->host_pos + n_steps > m->c.seq_len)
+        return set_error(PTMI_ERR_STATE, "pos %d + %d steps exceeds seq_len %d", m->host_pos, n_steps, m->c.seq_len);
+    hipStream_t s = lib_stream();
+    int st;
+    if ((st = set_ctl(m, first_token, m->host_pos, 0))) return st;
+    for (int i = 0; i < n_steps; i++) PTMI_HIP(hipGraphLaunch(m->exec, s));
+    m->host_pos += n_steps;
+    return PTMI_OK;
+}
+
+int ptmi_model_profile(ptmi_model_t *m, int first_token, int n_steps, float role_ms[7], int role_launches[7]) {
+    if (!m || !role_ms || !role_launches) return set_error(PTMI_ERR_ARG, "NULL argument");
+    if (first_token < 0 || first_token >= m->c.vocab) return set_error(PTMI_ERR_ARG, "token out of range");
+    if (n_steps < 0 || m->host_pos + n_steps > m->c.seq_len)
+        return set_error(PTMI_ERR_STATE, "pos %d + %d steps exceeds seq_len %d", m->host_pos, n_steps, m->c.seq_len);
+    for (int i = 0; i < 7; i++) { role_ms[i] = 0.0f; role_launches[i] = 0; }
+    hipStream_t s = lib_stream();
+    int st;
+    if ((st = set_ctl(m, first_token, m->host_pos, 0))) return st;
+    StepTimer tm;
+    for (int k = 0; k < n_steps; k++) {
+        tm.used = 0;
+        if ((st = enqueue_step(m, s, &tm))) return st;
+        PTMI_HIP(hipStreamSynchronize(s));
+        for (size_t i = 0; i < tm.used / 2; i++) {
+            float ms = 0.0f;
+            PTMI_HIP(hipEventElapsedTime(&ms, tm.ev[2 * i], tm.ev[2 * i + 1]));
+            role_ms[tm.role[i]] += ms;
+            role_launches[tm.role[i]]++;
+        }
+        m->host_pos++;
+    }
+    return PTMI_OK;
+}
+
+int ptmi_model_read_weights(ptmi_model_t *m, void *blob, size_t bytes) {
+    if (!m || !blob) return set_error(PTMI_ERR_ARG, "NULL argument");
+    if (bytes < m->res->bytes) return set_error(PTMI_ERR_ARG, "destination smaller than the blob");
+    if (blob != (void *)m->res->blob) memcpy(blob, m->res->blob, m->res->bytes);   // header, freq_cis
+    return download_resident(m->res, blob, lib_stream());
+}
+
+}  // extern "C"

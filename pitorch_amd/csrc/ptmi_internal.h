@@ -1,0 +1,207 @@
+// Internal declarations shared by the libptmi translation units.
+// All device code targets gfx950 (CDNA4, wave64).  Built with
+// -ffp-contract=off: every a*b+c below rounds twice unless written as an
+// explicit fmaf, which keeps the non-matvec ops bit-compatible with the
+// reference's host build.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/ptmi.h"
+
+namespace ptmi {
+
+// ── device math: the reference's libm-free polynomials ──────────────────
+// pitorch/ops/core/pt_math.c (same literals and evaluation order).
+__device__ __forceinline__ float bits_f(uint32_t u) { return __uint_as_float(u); }
+
+__device__ __forceinline__ float d_expf(float x) {       // pt_math.c:8-25
+    if (x > 88.7f) return 3.4028235e+38f;
+    if (x < -87.3f) return 0.0f;
+    const float ln2 = 0.6931471805599453f, inv_ln2 = 1.4426950408889634f;
+    float t = x * inv_ln2;
+    int n = (int)(t + (t >= 0 ? 0.5f : -0.5f));
+    float r = x - (float)n * ln2;
+    float poly = 0.0416666667f + r * 0.0083333333f;
+    poly = 0.1666666667f + r * poly;
+    poly = 0.5f + r * poly;
+    poly = 1.0f + r * poly;
+    poly = 1.0f + r * poly;
+    return poly * bits_f((uint32_t)(n + 127) << 23);
+}
+
+__device__ __forceinline__ float d_logf(float x) {       // pt_math.c:31-44
+    if (x <= 0.0f) return -3.4028235e+38f;
+    uint32_t u = __float_as_uint(x);
+    int e = (int)((u >> 23) & 0xFF) - 127;
+    float m = bits_f((u & 0x007FFFFFu) | 0x3F800000u);
+    if (m > 1.41421356f) { m *= 0.5f; e++; }
+    float f = m - 1.0f;
+    float s = -0.125f + f * 0.11111111f;
+    s = 0.14285714f + f * s;
+    s = -0.16666667f + f * s;
+    s = 0.2f + f * s;
+    s = -0.25f + f * s;
+    s = 0.33333333f + f * s;
+    s = -0.5f + f * s;
+    s = 1.0f + f * s;
+    return f * s + (float)e * 0.69314718f;
+}
+
+__device__ __forceinline__ float d_wrap_pi(float x) {    // pt_math.c:52-62
+    float k = x * 0.15915494309190f;
+    k = (float)(int)(k + (k >= 0 ? 0.5f : -0.5f));
+    return x - k * 6.28318530717959f;
+}
+
+__device__ __forceinline__ float d_sinf(float x) {       // pt_math.c:64-74
+    const float pi = 3.14159265358979f, half_pi = 1.57079632679490f;
+    x = d_wrap_pi(x);
+    if (x > half_pi) x = pi - x;
+    else if (x < -half_pi) x = -pi - x;
+    float z = x * x;
+    float s = -0.00019841270f + z * 0.00000275573f;
+    s = 0.00833333333f + z * s;
+    s = -0.16666666667f + z * s;
+    s = 1.0f + z * s;
+    return x * s;
+}
+
+__device__ __forceinline__ float d_cosf(float x) {       // pt_math.c:76-87
+    const float pi = 3.14159265358979f, half_pi = 1.57079632679490f;
+    x = d_wrap_pi(x);
+    float sign = 1.0f;
+    if (x > half_pi) { x = pi - x; sign = -1.0f; }
+    else if (x < -half_pi) { x = -pi - x; sign = -1.0f; }
+    float z = x * x;
+    float c = -0.00138888889f + z * 0.00002480159f;
+    c = 0.04166666667f + z * c;
+    c = -0.50000000000f + z * c;
+    c = 1.0f + z * c;
+    return sign * c;
+}
+
+__device__ __forceinline__ float d_sqrtf(float x) {      // pt_math.c:92-102
+    if (x <= 0.0f) return 0.0f;
+    float y = bits_f(0x1fbd1df5u + (__float_as_uint(x) >> 1));
+    y = 0.5f * (y + x / y);
+    y = 0.5f * (y + x / y);
+    y = 0.5f * (y + x / y);
+    return y;
+}
+
+// RoPE angle for element pair starting at i (pt_ops.c:33-40).
+__device__ __forceinline__ void d_rope_cs(int i, int head_dim, int pos, float *c, float *s) {
+    int hi = i % head_dim;
+    float freq = d_expf(-9.210340372f * (float)hi / (float)head_dim);
+    float ang = (float)pos * freq;
+    *c = d_cosf(ang);
+    *s = d_sinf(ang);
+}
+
+// ── cross-lane reductions (wave64) ──────────────────────────────────────
+// Butterfly all-reduce over aligned groups of G lanes.  Lane distance 1
+// and 2 use DPP quad permutes, 4..16 use ds_swizzle (bit-mask mode, no LDS
+// allocation), 32 uses ds_bpermute.
+__device__ __forceinline__ float dpp_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float dpp_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
+}
+template <int MASK>
+__device__ __forceinline__ float swz_xor(float v) {
+    static_assert(MASK == 4 || MASK == 8 || MASK == 16, "swizzle xor mask");
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (MASK << 10) | 0x1F));
+}
+__device__ __forceinline__ float xor32(float v) {
+    int lane = __lane_id();
+    return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __float_as_int(v)));
+}
+
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (G >= 2) v += dpp_xor1(v);
+    if constexpr (G >= 4) v += dpp_xor2(v);
+    if constexpr (G >= 8) v += swz_xor<4>(v);
+    if constexpr (G >= 16) v += swz_xor<8>(v);
+    if constexpr (G >= 32) v += swz_xor<16>(v);
+    if constexpr (G >= 64) v += xor32(v);
+    return v;
+}
+
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (G >= 2) v = fmaxf(v, dpp_xor1(v));
+    if constexpr (G >= 4) v = fmaxf(v, dpp_xor2(v));
+    if constexpr (G >= 8) v = fmaxf(v, swz_xor<4>(v));
+    if constexpr (G >= 16) v = fmaxf(v, swz_xor<8>(v));
+    if constexpr (G >= 32) v = fmaxf(v, swz_xor<16>(v));
+    if constexpr (G >= 64) v = fmaxf(v, xor32(v));
+    return v;
+}
+
+// ── matvec launch description ───────────────────────────────────────────
+enum Prologue { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_EMBED_RMSNORM = 2 };
+enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_QKV_ROPE = 2, EPI_SWIGLU = 3 };
+
+struct MatvecParams {
+    const float *W;        // row r starts at W + r*ld
+    long ld;               // row stride in floats
+    int rows, n;           // output rows, dot length
+    const float *x;        // input vector (PRO_EMBED_RMSNORM: embedding table)
+    float *y;              // output (EPI_RESIDUAL: residual updated in place)
+    int pro;
+    const float *norm_w;   // RMSNorm weight [n]
+    const int *token;      // PRO_EMBED_RMSNORM: row of x to use (device scalar)
+    float *x_out;          // PRO_EMBED_RMSNORM: raw embedding row written here
+    int epi;
+    const int *pos;        // EPI_QKV_ROPE: decode position (device scalar)
+    int q_rows, kv_rows, head_dim;
+    float *k_cache, *v_cache;   // this layer's [seq_len, kv_rows] caches
+    int rows_per_wave;     // filled by the launcher
+};
+
+// Launch y = epilogue(W . prologue(x)); validates shapes, picks a kernel.
+int launch_matvec(MatvecParams p, hipStream_t s);
+
+// ── library state ───────────────────────────────────────────────────────
+struct Config {
+    int dim, hidden, n_layers, n_heads, n_kv_heads, vocab, seq_len;
+    int head_dim, kv_dim, shared;
+};
+
+// Device copy of one registered blob in the device layout.
+struct Resident {
+    const char *blob;          // host blob (header included)
+    size_t bytes;
+    Config c;
+    float *mem;                // one allocation for all tensors
+    size_t mem_floats;
+    float *emb, *rms_att, *wqkv, *wo, *rms_ffn, *w13, *w2, *rms_final, *wcls;
+    // host tensor offsets in floats from blob+28 (file order)
+    size_t off_emb, off_rms_att, off_wq, off_wk, off_wv, off_wo, off_rms_ffn,
+           off_w1, off_w2, off_w3, off_rms_final, off_wcls, off_end;
+};
+
+int  set_error(int status, const char *fmt, ...);
+int  ensure_init();
+hipStream_t lib_stream();
+int  hip_check(hipError_t e, const char *what);
+Resident *find_resident(const void *p);
+Resident *register_blob(const void *blob, size_t bytes, int *status);
+int  upload_resident(Resident *r, hipStream_t s);   // host blob -> device layout
+int  download_resident(Resident *r, void *blob, hipStream_t s);
+int  parse_config(const void *blob, size_t bytes, Config *c);
+// Grow-only device scratch owned by the library (host-pointer entry points).
+float *scratch_buf(int slot, size_t floats);
+
+}  // namespace ptmi
+
+#define PTMI_HIP(call)                                              \
+    do {                                                            \
+        hipError_t e_ = (call);                                     \
+        if (e_ != hipSuccess) return ptmi::hip_check(e_, #call);    \
+    } while (0)

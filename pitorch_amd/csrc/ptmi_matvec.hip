@@ -1,0 +1,334 @@
+// fp32 matvec y = W[rows, n] . x[n] for gfx950, with the decode step's
+// prologues (RMSNorm, embedding gather) and epilogues (residual add,
+// RoPE + KV-cache write, SwiGLU) fused in.
+//
+// HBM-bound design (2 flop per 4-byte weight, ~0.5 flop/B):
+//  * LPR lanes own one row; each lane streams 16-byte (dwordx4) weight
+//    chunks sub, sub+LPR, ... so a wave's load instruction covers 64/LPR
+//    rows x LPR*16 contiguous bytes — fully used 64..1024-byte segments.
+//  * The lane's x chunks (at most 9 float4) stay in registers for the whole
+//    wave: x is read once per wave, never re-staged per row.
+//  * Two row passes are issued before either is reduced so each lane keeps
+//    2*IT independent 16-byte loads in flight.
+//  * Row sums are combined with DPP / ds_swizzle butterflies (no LDS tree);
+//    LDS holds only the <=64 finished row values a wave hands to its
+//    epilogue.
+// Reduction order differs from the reference's sequential j loop
+// (pitorch/ops/core/pt_ops.c:72-80): results agree to fp32 rounding.
+#include "ptmi_internal.h"
+
+#include <algorithm>
+
+namespace ptmi {
+
+namespace {
+
+constexpr int kWaves = 4;          // waves per workgroup
+constexpr int kMaxRowsPerWave = 64;
+
+__device__ __forceinline__ float dot4(float4 w, float4 x, float acc) {
+    acc = fmaf(w.x, x.x, acc);
+    acc = fmaf(w.y, x.y, acc);
+    acc = fmaf(w.z, x.z, acc);
+    acc = fmaf(w.w, x.w, acc);
+    return acc;
+}
+
+// Epilogue for rows [row0, row0 + nrows) whose sums sit in vals[0..nrows).
+// Runs on one wave; lane i handles row row0+i (pairs handled by even lanes).
+template <int EPI>
+__device__ __forceinline__ void run_epilogue(const MatvecParams &p, const float *vals,
+                                             int row0, int nrows, int lane) {
+    if (lane >= nrows) return;
+    const int r = row0 + lane;
+    const float v = vals[lane];
+    if constexpr (EPI == EPI_STORE) {
+        p.y[r] = v;
+    } else if constexpr (EPI == EPI_RESIDUAL) {   // vec_add(x, x, xb2): llama2.c:180,190
+        p.y[r] = p.y[r] + v;
+    } else if constexpr (EPI == EPI_SWIGLU) {     // rows interleaved w1[i], w3[i]
+        if (lane & 1) return;                     // llama2.c:187-188 (silu, vec_mul)
+        const float h1 = v, h3 = vals[lane + 1];
+        const float s = h1 / (1.0f + d_expf(-h1));
+        p.y[r >> 1] = s * h3;
+    } else {                                      // rope + KV write: llama2.c:147-151
+        static_assert(EPI == EPI_QKV_ROPE, "epilogue");
+        if (lane & 1) return;
+        const int pos = *p.pos;
+        const float a = v, b = vals[lane + 1];
+        if (r < p.q_rows) {
+            float c, s;
+            d_rope_cs(r, p.head_dim, pos, &c, &s);
+            p.y[r] = a * c - b * s;
+            p.y[r + 1] = a * s + b * c;
+        } else if (r < p.q_rows + p.kv_rows) {
+            const int i = r - p.q_rows;
+            float c, s;
+            d_rope_cs(i, p.head_dim, pos, &c, &s);
+            float *dst = p.k_cache + (long)pos * p.kv_rows + i;
+            dst[0] = a * c - b * s;
+            dst[1] = a * s + b * c;
+        } else {
+            const int i = r - p.q_rows - p.kv_rows;
+            float *dst = p.v_cache + (long)pos * p.kv_rows + i;
+            dst[0] = a;
+            dst[1] = b;
+        }
+    }
+}
+
+// Register-resident-x kernel: LPR lanes per row, IT float4 chunks per lane.
+// EXACT: n/4 == LPR*IT, so no chunk is out of range.  Otherwise chunk
+// addresses are clamped into the row and the loaded value replaced by 0,
+// which keeps every load unconditional (no per-load branches).
+template <int LPR, int IT, bool EXACT, int PRO, int EPI>
+__global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
+    constexpr int RPP = 64 / LPR;                  // rows per pass
+    __shared__ float ybuf[kWaves][kMaxRowsPerWave];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int slot = lane / LPR;
+    const int sub = lane % LPR;
+    const int n4 = p.n >> 2;
+    const long wave_id = (long)blockIdx.x * kWaves + wave;
+    const long row0l = wave_id * p.rows_per_wave;
+    const bool active = row0l < p.rows;
+    const int row0 = active ? (int)row0l : 0;
+    const int nrows = active ? min(p.rows_per_wave, p.rows - row0) : 0;
+
+    // ---- prologue: this lane's x chunks -> registers ----
+    const float *xs = p.x;
+    if constexpr (PRO == PRO_EMBED_RMSNORM) xs = p.x + (long)(*p.token) * p.n;
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 xr[IT];
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const int c = sub + it * LPR;
+        if constexpr (EXACT) {
+            xr[it] = reinterpret_cast<const float4 *>(xs)[c];
+        } else {
+            xr[it] = reinterpret_cast<const float4 *>(xs)[min(c, n4 - 1)];
+            if (c >= n4) xr[it] = zero4;
+        }
+    }
+    if (PRO == PRO_EMBED_RMSNORM && blockIdx.x == 0 && wave == 0 && slot == 0) {
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int c = sub + it * LPR;
+            if (c < n4) reinterpret_cast<float4 *>(p.x_out)[c] = xr[it];
+        }
+    }
+    if constexpr (PRO != PRO_NONE) {              // rmsnorm, pt_ops.c:5-12
+        float ss = 0.0f;
+#pragma unroll
+        for (int it = 0; it < IT; it++)
+            ss += xr[it].x * xr[it].x + xr[it].y * xr[it].y + xr[it].z * xr[it].z + xr[it].w * xr[it].w;
+        ss = group_sum<LPR>(ss);
+        const float inv = 1.0f / d_sqrtf(ss / (float)p.n + 1e-5f);
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int c = sub + it * LPR;
+            if (c < n4) {
+                const float4 w = reinterpret_cast<const float4 *>(p.norm_w)[c];
+                xr[it].x = xr[it].x * inv * w.x;
+                xr[it].y = xr[it].y * inv * w.y;
+                xr[it].z = xr[it].z * inv * w.z;
+                xr[it].w = xr[it].w * inv * w.w;
+            }
+        }
+    }
+
+    // ---- main loop: two passes (2*RPP rows) per iteration ----
+    // Rows past the end re-read the wave's last row; their sums are dropped.
+    for (int base = 0; base < nrows; base += 2 * RPP) {
+        const int ra = base + slot, rb = base + RPP + slot;
+        const bool va = ra < nrows, vb = rb < nrows;
+        const float4 *wa = reinterpret_cast<const float4 *>(p.W + (long)(row0 + min(ra, nrows - 1)) * p.ld);
+        const float4 *wb = reinterpret_cast<const float4 *>(p.W + (long)(row0 + min(rb, nrows - 1)) * p.ld);
+        float4 la[IT], lb[IT];
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int c = sub + it * LPR;
+            if constexpr (EXACT) {
+                la[it] = wa[c];
+                lb[it] = wb[c];
+            } else {
+                const int cc = min(c, n4 - 1);
+                la[it] = wa[cc];
+                lb[it] = wb[cc];
+                if (c >= n4) { la[it] = zero4; lb[it] = zero4; }
+            }
+        }
+        float acc_a = 0.0f, acc_b = 0.0f;
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            acc_a = dot4(la[it], xr[it], acc_a);
+            acc_b = dot4(lb[it], xr[it], acc_b);
+        }
+        acc_a = group_sum<LPR>(acc_a);
+        acc_b = group_sum<LPR>(acc_b);
+        if (sub == 0) {
+            if (va) ybuf[wave][ra] = acc_a;
+            if (vb) ybuf[wave][rb] = acc_b;
+        }
+    }
+    __syncthreads();
+    if (active) run_epilogue<EPI>(p, ybuf[wave], row0, nrows, lane);
+}
+
+// Long rows (n > 64*9*4): one wave per row pair, x read through the cache
+// in 64-chunk strides.  Used by the drop-in path for transposed weights
+// (e.g. W_cls^T, in_dim = vocab) — not by the decode step.
+__global__ __launch_bounds__(256) void k_matvec_long(MatvecParams p) {
+    __shared__ float ybuf[kWaves][kMaxRowsPerWave];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n4 = p.n >> 2;
+    const long wave_id = (long)blockIdx.x * kWaves + wave;
+    const long row0l = wave_id * p.rows_per_wave;
+    const bool active = row0l < p.rows;
+    const int row0 = active ? (int)row0l : 0;
+    const int nrows = active ? min(p.rows_per_wave, p.rows - row0) : 0;
+    const float4 *x4 = reinterpret_cast<const float4 *>(p.x);
+    for (int r = 0; r < nrows; r += 2) {
+        const bool vb = r + 1 < nrows;
+        const float4 *wa = reinterpret_cast<const float4 *>(p.W + (long)(row0 + r) * p.ld);
+        const float4 *wb = reinterpret_cast<const float4 *>(p.W + (long)(row0 + (vb ? r + 1 : r)) * p.ld);
+        float a = 0.0f, b = 0.0f;
+        for (int c = lane; c < n4; c += 64) {
+            const float4 xv = x4[c];
+            a = dot4(wa[c], xv, a);
+            b = dot4(wb[c], xv, b);
+        }
+        a = group_sum<64>(a);
+        b = group_sum<64>(b);
+        if (lane == 0) {
+            ybuf[wave][r] = a;
+            if (vb) ybuf[wave][r + 1] = b;
+        }
+    }
+    __syncthreads();
+    if (active) run_epilogue<EPI_STORE>(p, ybuf[wave], row0, nrows, lane);
+}
+
+// Any alignment / any n: one wave per row, scalar loads.
+__global__ __launch_bounds__(256) void k_matvec_scalar(MatvecParams p) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (row >= p.rows) return;
+    const float *w = p.W + row * p.ld;
+    float a = 0.0f;
+    for (int j = lane; j < p.n; j += 64) a = fmaf(w[j], p.x[j], a);
+    a = group_sum<64>(a);
+    if (lane == 0) p.y[row] = (p.epi == EPI_RESIDUAL) ? p.y[row] + a : a;
+}
+
+using KernelFn = void (*)(MatvecParams);
+
+template <int LPR, bool EXACT, int PRO, int EPI>
+KernelFn pick_it(int it) {
+    switch (it) {
+    case 1: return k_matvec<LPR, 1, EXACT, PRO, EPI>;
+    case 2: return k_matvec<LPR, 2, EXACT, PRO, EPI>;
+    case 3: return k_matvec<LPR, 3, EXACT, PRO, EPI>;
+    case 4: return k_matvec<LPR, 4, EXACT, PRO, EPI>;
+    case 5: return k_matvec<LPR, 5, EXACT, PRO, EPI>;
+    case 6: return k_matvec<LPR, 6, EXACT, PRO, EPI>;
+    case 7: return k_matvec<LPR, 7, EXACT, PRO, EPI>;
+    case 8: return k_matvec<LPR, 8, EXACT, PRO, EPI>;
+    case 9: return k_matvec<LPR, 9, EXACT, PRO, EPI>;
+    default: return nullptr;
+    }
+}
+
+// Only the (prologue, epilogue) pairs the library launches are built:
+// plain y=Wx, QKV (+embed on layer 0), residual (Wo, w2), SwiGLU (w1|w3),
+// classifier (RMSNorm prologue, plain store).
+template <int LPR, bool EXACT>
+KernelFn pick_role(int it, int pro, int epi) {
+    if (pro == PRO_NONE && epi == EPI_STORE) return pick_it<LPR, EXACT, PRO_NONE, EPI_STORE>(it);
+    if (pro == PRO_NONE && epi == EPI_RESIDUAL) return pick_it<LPR, EXACT, PRO_NONE, EPI_RESIDUAL>(it);
+    if (pro == PRO_RMSNORM && epi == EPI_STORE) return pick_it<LPR, EXACT, PRO_RMSNORM, EPI_STORE>(it);
+    if (pro == PRO_RMSNORM && epi == EPI_SWIGLU) return pick_it<LPR, EXACT, PRO_RMSNORM, EPI_SWIGLU>(it);
+    if (pro == PRO_RMSNORM && epi == EPI_QKV_ROPE) return pick_it<LPR, EXACT, PRO_RMSNORM, EPI_QKV_ROPE>(it);
+    if (pro == PRO_EMBED_RMSNORM && epi == EPI_QKV_ROPE)
+        return pick_it<LPR, EXACT, PRO_EMBED_RMSNORM, EPI_QKV_ROPE>(it);
+    return nullptr;
+}
+
+template <int LPR>
+KernelFn pick(int it, bool exact, int pro, int epi) {
+    return exact ? pick_role<LPR, true>(it, pro, epi) : pick_role<LPR, false>(it, pro, epi);
+}
+
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+// Host-side launcher.  Chooses lanes-per-row so that each lane holds at
+// most 9 float4 of x, and rows-per-wave so that the grid has ~2048 waves
+// (8 per CU) when the matrix is large enough.
+int launch_matvec(MatvecParams p, hipStream_t s) {
+    if (p.rows <= 0 || p.n <= 0) return set_error(PTMI_ERR_ARG, "matvec: rows=%d n=%d", p.rows, p.n);
+    if (!p.W || !p.x || !p.y) return set_error(PTMI_ERR_ARG, "matvec: null pointer");
+    if (p.ld < p.n) return set_error(PTMI_ERR_ARG, "matvec: ld=%ld < n=%d", p.ld, p.n);
+    const int n4 = p.n / 4;
+    const bool vec_ok = (p.n % 4 == 0) && (p.ld % 4 == 0) && aligned16(p.W) && aligned16(p.x) &&
+                        (p.pro == PRO_NONE || aligned16(p.norm_w)) &&
+                        (p.pro != PRO_EMBED_RMSNORM || aligned16(p.x_out));
+    const bool fused = p.pro != PRO_NONE || p.epi == EPI_QKV_ROPE || p.epi == EPI_SWIGLU;
+    if (p.epi == EPI_QKV_ROPE &&
+        ((p.q_rows & 1) || (p.kv_rows & 1) || p.head_dim <= 0 || !p.pos || !p.k_cache || !p.v_cache))
+        return set_error(PTMI_ERR_ARG, "matvec: bad QKV epilogue description");
+    if (p.epi == EPI_SWIGLU && (p.rows & 1))
+        return set_error(PTMI_ERR_ARG, "matvec: SwiGLU needs an even row count");
+
+    KernelFn fn = nullptr;
+    int rpp = 1;
+    if (vec_ok && n4 <= 64 * 9) {
+        int lpr, it;
+        if (n4 <= 8 * 9) lpr = 8;
+        else if (n4 <= 16 * 9) lpr = 16;
+        else if (n4 <= 32 * 9) lpr = 32;
+        else lpr = 64;
+        it = (n4 + lpr - 1) / lpr;
+        const bool exact = n4 == lpr * it;
+        switch (lpr) {
+        case 8: fn = pick<8>(it, exact, p.pro, p.epi); break;
+        case 16: fn = pick<16>(it, exact, p.pro, p.epi); break;
+        case 32: fn = pick<32>(it, exact, p.pro, p.epi); break;
+        default: fn = pick<64>(it, exact, p.pro, p.epi); break;
+        }
+        if (!fn) return set_error(PTMI_ERR_ARG, "matvec: unsupported prologue/epilogue pair %d/%d", p.pro, p.epi);
+        rpp = 64 / lpr;
+    } else if (vec_ok) {
+        if (p.pro != PRO_NONE || p.epi != EPI_STORE)
+            return set_error(PTMI_ERR_ARG, "matvec: fused variants need n <= %d", 64 * 9 * 4);
+        fn = k_matvec_long;
+        rpp = 1;
+    } else {
+        if (fused) return set_error(PTMI_ERR_ARG, "matvec: fused variants need 16-byte aligned rows, n%%4==0");
+        p.rows_per_wave = 1;
+        const int blocks = (p.rows + kWaves - 1) / kWaves;
+        hipLaunchKernelGGL(k_matvec_scalar, dim3(blocks), dim3(kWaves * 64), 0, s, p);
+        PTMI_HIP(hipGetLastError());
+        return PTMI_OK;
+    }
+    // rows per wave: a multiple of 2*rpp (row pairs for the fused epilogues),
+    // at most 64, chosen for ~2048 waves in flight.
+    const int step = 2 * rpp;
+    const long target_waves = 2048;
+    long rpw = (p.rows + target_waves - 1) / target_waves;
+    rpw = ((rpw + step - 1) / step) * step;
+    rpw = std::max<long>(rpw, step);
+    rpw = std::min<long>(rpw, kMaxRowsPerWave);
+    p.rows_per_wave = (int)rpw;
+    const long waves = (p.rows + rpw - 1) / rpw;
+    const long blocks = (waves + kWaves - 1) / kWaves;
+    hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kWaves * 64), 0, s, p);
+    PTMI_HIP(hipGetLastError());
+    return PTMI_OK;
+}
+
+}  // namespace ptmi

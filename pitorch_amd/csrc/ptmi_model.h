@@ -1,0 +1,47 @@
+// Device-resident model state shared by the decode and training units.
+#pragma once
+
+#include "ptmi_internal.h"
+
+namespace ptmi {
+
+// Per-step control block in device memory.  Kernels of a captured decode
+// step read the position and input token from here, so one graph serves
+// every position.
+struct DecodeCtl {
+    int tok_in;      // token fed at `pos`
+    int pos;         // current position
+    int n_prompt;    // generate: positions < n_prompt-1 force prompt[pos+1]
+    int next;        // argmax of the last step's logits
+};
+
+struct TrainState;   // defined by the training unit
+
+constexpr int kAttnChunk = 64;      // positions per attention workgroup
+constexpr int kMaxHeadDim = 128;
+
+}  // namespace ptmi
+
+struct ptmi_model {
+    ptmi::Resident *res = nullptr;
+    ptmi::Config c{};
+    int max_T = 0;
+    int host_pos = 0;
+    // decode buffers (device)
+    float *mem = nullptr;
+    float *x = nullptr, *xb = nullptr, *q = nullptr, *hb = nullptr, *logits = nullptr;
+    float *kc = nullptr, *vc = nullptr;
+    float *part_o = nullptr, *part_ml = nullptr;
+    unsigned *attn_cnt = nullptr;
+    ptmi::DecodeCtl *ctl = nullptr;
+    int *prompt = nullptr, *out_tokens = nullptr;
+    int n_chunks = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    ptmi::TrainState *train = nullptr;
+};
+
+namespace ptmi {
+int  train_create(ptmi_model *m);
+void train_destroy(ptmi_model *m);
+}

@@ -1,0 +1,100 @@
+/*
+ * pt.h — host API of the MI355X build, in C, with pitorch's call
+ * signatures (pitorch/pt.h:23-104) so callers of pt_forward_step /
+ * pt_train_step / the generate loop switch by changing the init call.
+ *
+ * The context owns a device-resident model in libptmi (include/ptmi.h):
+ * decode steps are one hipGraph launch each, training steps run forward,
+ * backward and SGD on the device.  ctx->matvec is ptmi_matvec, the
+ * pt_matvec_fn drop-in, for callers that drive the layer code themselves
+ * (pitorch/model/llama2.c pt_forward with the matvec pointer).
+ *
+ * Failures panic (message + abort), as the reference does with
+ * demand()/panic(); the pt_try_* forms return a ptmi status instead.
+ */
+#ifndef PTAMD_PT_H
+#define PTAMD_PT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ptmi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* pitorch/model/llama2.h:10-18 */
+typedef struct {
+    int dim;
+    int hidden_dim;
+    int n_layers;
+    int n_heads;
+    int n_kv_heads;
+    int vocab_size;
+    int seq_len;
+} pt_config_t;
+
+/* pitorch/model/llama2.h:73-75 */
+typedef void (*pt_matvec_fn)(const float *W, const float *x, float *y,
+                             int out_dim, int in_dim);
+
+/* pitorch/pt.h:23-44, with the device model in place of host buffers. */
+typedef struct {
+    pt_config_t   cfg;
+    int           shared_weights;
+    pt_matvec_fn  matvec;        /* = ptmi_matvec */
+    int           pos;           /* current decode position */
+    int           max_T;         /* > 0: training buffers allocated */
+    void         *weight_data;   /* caller's .bin blob (header + weights) */
+    size_t        weight_bytes;
+    ptmi_model_t *dev;
+    float        *logits;        /* host copy, filled on demand */
+} pt_context_t;
+
+/* ── model file (pitorch/model/llama2.c:9-47) ── */
+void     pt_load_config(pt_config_t *cfg, const void *data);
+uint64_t pt_file_size(const void *data);
+
+/* ── init / teardown: replaces pt_host_init / pt_pi_init (pt.c:38-114,
+ * 232-248).  weight_data stays owned by the caller and must outlive ctx. */
+int  pt_try_gpu_init(pt_context_t *ctx, void *weight_data, size_t bytes, int max_T);
+void pt_gpu_init(pt_context_t *ctx, void *weight_data, size_t bytes, int max_T);
+void pt_free(pt_context_t *ctx);
+
+/* ── inference (pt.c:267-280) ── */
+int  pt_forward_step(pt_context_t *ctx, int token);
+int  pt_try_forward_step(pt_context_t *ctx, int token, int *next);
+void pt_reset_kv(pt_context_t *ctx);
+const float *pt_logits(pt_context_t *ctx);
+void pt_print_config(const pt_context_t *ctx);
+
+/* Greedy generation over token ids: the pt_generate loop
+ * (pitorch/text/pt_text.c:314-361) at temperature 0, tokenizer excluded.
+ * Writes the token chosen after each position to out; returns the number
+ * of positions run (stops after a sampled BOS/EOS, pt_text.c:354).     */
+int  pt_generate_ids(pt_context_t *ctx, const int *prompt, int n_prompt,
+                     int max_tokens, int *out);
+
+/* ── training (pt.c:339-364) ── */
+float pt_train_step(pt_context_t *ctx, const int *tokens, int T, float lr);
+int   pt_try_train_step(pt_context_t *ctx, const int *tokens, int T, float lr, float *loss);
+/* Copy the trained device weights back into ctx->weight_data. */
+int   pt_sync_weights(pt_context_t *ctx);
+
+/* ── synthetic inputs (the benchmark configurations' model and ids) ──
+ * A llama2.c .bin with weights ~ N(0, std) from splitmix64 + Box-Muller,
+ * RMSNorm weights 1, freq_cis blocks 0, tied classifier (positive
+ * vocab_size).  Deterministic for a given seed on every host.          */
+uint64_t pt_synth_model_bytes(const pt_config_t *cfg);
+int      pt_synth_model(const pt_config_t *cfg, uint64_t seed, float std,
+                        void *out, uint64_t bytes);
+/* n ids uniform in [0, vocab) from seed. */
+void     pt_seed_tokens(uint64_t seed, int n, int vocab, int *out);
+/* n floats uniform in [lo, hi) from seed (matvec sweep inputs). */
+void     pt_seed_uniform(uint64_t seed, uint64_t n, float lo, float hi, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,140 @@
+"""GPU parity of the device-resident decode step (pt_forward_step drop-in).
+
+Golden tokens come from the reference's own host build (tests/golden/
+make_golden.py).  Greedy tokens must be IDENTICAL over the full runs
+(256 positions for 15M, 1024 for 42M/110M); logits are compared with the
+oracle at a relative tolerance (matvec reduction order differs).
+"""
+import ctypes
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+import pitorch_amd as pa
+from tests._oracle import OracleModel, P, greedy_tokens, ref, ref_available
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def fixture(name):
+    return json.load(open(os.path.join(ROOT, "tests", "golden", f"decode_{name}.json")))
+
+
+def model_for(name):
+    blob = pa.synth_model(pa.STORIES[name], pa.SEED_MODEL[name])
+    assert hashlib.sha256(blob.tobytes()).hexdigest() == fixture(name)["blob_sha256"], \
+        "synthetic model generator drifted on this host"
+    return blob
+
+
+def test_logits_track_oracle_15M():
+    blob = model_for("stories15M")
+    m = pa.Model(blob)
+    om = OracleModel(blob.copy())
+    prompt = fixture("stories15M")["prompt"]
+    tok = prompt[0]
+    worst = 0.0
+    for pos in range(40):
+        a = m.forward_step(tok)
+        b = om.forward_step(tok)
+        lg, ref_lg = m.logits(), om.logits()
+        err = np.max(np.abs(lg - ref_lg)) / np.max(np.abs(ref_lg))
+        worst = max(worst, err)
+        assert err < 1e-5, (pos, err)
+        assert a == b == int(np.argmax(ref_lg))
+        tok = prompt[pos + 1] if pos + 1 < len(prompt) else a
+    assert m.pos() == 40
+    m.close()
+    om.close()
+
+
+@pytest.mark.parametrize("name", ["stories15M", "stories42M", "stories110M"])
+def test_greedy_tokens_identical_to_reference(name):
+    fx = fixture(name)
+    blob = model_for(name)
+    m = pa.Model(blob)
+    toks = m.generate(np.array(fx["prompt"], np.int32), pa.DECODE_POSITIONS[name], stop_on_eos=False)
+    assert len(toks) == len(fx["tokens"])
+    first_diff = next((i for i, (a, b) in enumerate(zip(toks, fx["tokens"])) if a != b), None)
+    assert first_diff is None, f"first divergence at position {first_diff}"
+    m.close()
+
+
+def test_forward_step_matches_generate_and_reset():
+    fx = fixture("stories15M")
+    blob = model_for("stories15M")
+    m = pa.Model(blob)
+    toks = greedy_tokens(m.forward_step, fx["prompt"], 64)
+    assert toks == fx["tokens"][:64]
+    m.reset_kv()
+    assert m.pos() == 0
+    assert greedy_tokens(m.forward_step, fx["prompt"], 16) == fx["tokens"][:16]
+    m.close()
+
+
+def test_generate_stop_and_clamp_semantics():
+    """pt_text.c:321-322 clamp, :344-347 forced prefill, :354 stop on 1/2."""
+    cfg = (64, 160, 2, 4, 4, 512, 24)
+    blob = pa.synth_model(cfg, 5, 0.3)
+    om = OracleModel(blob.copy())
+    prompt = np.array([3, 9, 27, 81], np.int32)
+    out = np.zeros(64, np.int32)
+    n = om.L.po_generate_greedy(om.h, prompt.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), 4, 100,
+                                out.ctypes.data_as(ctypes.POINTER(ctypes.c_int)))
+    m = pa.Model(blob)
+    got = m.generate(prompt, 100, stop_on_eos=True)
+    assert list(got) == list(out[:n])
+    m.close()
+    om.close()
+
+
+def test_errors_are_reported():
+    cfg = (64, 160, 1, 4, 4, 512, 8)
+    blob = pa.synth_model(cfg, 6)
+    m = pa.Model(blob)
+    with pytest.raises(pa.PtmiError):
+        m.forward_step(512)                       # token out of range
+    for _ in range(8):
+        m.forward_step(1)
+    with pytest.raises(pa.PtmiError) as e:
+        m.forward_step(1)                         # KV cache full
+    assert "seq_len" in str(e.value)
+    with pytest.raises(pa.PtmiError):
+        m.decode_async(1, 1)
+    m.close()
+
+
+@pytest.mark.skipif(not ref_available(), reason="oracle/_ref not built")
+def test_reference_forward_with_ptmi_matvec_dropin():
+    """The reference's own pt_forward_step (pitorch/pt.c:267-271) with
+    ctx->matvec = ptmi_matvec: the drop-in binding of INTEGRATION.md."""
+    fx = fixture("stories15M")
+    blob = model_for("stories15M")
+    L = pa.load_ptmi()
+    assert L.ptmi_register_weights(P(blob), blob.nbytes) == 0
+    R = ref()
+    ctx = R.ref_ctx_new(P(blob), 0)
+    fn = ctypes.cast(L.ptmi_matvec, ctypes.c_void_p)
+    R.ref_set_matvec(ctx, fn)
+    try:
+        toks = greedy_tokens(lambda t: R.ref_forward_step(ctx, t), fx["prompt"], 48)
+        assert toks == fx["tokens"][:48]
+    finally:
+        R.ref_ctx_free(ctx)
+        L.ptmi_unregister_weights(P(blob))
+
+
+def test_profile_roles_cover_every_launch():
+    cfg = pa.STORIES["stories15M"]
+    blob = model_for("stories15M")
+    m = pa.Model(blob)
+    prof = m.profile(1, 4)
+    Lyr = cfg[2]
+    assert prof["qkv"][1] == prof["attention"][1] == prof["wo"][1] == prof["w13"][1] == prof["w2"][1] == 4 * Lyr
+    assert prof["classifier"][1] == prof["argmax"][1] == 4
+    assert all(ms > 0 for ms, _ in prof.values())
+    m.close()

@@ -1,0 +1,135 @@
+"""GPU parity of the fp32 matvec (pt_matvec_fn drop-in) against the oracle.
+
+Tolerances (north_star: per-output relative error <= 1e-5, fp32 with a
+different reduction order):
+  * integer-valued inputs (dev/tests/matvec/test_matvec.c:25-35 idea): every
+    partial sum is exact in fp32, so GPU == oracle BIT FOR BIT;
+  * U(-1,1) inputs: |y_gpu - y_oracle| <= 1e-5 * max(|y_oracle|, rms(y_oracle))
+    per output (the rms floor keeps outputs that cancel to ~0 meaningful),
+    and within the fp64 forward-error bound gamma_n * sum|W||x|.
+"""
+import numpy as np
+import pytest
+
+import pitorch_amd as pa
+from tests._oracle import P, oracle
+from tests.test_oracle import lcg_ints
+
+pytestmark = pytest.mark.gpu
+
+SWEEP = [(288, 288), (768, 288), (288, 768), (32000, 288), (2048, 768), (768, 2048), (32000, 768),
+         (2304, 768), (4096, 768)]
+EXTRA = [(48, 48), (512, 512), (1376, 512), (512, 1376), (1, 4), (3, 8), (37, 44), (16, 2304)]
+
+
+def oracle_mv(W, x):
+    y = np.zeros(W.shape[0], np.float32)
+    oracle().po_smatvec(P(W), P(x), P(y), W.shape[0], W.shape[1])
+    return y
+
+
+def check_close(y, ref, W, x):
+    scale = np.maximum(np.abs(ref), np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    rel = np.abs(y - ref) / scale
+    assert rel.max() <= 1e-5, rel.max()
+    exact = W.astype(np.float64) @ x.astype(np.float64)
+    n = W.shape[1]
+    gamma = n * 2.0 ** -24 / (1 - n * 2.0 ** -24)
+    assert (np.abs(y - exact) <= gamma * (np.abs(W) @ np.abs(x)) + 1e-30).all()
+
+
+@pytest.mark.parametrize("d,n", SWEEP + EXTRA)
+def test_integer_inputs_bit_exact(d, n):
+    W = lcg_ints(d * n, 42).reshape(d, n) if d * n <= 2_000_000 else \
+        np.random.default_rng(d).integers(1, 9, (d, n)).astype(np.float32)
+    x = lcg_ints(n, 137)
+    y = pa.matvec(W, x)
+    assert np.array_equal(y, oracle_mv(W, x))
+
+
+@pytest.mark.parametrize("d,n", SWEEP + EXTRA)
+def test_random_inputs_within_tolerance(d, n):
+    W = pa.seed_uniform(1000 + d, d * n).reshape(d, n)
+    x = pa.seed_uniform(2000 + n, n)
+    y = pa.matvec(W, x)
+    check_close(y, oracle_mv(W, x), W, x)
+
+
+def test_long_rows_and_unaligned_views():
+    rng = np.random.default_rng(3)
+    W = rng.uniform(-1, 1, (288, 32000)).astype(np.float32)      # W_cls^T shape (dX path)
+    x = rng.uniform(-1, 1, 32000).astype(np.float32)
+    check_close(pa.matvec(W, x), oracle_mv(W, x), W, x)
+    big = rng.uniform(-1, 1, 1 + 40 * 45).astype(np.float32)
+    Wv = big[1:].reshape(40, 45)                                   # 4-byte aligned only, n%4 != 0
+    x = rng.uniform(-1, 1, 45).astype(np.float32)
+    check_close(pa.matvec(Wv, x), oracle_mv(np.ascontiguousarray(Wv), x), Wv, x)
+
+
+def test_bad_arguments_are_errors():
+    L = pa.load_ptmi()
+    W = np.ones((4, 4), np.float32)
+    y = np.zeros(4, np.float32)
+    assert L.ptmi_matvec_checked(P(W), P(W[0]), P(y), 0, 4) == 1
+    assert L.ptmi_matvec_checked(None, P(W[0]), P(y), 4, 4) == 1
+    assert b"bad arguments" in L.ptmi_last_error()
+
+
+def test_registered_weights_resolve_to_device_layout():
+    """Host pointers into a registered blob hit the device copy, including the
+    fused [wq;wk;wv] and row-interleaved [w1|w3] layouts."""
+    cfg = pa.STORIES["stories15M"]
+    D, H, Lyr, V = cfg[0], cfg[1], cfg[2], cfg[5]
+    blob = pa.synth_model(cfg, 77)
+    L = pa.load_ptmi()
+    assert L.ptmi_register_weights(P(blob), blob.nbytes) == 0
+    try:
+        w = np.frombuffer(blob, np.float32, offset=28)
+        o = {}
+        off = 0
+        for name, n in (("emb", V * D), ("rms_att", Lyr * D), ("wq", Lyr * D * D), ("wk", Lyr * D * D),
+                        ("wv", Lyr * D * D), ("wo", Lyr * D * D), ("rms_ffn", Lyr * D), ("w1", Lyr * H * D),
+                        ("w2", Lyr * D * H), ("w3", Lyr * H * D)):
+            o[name] = off
+            off += n
+        rng = np.random.default_rng(9)
+        views = [("wq", 2, D, D, 0), ("wk", 5, D, D, 0), ("wv", 0, D, D, 16), ("wo", 3, D, D, 0),
+                 ("w1", 1, H, D, 0), ("w3", 4, H, D, 100), ("w2", 2, D, H, 0), ("emb", 0, V, D, 0)]
+        for name, layer, rows, cols, r0 in views:
+            start = o[name] + layer * rows * cols + r0 * cols
+            nrow = rows - r0 if name != "w3" else 64
+            W = w[start: start + nrow * cols].reshape(nrow, cols)
+            x = rng.uniform(-1, 1, cols).astype(np.float32)
+            y = np.zeros(nrow, np.float32)
+            assert L.ptmi_matvec_checked(P(W), P(x), P(y), nrow, cols) == 0
+            check_close(y, oracle_mv(np.ascontiguousarray(W), x), W, x)
+        # invalidation: host writes become visible only after ptmi_invalidate
+        start = o["wq"]
+        W = w[start: start + D * D].reshape(D, D)
+        x = rng.uniform(-1, 1, D).astype(np.float32)
+        before = oracle_mv(np.ascontiguousarray(W), x)
+        W *= 2.0
+        y = np.zeros(D, np.float32)
+        assert L.ptmi_matvec_checked(P(W), P(x), P(y), D, D) == 0
+        check_close(y, before, W / 2, x)                 # stale device copy until invalidated
+        assert L.ptmi_invalidate(P(W), W.nbytes) == 0
+        assert L.ptmi_matvec_checked(P(W), P(x), P(y), D, D) == 0
+        check_close(y, oracle_mv(np.ascontiguousarray(W), x), W, x)
+    finally:
+        L.ptmi_unregister_weights(P(blob))
+
+
+def test_device_pointer_entry_on_caller_stream():
+    torch = pytest.importorskip("torch")
+    L = pa.load_ptmi()
+    d, n = 4096, 768
+    W = pa.seed_uniform(5, d * (n + 4)).reshape(d, n + 4)         # ld = n + 4
+    x = pa.seed_uniform(6, n)
+    dW = torch.from_numpy(W).cuda()
+    dx = torch.from_numpy(x).cuda()
+    dy = torch.empty(d, device="cuda")
+    s = torch.cuda.current_stream()
+    assert L.ptmi_matvec_dev(dW.data_ptr(), n + 4, dx.data_ptr(), dy.data_ptr(), d, n, s.cuda_stream) == 0
+    s.synchronize()
+    Wc = np.ascontiguousarray(W[:, :n])
+    check_close(dy.cpu().numpy(), oracle_mv(Wc, x), Wc, x)

@@ -1,0 +1,442 @@
+"""Pins for the CPU oracle (oracle/ptoracle.c) — CPU only.
+
+Three independent anchors:
+  1. the reference's own known-answer tests (dev/tests/ops/test_ops.c) —
+     tests/golden/ops_kats.json;
+  2. the reference's own host build (oracle/_ref, compiled from its sources):
+     the restatement must agree BIT FOR BIT;
+  3. mathematics: libm in fp64, closed forms (W^T dy, outer products,
+     orthogonality of RoPE), integer-exact sums, finite differences.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from tests._oracle import P, OracleModel, arr, fp, ip, oracle, ref, ref_available
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KATS = json.load(open(os.path.join(HERE, "golden", "ops_kats.json")))
+f32 = np.float32
+
+
+def approx_eq(got, want, atol, rtol):
+    """test_ops.c:21-28 semantics."""
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    diff = np.abs(got - want)
+    scale = np.abs(want)
+    return np.where(scale < 1e-6, diff < atol, (diff < atol) | (diff / np.maximum(scale, 1e-30) < rtol))
+
+
+# ── 1. reference KATs ─────────────────────────────────────────────────────
+
+@pytest.mark.parametrize("fn", ["expf", "sinf", "cosf"])
+def test_kat_math(fn):
+    k = KATS[fn]
+    f = getattr(oracle(), "po_" + fn)
+    got = [f(x) for x in k["in"]]
+    assert approx_eq(got, k["ref"], k["atol"], k["rtol"]).all(), (fn, got)
+
+
+def test_kat_ops():
+    L = oracle()
+    k = KATS["rmsnorm"]
+    x, w, o = np.array(k["x"], f32), np.array(k["w"], f32), np.zeros(6, f32)
+    L.po_rmsnorm(P(o), P(x), P(w), 6)
+    assert approx_eq(o, k["ref"], k["atol"], k["rtol"]).all()
+    k = KATS["softmax"]
+    x = np.array(k["x"], f32)
+    L.po_softmax(P(x), 6)
+    assert approx_eq(x, k["ref"], k["atol"], k["rtol"]).all()
+    k = KATS["silu"]
+    x = np.array(k["x"], f32)
+    L.po_silu(P(x), 6)
+    assert approx_eq(x, k["ref"], k["atol"], k["rtol"]).all()
+    k = KATS["rope"]
+    q, kk = np.array(k["q"], f32), np.array(k["k"], f32)
+    L.po_rope(P(q), P(kk), k["dim"], k["head_dim"], k["pos"])
+    assert approx_eq(q, k["q_ref"], k["atol"], k["rtol"]).all()
+    assert approx_eq(kk, k["k_ref"], k["atol"], k["rtol"]).all()
+    k = KATS["vec_add"]
+    a, b, o = np.array(k["a"], f32), np.array(k["b"], f32), np.zeros(6, f32)
+    L.po_vec_add(P(o), P(a), P(b), 6)
+    assert (o == np.array(k["ref"], f32)).all()
+    k = KATS["vec_mul"]
+    a, b = np.array(k["a"], f32), np.array(k["b"], f32)
+    L.po_vec_mul(P(o), P(a), P(b), 6)
+    assert approx_eq(o, k["ref"], k["atol"], k["rtol"]).all()
+    k = KATS["embedding_lookup"]
+    t = np.array(k["table"], f32)
+    L.po_embedding_lookup(P(o), P(t), k["dim"], k["token"])
+    assert (o == np.array(k["ref"], f32)).all()
+    k = KATS["argmax"]
+    assert L.po_argmax(P(np.array(k["x"], f32)), 6) == k["ref"]
+    k = KATS["smatvec_cpu"]
+    W, x, y = np.array(k["W"], f32), np.array(k["x"], f32), np.zeros(4, f32)
+    L.po_smatvec(P(W), P(x), P(y), 4, 6)
+    assert approx_eq(y, k["ref"], k["atol"], k["rtol"]).all()
+
+
+# ── 2. bitwise agreement with the reference's own build ──────────────────
+
+needs_ref = pytest.mark.skipif(not ref_available(), reason="oracle/_ref not built (reference checkout absent)")
+
+
+@needs_ref
+def test_ref_math_bitwise():
+    L, R = oracle(), ref()
+    rng = np.random.default_rng(1)
+    xs = np.concatenate([rng.uniform(-90, 90, 4000), rng.uniform(-3, 3, 4000), rng.uniform(0, 1e4, 2000),
+                         [0.0, -0.0, 88.7, 88.71, -87.3, -87.31, 1e-30, 3.4e38]]).astype(f32)
+    for po, pt in (("po_expf", "pt_expf"), ("po_sinf", "pt_sinf"), ("po_cosf", "pt_cosf"),
+                   ("po_logf", "pt_logf"), ("po_sqrtf", "pt_sqrtf")):
+        a = np.array([getattr(L, po)(float(x)) for x in xs], f32)
+        b = np.array([getattr(R, pt)(float(x)) for x in xs], f32)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), po
+
+
+@needs_ref
+def test_ref_ops_bitwise():
+    L, R = oracle(), ref()
+    rng = np.random.default_rng(2)
+    for n in (6, 48, 288, 768):
+        x = rng.standard_normal(n).astype(f32)
+        w = rng.standard_normal(n).astype(f32)
+        a, b = np.zeros(n, f32), np.zeros(n, f32)
+        L.po_rmsnorm(P(a), P(x), P(w), n)
+        R.rmsnorm(P(b), P(x), P(w), n)
+        assert np.array_equal(a, b)
+        a, b = x.copy(), x.copy()
+        L.po_softmax(P(a), n)
+        R.softmax(P(b), n)
+        assert np.array_equal(a, b)
+        a, b = x.copy(), x.copy()
+        L.po_silu(P(a), n)
+        R.silu(P(b), n)
+        assert np.array_equal(a, b)
+    for dim, hd, pos in ((288, 48, 0), (288, 48, 255), (768, 64, 1023), (12, 6, 3)):
+        q, k = rng.standard_normal(dim).astype(f32), rng.standard_normal(dim).astype(f32)
+        q2, k2 = q.copy(), k.copy()
+        L.po_rope(P(q), P(k), dim, hd, pos)
+        R.rope(P(q2), P(k2), dim, hd, pos)
+        assert np.array_equal(q, q2) and np.array_equal(k, k2)
+        dq, dk, dq2, dk2 = (np.zeros(dim, f32) for _ in range(4))
+        L.po_rope_backward(P(dq), P(dk), P(q), P(k), dim, hd, pos)
+        R.rope_backward(P(dq2), P(dk2), P(q), P(k), dim, hd, pos)
+        assert np.array_equal(dq, dq2) and np.array_equal(dk, dk2)
+    for (d, n) in ((48, 48), (288, 768), (768, 288), (1000, 288)):
+        W = rng.uniform(-1, 1, (d, n)).astype(f32)
+        x = rng.uniform(-1, 1, n).astype(f32)
+        a, b = np.zeros(d, f32), np.zeros(d, f32)
+        L.po_smatvec(P(W), P(x), P(a), d, n)
+        R.smatvec_cpu(P(W), P(x), P(b), d, n)
+        assert np.array_equal(a, b)
+        dy = rng.uniform(-1, 1, d).astype(f32)
+        a, b = rng.uniform(-1, 1, n).astype(f32), None
+        b = a.copy()
+        L.po_matmul_backward_input(P(a), P(W), P(dy), d, n)
+        R.matmul_backward_input(P(b), P(W), P(dy), d, n)
+        assert np.array_equal(a, b)
+        T = 7
+        dY = rng.uniform(-1, 1, (T, d)).astype(f32)
+        X = rng.uniform(-1, 1, (T, n)).astype(f32)
+        a = rng.uniform(-1, 1, (d, n)).astype(f32)
+        b = a.copy()
+        L.po_matmul_backward_weight_batched(P(a), P(dY), P(X), d, n, T)
+        R.matmul_backward_weight_batched(P(b), P(dY), P(X), d, n, T)
+        assert np.array_equal(a, b)
+    for n in (6, 288):
+        x, w, do = (rng.standard_normal(n).astype(f32) for _ in range(3))
+        dx, dw, dx2, dw2 = (np.full(n, 0.5, f32) for _ in range(4))
+        L.po_rmsnorm_backward(P(dx), P(dw), P(do), P(x), P(w), n)
+        R.rmsnorm_backward(P(dx2), P(dw2), P(do), P(x), P(w), n)
+        assert np.array_equal(dx, dx2) and np.array_equal(dw, dw2)
+        y = np.abs(x) / np.abs(x).sum()
+        a, b = np.zeros(n, f32), np.zeros(n, f32)
+        L.po_softmax_backward(P(a), P(do), P(y.astype(f32)), n)
+        R.softmax_backward(P(b), P(do), P(y.astype(f32)), n)
+        assert np.array_equal(a, b)
+        a, b = np.zeros(n, f32), np.zeros(n, f32)
+        L.po_silu_backward(P(a), P(do), P(x), n)
+        R.silu_backward(P(b), P(do), P(x), n)
+        assert np.array_equal(a, b)
+
+
+def tiny_blob(dim=16, hidden=40, L=2, nh=2, V=256, S=16, seed=3, std=0.3):
+    """Small model for whole-step checks.  The reference's backward packs
+    seven per-layer transposes (4*D*D + 3*H*D floats, pt_train.c:669-680)
+    into w_transpose sized max(V*D, H*D) (pt_train.c:405-407), so reference
+    runs need V >= 4*D + 3*H."""
+    from pitorch_amd import synth_model
+    return synth_model((dim, hidden, L, nh, nh, V, S), seed, std)
+
+
+@needs_ref
+def test_ref_forward_and_train_bitwise():
+    """Whole decode steps and training steps: restatement == reference build."""
+    R = ref()
+    blob = tiny_blob()
+    ref_blob = blob.copy()
+    om = OracleModel(blob, max_T=8)
+    rc = R.ref_ctx_new(P(ref_blob), 8)
+    try:
+        tok = 5
+        for _ in range(12):
+            a = om.forward_step(tok)
+            b = R.ref_forward_step(rc, tok)
+            assert a == b
+            assert np.array_equal(om.logits(), arr(R.ref_logits(rc), 256))
+            tok = (a * 7 + 3) % 256
+        tokens = np.array([1, 9, 33, 2, 170, 60, 4, 211], np.int32)
+        for _ in range(3):
+            la = om.train_step(tokens, 0.05)
+            lb = R.ref_train_step(rc, tokens.ctypes.data_as(ip), 8, 0.05)
+            assert np.float32(la) == np.float32(lb)
+            n = __import__("ctypes").c_int()
+            g = arr(R.ref_grads(rc, __import__("ctypes").byref(n)), n.value)
+            assert np.array_equal(om.grads(), g)
+        assert np.array_equal(blob, ref_blob)   # SGD updated both blobs identically
+    finally:
+        om.close()
+        R.ref_ctx_free(rc)
+
+
+# ── 3. mathematics ────────────────────────────────────────────────────────
+
+def test_math_vs_libm():
+    L = oracle()
+    xs = np.linspace(-80, 80, 20001).astype(f32).astype(np.float64)   # exact float32 inputs
+    got = np.array([L.po_expf(float(x)) for x in xs])
+    # Degree-5 Taylor on |r| <= ln2/2: remainder <= r^6/6! * e^|r| = 3.4e-6
+    # (the reference comment's "~2e-7" is optimistic); the float32 range
+    # reduction r = x - n*ln2 adds |n|*ulp(ln2)-size error for large |x|.
+    assert np.max(np.abs(got / np.exp(xs) - 1)[np.abs(xs) < 10]) < 3.4e-6 + 1e-7
+    assert np.max(np.abs(got / np.exp(xs) - 1)) < 1e-5
+    # After folding to |x| <= pi/2 the Taylor remainders are x^11/11! = 3.6e-6
+    # (sin, degree 9) and x^10/10! = 2.5e-5 (cos, degree 8); the float32
+    # reduction by 2pi adds ~|k|*1.7e-7.
+    xs = np.linspace(-50, 50, 20001).astype(f32).astype(np.float64)
+    assert np.max(np.abs([L.po_sinf(float(x)) - math.sin(x) for x in xs])) < 3.6e-6 + 2e-6
+    assert np.max(np.abs([L.po_cosf(float(x)) - math.cos(x) for x in xs])) < 2.5e-5 + 3e-6
+    # log: 9-term series of ln(1+f), |f| <= 0.414: remainder f^10/10 = 1.5e-5
+    xs = np.exp(np.linspace(-20, 20, 5001)).astype(f32).astype(np.float64)
+    assert np.max(np.abs([L.po_logf(float(x)) - math.log(x) for x in xs])) < 1.5e-5
+    assert np.max(np.abs([L.po_sqrtf(float(x)) / math.sqrt(x) - 1 for x in xs])) < 1.2e-7
+    assert L.po_expf(100.0) == np.float32(3.4028235e38) and L.po_expf(-100.0) == 0.0
+    assert L.po_sqrtf(-1.0) == 0.0 and L.po_logf(0.0) < -3e38
+
+
+def lcg_ints(n, seed, hi=8):
+    """test_matvec.c:25-35: integer-valued floats 1..8 from an LCG."""
+    out = np.empty(n, f32)
+    s = seed
+    for i in range(n):
+        s = (s * 1103515245 + 12345) & 0xFFFFFFFF
+        out[i] = float((s >> 16) & (hi - 1)) + 1.0
+    return out
+
+
+def test_smatvec_exact_and_bounded():
+    L = oracle()
+    for (d, n) in ((48, 48), (288, 288), (768, 288), (288, 768)):
+        W = lcg_ints(d * n, 42).reshape(d, n)
+        x = lcg_ints(n, 137)
+        y = np.zeros(d, f32)
+        L.po_smatvec(P(W), P(x), P(y), d, n)
+        assert np.array_equal(y.astype(np.int64), W.astype(np.int64) @ x.astype(np.int64))
+    rng = np.random.default_rng(5)
+    d, n = 500, 2048
+    W = rng.uniform(-1, 1, (d, n)).astype(f32)
+    x = rng.uniform(-1, 1, n).astype(f32)
+    y = np.zeros(d, f32)
+    L.po_smatvec(P(W), P(x), P(y), d, n)
+    exact = W.astype(np.float64) @ x.astype(np.float64)
+    gamma = n * 2.0 ** -24 / (1 - n * 2.0 ** -24)
+    assert (np.abs(y - exact) <= gamma * (np.abs(W) @ np.abs(x))).all()
+
+
+def test_gemm_closed_forms():
+    L = oracle()
+    rng = np.random.default_rng(6)
+    M, K, N = 33, 17, 48
+    A = lcg_ints(M * K, 7, 16).reshape(M, K)
+    B = lcg_ints(K * N, 9, 16).reshape(K, N)
+    C = np.zeros((M, N), f32)
+    L.po_sgemm(P(A), P(B), P(C), M, K, N)
+    assert np.array_equal(C.astype(np.int64), A.astype(np.int64) @ B.astype(np.int64))
+    C0 = lcg_ints(M * N, 11, 16).reshape(M, N)
+    C = C0.copy()
+    L.po_sgemm_rect(P(A), P(B), P(C), M, K, N, 1)
+    assert np.array_equal(C.astype(np.int64), C0.astype(np.int64) + A.astype(np.int64) @ B.astype(np.int64))
+    # backward closed forms: d_x += W^T dy, d_W += dy x^T, batched = dY^T X
+    d, n, T = 40, 24, 9
+    W = rng.uniform(-1, 1, (d, n)).astype(f32)
+    dy = rng.uniform(-1, 1, d).astype(f32)
+    x = rng.uniform(-1, 1, n).astype(f32)
+    dx = np.zeros(n, f32)
+    L.po_matmul_backward_input(P(dx), P(W), P(dy), d, n)
+    assert np.allclose(dx, W.T.astype(np.float64) @ dy, rtol=0, atol=d * 2e-7)
+    dW = np.zeros((d, n), f32)
+    L.po_matmul_backward_weight(P(dW), P(dy), P(x), d, n)
+    assert np.array_equal(dW, np.outer(dy, x).astype(f32))       # one rounding per element
+    dY = rng.uniform(-1, 1, (T, d)).astype(f32)
+    X = rng.uniform(-1, 1, (T, n)).astype(f32)
+    dW = np.zeros((d, n), f32)
+    L.po_matmul_backward_weight_batched(P(dW), P(dY), P(X), d, n, T)
+    assert np.allclose(dW, dY.T.astype(np.float64) @ X, rtol=0, atol=T * 2e-7)
+
+
+def test_backward_ops_by_calculus():
+    L = oracle()
+    rng = np.random.default_rng(7)
+    n = 24
+    x, w, do = (rng.standard_normal(n) for _ in range(3))
+    # rmsnorm: o = x * w / sqrt(mean(x^2)+eps); analytic gradient in fp64
+    r = np.sqrt((x * x).mean() + 1e-5)
+    dw_ref = do * x / r
+    dx_ref = do * w / r - x * np.dot(do * w, x) / (n * r ** 3)
+    dx, dw = np.zeros(n, f32), np.zeros(n, f32)
+    L.po_rmsnorm_backward(P(dx), P(dw), P(do.astype(f32)), P(x.astype(f32)), P(w.astype(f32)), n)
+    assert np.allclose(dx, dx_ref, atol=1e-5) and np.allclose(dw, dw_ref, atol=1e-5)
+    # softmax backward vs explicit Jacobian
+    y = np.exp(x) / np.exp(x).sum()
+    J = np.diag(y) - np.outer(y, y)
+    g = np.zeros(n, f32)
+    L.po_softmax_backward(P(g), P(do.astype(f32)), P(y.astype(f32)), n)
+    assert np.allclose(g, J.T @ do, atol=1e-6)
+    # silu backward vs d/dx[x*sigmoid(x)]
+    s = 1 / (1 + np.exp(-x))
+    g = np.zeros(n, f32)
+    L.po_silu_backward(P(g), P(do.astype(f32)), P(x.astype(f32)), n)
+    assert np.allclose(g, do * (s + x * s * (1 - s)), atol=1e-5)
+    # rope backward is the transpose: <rope(a), b> == <a, rope_bwd(b)>; and it inverts rope
+    dim, hd, pos = 48, 12, 37
+    a, b = rng.standard_normal(dim).astype(f32), rng.standard_normal(dim).astype(f32)
+    ra, rk = a.copy(), a.copy()
+    L.po_rope(P(ra), P(rk), dim, hd, pos)
+    gq, gk = np.zeros(dim, f32), np.zeros(dim, f32)
+    L.po_rope_backward(P(gq), P(gk), P(b), P(b), dim, hd, pos)
+    assert abs(np.dot(ra.astype(np.float64), b) - np.dot(a.astype(np.float64), gq)) < 1e-4
+    inv_q, inv_k = np.zeros(dim, f32), np.zeros(dim, f32)
+    L.po_rope_backward(P(inv_q), P(inv_k), P(ra), P(rk), dim, hd, pos)
+    assert np.allclose(inv_q, a, atol=1e-5) and np.allclose(inv_k, a, atol=1e-5)
+
+
+def np_forward64(blob, tokens):
+    """Independent fp64 LLaMA-2 forward (positions 0..len-1) from the
+    architecture's definition, for the logits at the last position."""
+    h = np.frombuffer(blob[:28].tobytes(), np.int32)
+    D, H, Lyr, NH, _, V, S = (int(v) for v in h)
+    hd = D // NH
+    w = np.frombuffer(blob[28:].tobytes(), np.float32).astype(np.float64)
+    o = 0
+
+    def take(*shape):
+        nonlocal o
+        n = int(np.prod(shape))
+        t = w[o:o + n].reshape(shape)
+        o += n
+        return t
+    emb = take(V, D); ra = take(Lyr, D); wq = take(Lyr, D, D); wk = take(Lyr, D, D); wv = take(Lyr, D, D)
+    wo = take(Lyr, D, D); rf = take(Lyr, D); w1 = take(Lyr, H, D); w2 = take(Lyr, D, H); w3 = take(Lyr, H, D)
+    rfin = take(D)
+
+    def norm(x, g):
+        return x / np.sqrt((x * x).mean() + 1e-5) * g
+
+    def rope(v, p):
+        v = v.copy()
+        i = np.arange(0, D, 2)
+        ang = p * np.exp(-math.log(10000.0) * (i % hd) / hd)
+        c, s = np.cos(ang), np.sin(ang)
+        a, b = v[i].copy(), v[i + 1].copy()
+        v[i], v[i + 1] = a * c - b * s, a * s + b * c
+        return v
+    T = len(tokens)
+    x = emb[tokens].copy()
+    for l in range(Lyr):
+        xb = np.array([norm(x[t], ra[l]) for t in range(T)])
+        q = np.array([rope(wq[l] @ xb[t], t) for t in range(T)])
+        k = np.array([rope(wk[l] @ xb[t], t) for t in range(T)])
+        v = xb @ wv[l].T
+        att = np.zeros((T, D))
+        for hh in range(NH):
+            sl = slice(hh * hd, (hh + 1) * hd)
+            sc = q[:, sl] @ k[:, sl].T / math.sqrt(hd)
+            sc = np.where(np.tril(np.ones((T, T))) > 0, sc, -np.inf)
+            p = np.exp(sc - sc.max(1, keepdims=True))
+            p /= p.sum(1, keepdims=True)
+            att[:, sl] = p @ v[:, sl]
+        x = x + att @ wo[l].T
+        xb = np.array([norm(x[t], rf[l]) for t in range(T)])
+        h1, h3 = xb @ w1[l].T, xb @ w3[l].T
+        x = x + (h1 / (1 + np.exp(-h1)) * h3) @ w2[l].T
+    return norm(x[-1], rfin) @ emb.T
+
+
+def test_forward_vs_fp64_definition():
+    blob = tiny_blob()
+    om = OracleModel(blob)
+    toks = [5, 17, 3, 40, 9]
+    for t in toks:
+        om.forward_step(t)
+    want = np_forward64(blob, toks)
+    got = om.logits()
+    assert np.max(np.abs(got - want)) < 2e-4 * np.max(np.abs(want))
+    om.close()
+
+
+def test_train_gradients_by_finite_differences():
+    """po_backward's gradients match central differences of po_forward_train."""
+    import ctypes
+    L = oracle()
+    blob = tiny_blob(dim=8, hidden=16, L=1, nh=2, V=16, S=8, seed=4, std=0.5)
+    om = OracleModel(blob, max_T=6)
+    tokens = np.array([1, 7, 3, 12, 5, 9], np.int32)
+    L.po_zero_grads(om.h)
+    L.po_forward_train(om.h, tokens.ctypes.data_as(ip), 6)
+    L.po_backward(om.h, tokens.ctypes.data_as(ip), 6)
+    g = om.grads()
+    w = np.frombuffer(blob, dtype=np.float32, offset=28)   # view into the blob the oracle reads
+    n_params = len(g)
+    rng = np.random.default_rng(8)
+    idx = rng.choice(n_params, 40, replace=False)
+    eps = 2e-2
+    for i in idx:
+        old = float(w[i])
+        w[i] = old + eps
+        lp = L.po_forward_train(om.h, tokens.ctypes.data_as(ip), 6)
+        w[i] = old - eps
+        lm = L.po_forward_train(om.h, tokens.ctypes.data_as(ip), 6)
+        w[i] = old
+        fd = (lp - lm) / (2 * eps)
+        assert abs(fd - g[i]) < 2e-3 + 0.05 * abs(g[i]), (i, fd, g[i])
+    om.close()
+    del ctypes
+
+
+def test_generate_greedy_semantics():
+    """pt_text.c:314-361: forced prefill, clamp to seq_len, stop on 1/2."""
+    L = oracle()
+    blob = tiny_blob(S=12)
+    om = OracleModel(blob)
+    prompt = np.array([3, 9, 27], np.int32)
+    out = np.zeros(64, np.int32)
+    n = L.po_generate_greedy(om.h, prompt.ctypes.data_as(ip), 3, 100, out.ctypes.data_as(ip))
+    assert 1 <= n <= 12
+    assert list(out[:2]) == [9, 27]
+    om2 = OracleModel(blob.copy())
+    steps = []
+    tok = 3
+    for pos in range(n):
+        nxt = om2.forward_step(tok)
+        nxt = int(prompt[pos + 1]) if pos < 2 else nxt
+        steps.append(nxt)
+        tok = nxt
+    assert steps == list(out[:n])
+    if n < 12:
+        assert out[n - 1] in (1, 2)
+    om.close()
+    om2.close()
