@@ -14,6 +14,7 @@
 #include "ptmi_model.h"
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -25,108 +26,132 @@ struct AttnParams {
     const float *q;         // [D] post-RoPE query
     const float *kc, *vc;   // this layer's caches [seq_len, kv_dim]
     float *out;             // [D] attention output (xb)
-    float *part_o;          // [n_heads, n_chunks, head_dim]
-    float *part_ml;         // [n_heads, n_chunks, 2]  (max, sum)
-    unsigned *cnt;          // [n_heads] arrival counters, zero between launches
     const DecodeCtl *ctl;
-    int head_dim, kv_dim, kv_mul, n_chunks;
+    int head_dim, kv_dim, kv_mul;
     float scale;
 };
 
-// llama2.c:153-177, split over position chunks (flash-decoding).  Scores
-// use the reference's exponential (pt_math.c:8-25) at every rescale.
-__global__ __launch_bounds__(256) void k_attn_decode(AttnParams a) {
-    __shared__ float qs[kMaxHeadDim];
-    __shared__ float es[kAttnChunk];
-    __shared__ float red[4][kMaxHeadDim];
-    __shared__ float ml[2];
-    __shared__ int last;
+__device__ __forceinline__ float dot4(float4 a, float4 b, float acc) {
+    acc = fmaf(a.x, b.x, acc);
+    acc = fmaf(a.y, b.y, acc);
+    acc = fmaf(a.z, b.z, acc);
+    return fmaf(a.w, b.w, acc);
+}
 
-    const int h = blockIdx.y, c = blockIdx.x, tid = threadIdx.x;
-    const int pos = a.ctl->pos;
-    const int n_active = pos / kAttnChunk + 1;
-    if (c >= n_active) return;                    // uniform per block
-    const int hd = a.head_dim;
-    const int t0 = c * kAttnChunk;
+constexpr int kAttnWaves = 16;
+constexpr int kAttnUnroll = 8;
+
+// llama2.c:153-177: one workgroup per head over positions 0..pos.
+// G lanes hold one K/V row (G*4 >= head_dim) so a wave's load instruction
+// covers 64/G positions; kAttnUnroll such loads are issued before any is
+// consumed.  Scores live in LDS ([seq_len] floats, dynamic), the softmax is
+// block-wide, and the weighted V sum is reduced over row slots by shuffles
+// and over waves through LDS.  No cross-workgroup communication.
+template <int G>
+__global__ __launch_bounds__(kAttnWaves * 64) void k_attn_head(AttnParams a) {
+    constexpr int RPI = 64 / G;                 // rows per load instruction
+    constexpr int BATCH = RPI * kAttnUnroll;     // positions per wave per batch
+    extern __shared__ float sc[];
+    __shared__ float red[kAttnWaves][kMaxHeadDim];
+    __shared__ float wred[kAttnWaves];
+
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int slot = lane / G, sub = lane % G;
+    const int hd = a.head_dim, hd4 = hd >> 2;
+    const int n = a.ctl->pos + 1;
     const long ko = (long)(h / a.kv_mul) * hd;
+    const bool has = sub < hd4;
+    const int sub_c = has ? sub : 0;
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 q4 = reinterpret_cast<const float4 *>(a.q + h * hd)[sub_c];
+    if (!has) q4 = zero4;
 
-    if (tid < hd) qs[tid] = a.q[h * hd + tid];
-    __syncthreads();
-
-    // scores: 4 lanes per position, strided dims
-    {
-        const int p = tid >> 2, part = tid & 3;
-        const int t = t0 + p;
-        float s = 0.0f;
-        if (t <= pos) {
-            const float *kt = a.kc + (long)t * a.kv_dim + ko;
-            for (int i = part; i < hd; i += 4) s = fmaf(qs[i], kt[i], s);
+    // scores
+    for (int base = wave * BATCH; base < n; base += kAttnWaves * BATCH) {
+        float4 k4[kAttnUnroll];
+#pragma unroll
+        for (int u = 0; u < kAttnUnroll; u++) {
+            const int t = min(base + u * RPI + slot, n - 1);
+            k4[u] = reinterpret_cast<const float4 *>(a.kc + (long)t * a.kv_dim + ko)[sub_c];
         }
-        s = group_sum<4>(s);
-        if (part == 0) es[p] = s * a.scale;
-    }
-    __syncthreads();
-    if (tid < 64) {
-        const bool valid = t0 + tid <= pos;
-        const float s = valid ? es[tid] : -INFINITY;
-        const float m = group_max<64>(s);
-        const float e = valid ? d_expf(s - m) : 0.0f;
-        const float l = group_sum<64>(e);
-        es[tid] = e;
-        if (tid == 0) { ml[0] = m; ml[1] = l; }
-    }
-    __syncthreads();
-    // o[i] = sum_p e_p v_p[i]: 4 position groups x 64 dims
-    {
-        const int i = tid & 63, grp = tid >> 6;
-        if (i < hd) {
-            float o = 0.0f;
-            for (int p = grp; p < kAttnChunk && t0 + p <= pos; p += 4)
-                o = fmaf(es[p], a.vc[(long)(t0 + p) * a.kv_dim + ko + i], o);
-            red[grp][i] = o;
-        }
-        if (hd > 64) {   // second column block for head_dim in (64, 128]
-            const int i2 = i + 64;
-            if (i2 < hd) {
-                float o = 0.0f;
-                for (int p = grp; p < kAttnChunk && t0 + p <= pos; p += 4)
-                    o = fmaf(es[p], a.vc[(long)(t0 + p) * a.kv_dim + ko + i2], o);
-                red[grp][i2] = o;
-            }
+#pragma unroll
+        for (int u = 0; u < kAttnUnroll; u++) {
+            float s = has ? dot4(k4[u], q4, 0.0f) : 0.0f;
+            s = group_sum<G>(s);
+            const int t = base + u * RPI + slot;
+            if (sub == 0 && t < n) sc[t] = s * a.scale;
         }
     }
     __syncthreads();
-    const long slot = (long)h * a.n_chunks + c;
-    if (tid < hd) a.part_o[slot * hd + tid] = red[0][tid] + red[1][tid] + red[2][tid] + red[3][tid];
-    if (tid == 0) { a.part_ml[2 * slot] = ml[0]; a.part_ml[2 * slot + 1] = ml[1]; }
-    __threadfence();
+    // block max
+    float mx = -INFINITY;
+    for (int t = tid; t < n; t += kAttnWaves * 64) mx = fmaxf(mx, sc[t]);
+    mx = group_max<64>(mx);
+    if (lane == 0) wred[wave] = mx;
     __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = atomicAdd(&a.cnt[h], 1u);
-        last = (prev == (unsigned)(n_active - 1));
+    mx = wred[0];
+#pragma unroll
+    for (int w = 1; w < kAttnWaves; w++) mx = fmaxf(mx, wred[w]);
+    __syncthreads();
+    // exponentials (the reference's pt_expf) and their sum
+    float sum = 0.0f;
+    for (int t = tid; t < n; t += kAttnWaves * 64) {
+        const float e = d_expf(sc[t] - mx);
+        sc[t] = e;
+        sum += e;
+    }
+    sum = group_sum<64>(sum);
+    if (lane == 0) wred[wave] = sum;
+    __syncthreads();
+    sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; w++) sum += wred[w];
+    // weighted V rows
+    float4 acc = zero4;
+    for (int base = wave * BATCH; base < n; base += kAttnWaves * BATCH) {
+        float4 v4[kAttnUnroll];
+#pragma unroll
+        for (int u = 0; u < kAttnUnroll; u++) {
+            const int t = min(base + u * RPI + slot, n - 1);
+            v4[u] = reinterpret_cast<const float4 *>(a.vc + (long)t * a.kv_dim + ko)[sub_c];
+        }
+#pragma unroll
+        for (int u = 0; u < kAttnUnroll; u++) {
+            const int t = base + u * RPI + slot;
+            const float e = t < n ? sc[t] : 0.0f;
+            acc.x = fmaf(e, v4[u].x, acc.x);
+            acc.y = fmaf(e, v4[u].y, acc.y);
+            acc.z = fmaf(e, v4[u].z, acc.z);
+            acc.w = fmaf(e, v4[u].w, acc.w);
+        }
+    }
+    // reduce over the RPI row slots of the wave (lanes sub, sub+G, ...)
+#pragma unroll
+    for (int m = G; m < 64; m <<= 1) {
+        acc.x += __shfl_xor(acc.x, m);
+        acc.y += __shfl_xor(acc.y, m);
+        acc.z += __shfl_xor(acc.z, m);
+        acc.w += __shfl_xor(acc.w, m);
+    }
+    if (slot == 0 && has) {
+        red[wave][4 * sub + 0] = acc.x;
+        red[wave][4 * sub + 1] = acc.y;
+        red[wave][4 * sub + 2] = acc.z;
+        red[wave][4 * sub + 3] = acc.w;
     }
     __syncthreads();
-    if (!last) return;
-    __threadfence();
-    // combine the n_active partials of head h
     if (tid < hd) {
-        const float *pm = a.part_ml + 2 * (long)h * a.n_chunks;
-        const float *po = a.part_o + (long)h * a.n_chunks * hd;
-        float M = -INFINITY;
-        for (int k = 0; k < n_active; k++) M = fmaxf(M, pm[2 * k]);
-        float num = 0.0f, den = 0.0f;
-        for (int k = 0; k < n_active; k++) {
-            const float f = d_expf(pm[2 * k] - M);
-            num = fmaf(po[(long)k * hd + tid], f, num);
-            den = fmaf(pm[2 * k + 1], f, den);
-        }
-        a.out[h * hd + tid] = num / den;
+        float o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; w++) o += red[w][tid];
+        a.out[h * hd + tid] = o / sum;
     }
-    if (tid == 0) a.cnt[h] = 0u;
 }
 
 // argmax (pt_ops.c:65-70: first index of the maximum) + step bookkeeping
-// (pt.c:269 pos++, pt_text.c:344-350 prefill forcing).
+// (pt.c:269 pos++, pt_text.c:344-350 prefill forcing).  float4 loads, eight
+// in flight per thread; each thread scans ascending indices, ties resolve
+// to the smaller index.
 __global__ __launch_bounds__(1024) void k_argmax_step(const float *logits, int n, DecodeCtl *ctl,
                                                       const int *prompt, int *out_tokens) {
     __shared__ float sv[16];
@@ -134,9 +159,26 @@ __global__ __launch_bounds__(1024) void k_argmax_step(const float *logits, int n
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = tid; i < n; i += 1024) {
+    const int n4 = n >> 2;
+    const float4 *l4 = reinterpret_cast<const float4 *>(logits);
+    for (int base = tid; base < n4; base += 8 * 1024) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = l4[min(base + u * 1024, n4 - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i4 = base + u * 1024;
+            if (i4 < n4) {
+                if (v[u].x > bv) { bv = v[u].x; bi = 4 * i4; }
+                if (v[u].y > bv) { bv = v[u].y; bi = 4 * i4 + 1; }
+                if (v[u].z > bv) { bv = v[u].z; bi = 4 * i4 + 2; }
+                if (v[u].w > bv) { bv = v[u].w; bi = 4 * i4 + 3; }
+            }
+        }
+    }
+    for (int i = 4 * n4 + tid; i < n; i += 1024) {
         const float v = logits[i];
-        if (v > bv) { bv = v; bi = i; }      // ascending i: keeps the first max
+        if (v > bv) { bv = v; bi = i; }
     }
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) {
@@ -228,11 +270,13 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         TIMED(0, if ((st = launch_matvec(p, s))) return st);
 
         AttnParams a = {};
-        a.q = m->q; a.kc = kc; a.vc = vc; a.out = m->xb; a.part_o = m->part_o; a.part_ml = m->part_ml;
-        a.cnt = m->attn_cnt; a.ctl = m->ctl; a.head_dim = c.head_dim; a.kv_dim = (int)KV;
-        a.kv_mul = c.n_heads / c.n_kv_heads; a.n_chunks = m->n_chunks;
+        a.q = m->q; a.kc = kc; a.vc = vc; a.out = m->xb; a.ctl = m->ctl; a.head_dim = c.head_dim;
+        a.kv_dim = (int)KV; a.kv_mul = c.n_heads / c.n_kv_heads;
         a.scale = host_att_scale(c.head_dim);
-        TIMED(1, hipLaunchKernelGGL(k_attn_decode, dim3(m->n_chunks, c.n_heads), dim3(256), 0, s, a));
+        const size_t lds = (size_t)S * sizeof(float);
+        const int hd4 = c.head_dim / 4;
+        auto attn = hd4 <= 8 ? k_attn_head<8> : hd4 <= 16 ? k_attn_head<16> : k_attn_head<32>;
+        TIMED(1, hipLaunchKernelGGL(attn, dim3(c.n_heads), dim3(kAttnWaves * 64), lds, s, a));
         PTMI_HIP(hipGetLastError());
 
         p = MatvecParams{};
@@ -278,6 +322,15 @@ int build_graph(ptmi_model *m) {
     return PTMI_OK;
 }
 
+// One decode step: the captured graph, or the same launches enqueued
+// directly when PTMI_DECODE_EAGER=1 (profilers that do not follow graph
+// launches).
+int launch_step(ptmi_model *m, hipStream_t s) {
+    if (m->eager) return enqueue_step(m, s);
+    PTMI_HIP(hipGraphLaunch(m->exec, s));
+    return PTMI_OK;
+}
+
 int set_ctl(ptmi_model *m, int tok, int pos, int n_prompt) {
     DecodeCtl h = {tok, pos, n_prompt, 0};
     PTMI_HIP(hipMemcpyAsync(m->ctl, &h, sizeof(h), hipMemcpyHostToDevice, lib_stream()));
@@ -306,7 +359,7 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
     Resident *r = register_blob(blob, bytes, &st);
     if (!r) return st;
     const Config &c = r->c;
-    if (c.dim % 4 || c.hidden % 4 || c.head_dim % 2 || c.head_dim > kMaxHeadDim || c.kv_dim % 2)
+    if (c.dim % 4 || c.hidden % 4 || c.head_dim % 4 || c.head_dim > kMaxHeadDim || c.seq_len > kMaxSeqLen)
         return set_error(PTMI_ERR_ARG, "unsupported shape: dim=%d hidden=%d head_dim=%d", c.dim, c.hidden,
                          c.head_dim);
     if (max_T < 0 || max_T > c.seq_len) return set_error(PTMI_ERR_ARG, "max_T=%d outside [0, seq_len]", max_T);
@@ -314,20 +367,17 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
     m->res = r;
     m->c = c;
     m->max_T = max_T;
-    m->n_chunks = (c.seq_len + kAttnChunk - 1) / kAttnChunk;
     const size_t D = c.dim, H = c.hidden, V = c.vocab, S = c.seq_len, KV = c.kv_dim, L = c.n_layers;
-    const size_t NH = c.n_heads, NC = m->n_chunks, hd = c.head_dim;
-    size_t sizes[] = {D, D, D, H, V, L * S * KV, L * S * KV, NH * NC * hd, NH * NC * 2};
-    float **dst[] = {&m->x, &m->xb, &m->q, &m->hb, &m->logits, &m->kc, &m->vc, &m->part_o, &m->part_ml};
+    size_t sizes[] = {D, D, D, H, V, L * S * KV, L * S * KV};
+    float **dst[] = {&m->x, &m->xb, &m->q, &m->hb, &m->logits, &m->kc, &m->vc};
     size_t total = 0;
     for (size_t s : sizes) total += align_up(s, 64);
-    const size_t ints = align_up(NH, 64) + align_up(sizeof(DecodeCtl) / 4, 64) + 2 * align_up(S, 64);
+    const size_t ints = align_up(sizeof(DecodeCtl) / 4, 64) + 2 * align_up(S, 64);
     total += ints;
     hipError_t e = hipMalloc(&m->mem, total * sizeof(float));
     if (e != hipSuccess) { delete m; return hip_check(e, "hipMalloc(decode state)"); }
     size_t o = 0;
-    for (int i = 0; i < 9; i++) { *dst[i] = m->mem + o; o += align_up(sizes[i], 64); }
-    m->attn_cnt = (unsigned *)(m->mem + o); o += align_up(NH, 64);
+    for (int i = 0; i < 7; i++) { *dst[i] = m->mem + o; o += align_up(sizes[i], 64); }
     m->ctl = (DecodeCtl *)(m->mem + o); o += align_up(sizeof(DecodeCtl) / 4, 64);
     m->prompt = (int *)(m->mem + o); o += align_up(S, 64);
     m->out_tokens = (int *)(m->mem + o);
@@ -335,9 +385,13 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
     e = hipMemsetAsync(m->mem, 0, total * sizeof(float), s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) { (void)hipFree(m->mem); delete m; return hip_check(e, "zero decode state"); }
-    if ((st = build_graph(m))) { (void)hipFree(m->mem); delete m; return st; }
+    const char *eager = getenv("PTMI_DECODE_EAGER");
+    m->eager = eager && eager[0] == '1';
+    if (!m->eager && (st = build_graph(m))) { (void)hipFree(m->mem); delete m; return st; }
     if (max_T > 0 && (st = train_create(m))) {
-        (void)hipGraphExecDestroy(m->exec); (void)hipGraphDestroy(m->graph); (void)hipFree(m->mem);
+        if (m->exec) (void)hipGraphExecDestroy(m->exec);
+        if (m->graph) (void)hipGraphDestroy(m->graph);
+        (void)hipFree(m->mem);
         delete m;
         return st;
     }
@@ -381,8 +435,7 @@ int ptmi_model_forward_step(ptmi_model_t *m, int token, int *next) {
         return set_error(PTMI_ERR_STATE, "position %d: KV cache full (seq_len %d)", m->host_pos, m->c.seq_len);
     hipStream_t s = lib_stream();
     int st;
-    if ((st = set_ctl(m, token, m->host_pos, 0))) return st;
-    PTMI_HIP(hipGraphLaunch(m->exec, s));
+    if ((st = set_ctl(m, token, m->host_pos, 0)) || (st = launch_step(m, s))) return st;
     DecodeCtl h;
     PTMI_HIP(hipMemcpyAsync(&h, m->ctl, sizeof(h), hipMemcpyDeviceToHost, s));
     PTMI_HIP(hipStreamSynchronize(s));
@@ -415,7 +468,8 @@ int ptmi_model_generate(ptmi_model_t *m, const int *prompt, int n_prompt, int ma
     if ((st = zero_kv(m))) return st;
     PTMI_HIP(hipMemcpyAsync(m->prompt, prompt, (size_t)n_prompt * sizeof(int), hipMemcpyHostToDevice, s));
     if ((st = set_ctl(m, prompt[0], 0, n_prompt))) return st;
-    for (int i = 0; i < max_tokens; i++) PTMI_HIP(hipGraphLaunch(m->exec, s));
+    for (int i = 0; i < max_tokens; i++)
+        if ((st = launch_step(m, s))) return st;
     PTMI_HIP(hipMemcpyAsync(out, m->out_tokens, (size_t)max_tokens * sizeof(int), hipMemcpyDeviceToHost, s));
     PTMI_HIP(hipStreamSynchronize(s));
     m->host_pos = max_tokens;
@@ -435,7 +489,8 @@ int ptmi_model_decode_async(ptmi_model_t *m, int first_token, int n_steps) {
     hipStream_t s = lib_stream();
     int st;
     if ((st = set_ctl(m, first_token, m->host_pos, 0))) return st;
-    for (int i = 0; i < n_steps; i++) PTMI_HIP(hipGraphLaunch(m->exec, s));
+    for (int i = 0; i < n_steps; i++)
+        if ((st = launch_step(m, s))) return st;
     m->host_pos += n_steps;
     return PTMI_OK;
 }

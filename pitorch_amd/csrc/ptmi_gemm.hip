@@ -1,0 +1,308 @@
+// fp32 GEMMs on the CDNA4 matrix cores: C[M,N] (+)= op(A)[M,K] . op(B)[K,N]
+// with v_mfma_f32_16x16x4_f32.  These replace the training backward's
+// per-position matvecs / CPU outer products:
+//   dW = dY^T X  (TN) — matmul_backward_weight_batched, pt_train.c:475-492
+//   dX = dY W    (NN) — backward_input_pretrans, pt_train.c:442-453
+//   Y  = X W^T   (NT) — the batched form of the training forward's matvecs
+//
+// Block tile 64x64, K step 16, 256 threads = 4 waves in a 2x2 grid, each
+// wave a 32x32 sub-tile of 2x2 MFMA 16x16 blocks.  Tiles are staged in LDS
+// k-major (As[k][m], Bs[k][n]) so every MFMA operand read is 16 consecutive
+// floats; the next K tile is fetched into registers while the current one
+// feeds the matrix cores.  Operand layout of the 16x16x4 f32 MFMA (CDNA3/4):
+// lane l supplies A[l%16][l/16] and B[l/16][l%16]; result register r of lane
+// l is C[4*(l/16)+r][l%16].
+// Small-M*N shapes with long K split K over blockIdx.z into a workspace and
+// reduce in split order afterwards (deterministic, no atomics).
+#include "ptmi_internal.h"
+
+#include <algorithm>
+
+namespace ptmi {
+
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int BM = 64, BN = 64, BK = 16;
+
+struct GemmArgs {
+    const float *A; long lda;
+    const float *B; long ldb;
+    float *C; long ldc;
+    int M, N, K;
+    int accumulate;
+    float *partial;        // split-K workspace [splits][M][N] or null
+    int k_per_split;
+    bool a_vec, b_vec;     // 16-byte aligned rows: float4 global loads
+};
+
+// A(m, k): AT ? A[k*lda + m] : A[m*lda + k];  B(k, n): BT ? B[n*ldb + k] : B[k*ldb + n]
+template <bool AT>
+__device__ __forceinline__ void load_a(const GemmArgs &g, int m0, int k0, int kend, int tid, float (&r)[4]) {
+    if (AT) {   // rows of k, m contiguous: thread -> (k = tid/16, m = 4*(tid%16)+c)
+        const int k = k0 + tid / 16, m = m0 + 4 * (tid % 16);
+        const bool kin = k < kend;
+        const float *p = g.A + (long)min(k, kend - 1) * g.lda;
+        if (g.a_vec && m + 3 < g.M) {
+            float4 v = *reinterpret_cast<const float4 *>(p + m);
+            r[0] = kin ? v.x : 0.f; r[1] = kin ? v.y : 0.f; r[2] = kin ? v.z : 0.f; r[3] = kin ? v.w : 0.f;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++) r[c] = (kin && m + c < g.M) ? p[m + c] : 0.f;
+        }
+    } else {    // rows of m, k contiguous: thread -> (m = tid/4, k = 4*(tid%4)+c)
+        const int m = m0 + tid / 4, k = k0 + 4 * (tid % 4);
+        const bool min_ = m < g.M;
+        const float *p = g.A + (long)min(m, g.M - 1) * g.lda;
+        if (g.a_vec && k + 3 < kend) {
+            float4 v = *reinterpret_cast<const float4 *>(p + k);
+            r[0] = min_ ? v.x : 0.f; r[1] = min_ ? v.y : 0.f; r[2] = min_ ? v.z : 0.f; r[3] = min_ ? v.w : 0.f;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++) r[c] = (min_ && k + c < kend) ? p[k + c] : 0.f;
+        }
+    }
+}
+
+template <bool BT>
+__device__ __forceinline__ void load_b(const GemmArgs &g, int n0, int k0, int kend, int tid, float (&r)[4]) {
+    if (!BT) {  // rows of k, n contiguous
+        const int k = k0 + tid / 16, n = n0 + 4 * (tid % 16);
+        const bool kin = k < kend;
+        const float *p = g.B + (long)min(k, kend - 1) * g.ldb;
+        if (g.b_vec && n + 3 < g.N) {
+            float4 v = *reinterpret_cast<const float4 *>(p + n);
+            r[0] = kin ? v.x : 0.f; r[1] = kin ? v.y : 0.f; r[2] = kin ? v.z : 0.f; r[3] = kin ? v.w : 0.f;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++) r[c] = (kin && n + c < g.N) ? p[n + c] : 0.f;
+        }
+    } else {    // rows of n, k contiguous
+        const int n = n0 + tid / 4, k = k0 + 4 * (tid % 4);
+        const bool nin = n < g.N;
+        const float *p = g.B + (long)min(n, g.N - 1) * g.ldb;
+        if (g.b_vec && k + 3 < kend) {
+            float4 v = *reinterpret_cast<const float4 *>(p + k);
+            r[0] = nin ? v.x : 0.f; r[1] = nin ? v.y : 0.f; r[2] = nin ? v.z : 0.f; r[3] = nin ? v.w : 0.f;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++) r[c] = (nin && k + c < kend) ? p[k + c] : 0.f;
+        }
+    }
+}
+
+template <bool KMAJOR_ROWS>
+__device__ __forceinline__ void store_tile(float (*S)[BM + 4], int tid, const float (&r)[4]) {
+    if (KMAJOR_ROWS) {          // thread holds (k = tid/16, idx = 4*(tid%16)+c)
+        const int k = tid / 16, i = 4 * (tid % 16);
+#pragma unroll
+        for (int c = 0; c < 4; c++) S[k][i + c] = r[c];
+    } else {                    // thread holds (idx = tid/4, k = 4*(tid%4)+c)
+        const int i = tid / 4, k = 4 * (tid % 4);
+#pragma unroll
+        for (int c = 0; c < 4; c++) S[k + c][i] = r[c];
+    }
+}
+
+template <bool AT, bool BT>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
+    __shared__ float As[2][BK][BM + 4];
+    __shared__ float Bs[2][BK][BN + 4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int li = lane & 15, lk = lane >> 4;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kb = blockIdx.z * g.k_per_split;
+    const int kend = min(g.K, kb + g.k_per_split);
+
+    floatx4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    float ra[4], rb[4];
+    if (kb < kend) {
+        load_a<AT>(g, m0, kb, kend, tid, ra);
+        load_b<BT>(g, n0, kb, kend, tid, rb);
+        store_tile<AT>(As[0], tid, ra);
+        store_tile<!BT>(Bs[0], tid, rb);
+    }
+    __syncthreads();
+    int buf = 0;
+    for (int k0 = kb; k0 < kend; k0 += BK) {
+        const bool more = k0 + BK < kend;
+        if (more) {                                  // next tile -> registers
+            load_a<AT>(g, m0, k0 + BK, kend, tid, ra);
+            load_b<BT>(g, n0, k0 + BK, kend, tid, rb);
+        }
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 4) {
+            const float a0 = As[buf][kk + lk][wm * 32 + li];
+            const float a1 = As[buf][kk + lk][wm * 32 + 16 + li];
+            const float b0 = Bs[buf][kk + lk][wn * 32 + li];
+            const float b1 = Bs[buf][kk + lk][wn * 32 + 16 + li];
+            acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[1][1], 0, 0, 0);
+        }
+        if (more) {
+            store_tile<AT>(As[buf ^ 1], tid, ra);
+            store_tile<!BT>(Bs[buf ^ 1], tid, rb);
+        }
+        __syncthreads();
+        buf ^= 1;
+    }
+
+    // C[4*(l/16)+r][l%16] of each 16x16 block
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + wn * 32 + j * 16 + li;
+            if (n >= g.N) continue;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm * 32 + i * 16 + 4 * lk + r;
+                if (m >= g.M) continue;
+                const float v = acc[i][j][r];
+                if (g.partial) {
+                    g.partial[((long)blockIdx.z * g.M + m) * g.N + n] = v;
+                } else {
+                    float *c = g.C + (long)m * g.ldc + n;
+                    *c = g.accumulate ? *c + v : v;
+                }
+            }
+        }
+    }
+}
+
+// C (+)= sum_z partial[z], z ascending.
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float *partial, int splits, float *C, long ldc,
+                                                       int M, int N, int accumulate) {
+    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (long)M * N) return;
+    const int m = (int)(idx / N), n = (int)(idx % N);
+    float s = 0.0f;
+    for (int z = 0; z < splits; z++) s += partial[(long)z * M * N + idx];
+    float *c = C + (long)m * ldc + n;
+    *c = accumulate ? *c + s : s;
+}
+
+inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+// Launch op(A).op(B) with shapes validated; `ws` (optional) is a split-K
+// workspace of ws_floats floats.
+int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc, int M, int N,
+                int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s) {
+    if (M <= 0 || N <= 0 || K <= 0) return set_error(PTMI_ERR_ARG, "gemm: M=%d N=%d K=%d", M, N, K);
+    if (!A || !B || !C) return set_error(PTMI_ERR_ARG, "gemm: null operand");
+    if (op < 0 || op > 2) return set_error(PTMI_ERR_ARG, "gemm: op %d", op);
+    const bool AT = op == 1, BT = op == 2;
+    // minimum leading dimensions
+    if ((AT ? lda < M : lda < K) || (BT ? ldb < K : ldb < N) || ldc < N)
+        return set_error(PTMI_ERR_ARG, "gemm: leading dimension too small");
+    GemmArgs g;
+    g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc;
+    g.M = M; g.N = N; g.K = K; g.accumulate = accumulate;
+    g.a_vec = al16(A) && lda % 4 == 0;
+    g.b_vec = al16(B) && ldb % 4 == 0;
+    const int gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM;
+    const long blocks = (long)gx * gy;
+    int splits = 1;
+    if (blocks < 256 && K >= 4 * 256) {
+        splits = (int)std::min<long>((512 + blocks - 1) / blocks, K / 256);
+        while (splits > 1 && (size_t)splits * M * N > ws_floats) splits--;
+    }
+    g.k_per_split = ((K + splits - 1) / splits + BK - 1) / BK * BK;
+    splits = (K + g.k_per_split - 1) / g.k_per_split;
+    g.partial = splits > 1 ? ws : nullptr;
+    if (gy > 65535) return set_error(PTMI_ERR_ARG, "gemm: M too large");
+    dim3 grid(gx, gy, splits);
+    if (op == 0) hipLaunchKernelGGL((k_gemm<false, false>), grid, dim3(256), 0, s, g);
+    else if (op == 1) hipLaunchKernelGGL((k_gemm<true, false>), grid, dim3(256), 0, s, g);
+    else hipLaunchKernelGGL((k_gemm<false, true>), grid, dim3(256), 0, s, g);
+    PTMI_HIP(hipGetLastError());
+    if (splits > 1) {
+        const long n = (long)M * N;
+        hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ws, splits, C, ldc,
+                           M, N, accumulate);
+        PTMI_HIP(hipGetLastError());
+    }
+    return PTMI_OK;
+}
+
+}  // namespace ptmi
+
+using namespace ptmi;
+
+namespace {
+
+// Host-pointer GEMM: upload, run, download (the drop-in replacements for
+// the reference's host-memory GEMM calls).
+int host_gemm(int op, const float *A, size_t a_n, long lda, const float *B, size_t b_n, long ldb, float *C, int M,
+              int N, int K, int accumulate) {
+    int st = ensure_init();
+    if (st) return st;
+    hipStream_t s = lib_stream();
+    const size_t c_n = (size_t)M * N;
+    const size_t ws_n = std::min<size_t>(c_n * 64, (size_t)64 << 20);
+    float *dA = scratch_buf(0, a_n + b_n + c_n);
+    float *ws = scratch_buf(3, ws_n);
+    if (!dA || !ws) return ptmi_last_status();
+    float *dB = dA + a_n, *dC = dB + b_n;
+    PTMI_HIP(hipMemcpyAsync(dA, A, a_n * sizeof(float), hipMemcpyHostToDevice, s));
+    PTMI_HIP(hipMemcpyAsync(dB, B, b_n * sizeof(float), hipMemcpyHostToDevice, s));
+    if (accumulate) PTMI_HIP(hipMemcpyAsync(dC, C, c_n * sizeof(float), hipMemcpyHostToDevice, s));
+    if ((st = launch_gemm(op, dA, lda, dB, ldb, dC, N, M, N, K, accumulate, ws, ws_n, s))) return st;
+    PTMI_HIP(hipMemcpyAsync(C, dC, c_n * sizeof(float), hipMemcpyDeviceToHost, s));
+    PTMI_HIP(hipStreamSynchronize(s));
+    return PTMI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ptmi_gemm_dev(int op, const float *dA, long lda, const float *dB, long ldb, float *dC, long ldc, int M, int N,
+                  int K, int accumulate, void *stream) {
+    int st = ensure_init();
+    if (st) return st;
+    const size_t ws_n = std::min<size_t>((size_t)M * N * 64, (size_t)64 << 20);
+    float *ws = scratch_buf(3, ws_n);
+    if (!ws) return ptmi_last_status();
+    return launch_gemm(op, dA, lda, dB, ldb, dC, ldc, M, N, K, accumulate, ws, ws_n,
+                       stream ? (hipStream_t)stream : lib_stream());
+}
+
+int ptmi_sgemm_rect(const float *A, const float *B, float *C, int M, int K, int N, int accumulate) {
+    if (!A || !B || !C || M <= 0 || N <= 0 || K <= 0)
+        return set_error(PTMI_ERR_ARG, "ptmi_sgemm_rect: bad arguments (M=%d K=%d N=%d)", M, K, N);
+    return host_gemm(0, A, (size_t)M * K, K, B, (size_t)K * N, N, C, M, N, K, accumulate);
+}
+
+int ptmi_matmul_backward_weight_batched(float *d_W, const float *d_y_all, const float *x_all, int out_dim, int in_dim,
+                                        int T) {
+    if (!d_W || !d_y_all || !x_all || out_dim <= 0 || in_dim <= 0 || T < 0)
+        return set_error(PTMI_ERR_ARG, "ptmi_matmul_backward_weight_batched: bad arguments");
+    if (T == 0) return PTMI_OK;
+    // dW[out,in] += dY[T,out]^T . X[T,in]   (TN: A stored [K=T][M=out])
+    return host_gemm(1, d_y_all, (size_t)T * out_dim, out_dim, x_all, (size_t)T * in_dim, in_dim, d_W, out_dim, in_dim,
+                     T, 1);
+}
+
+int ptmi_matmul_backward_input_batched(float *d_x_all, const float *W, const float *d_y_all, int out_dim, int in_dim,
+                                       int T, int accumulate) {
+    if (!d_x_all || !W || !d_y_all || out_dim <= 0 || in_dim <= 0 || T < 0)
+        return set_error(PTMI_ERR_ARG, "ptmi_matmul_backward_input_batched: bad arguments");
+    if (T == 0) return PTMI_OK;
+    // dX[T,in] (+)= dY[T,out] . W[out,in]   (NN)
+    return host_gemm(0, d_y_all, (size_t)T * out_dim, out_dim, W, (size_t)out_dim * in_dim, in_dim, d_x_all, T, in_dim,
+                     out_dim, accumulate);
+}
+
+}  // extern "C"

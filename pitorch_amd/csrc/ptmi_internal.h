@@ -167,6 +167,11 @@ struct MatvecParams {
 // Launch y = epilogue(W . prologue(x)); validates shapes, picks a kernel.
 int launch_matvec(MatvecParams p, hipStream_t s);
 
+// C[M,N] (+)= op(A).op(B) on the matrix cores; op 0 NN, 1 TN (A stored
+// [K][M]), 2 NT (B stored [N][K]).  ws: split-K workspace (may be null).
+int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc, int M, int N,
+                int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s);
+
 // ── library state ───────────────────────────────────────────────────────
 struct Config {
     int dim, hidden, n_layers, n_heads, n_kv_heads, vocab, seq_len;

@@ -38,7 +38,7 @@ __device__ __forceinline__ float dot4(float4 w, float4 x, float acc) {
 // Runs on one wave; lane i handles row row0+i (pairs handled by even lanes).
 template <int EPI>
 __device__ __forceinline__ void run_epilogue(const MatvecParams &p, const float *vals,
-                                             int row0, int nrows, int lane) {
+                                             int row0, int nrows, int lane, int pos = 0) {
     if (lane >= nrows) return;
     const int r = row0 + lane;
     const float v = vals[lane];
@@ -54,7 +54,6 @@ __device__ __forceinline__ void run_epilogue(const MatvecParams &p, const float 
     } else {                                      // rope + KV write: llama2.c:147-151
         static_assert(EPI == EPI_QKV_ROPE, "epilogue");
         if (lane & 1) return;
-        const int pos = *p.pos;
         const float a = v, b = vals[lane + 1];
         if (r < p.q_rows) {
             float c, s;
@@ -97,20 +96,47 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
     const int row0 = active ? (int)row0l : 0;
     const int nrows = active ? min(p.rows_per_wave, p.rows - row0) : 0;
 
-    // ---- prologue: this lane's x chunks -> registers ----
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    // ---- main loop: two passes (2*RPP rows) per iteration ----
+    // Rows past the end re-read the wave's last row; their sums are dropped.
+    float4 la[IT], lb[IT];
+    auto load_pair = [&](int base) {
+        const int ra = min(base + slot, nrows - 1), rb = min(base + RPP + slot, nrows - 1);
+        const float4 *wa = reinterpret_cast<const float4 *>(p.W + (long)(row0 + ra) * p.ld);
+        const float4 *wb = reinterpret_cast<const float4 *>(p.W + (long)(row0 + rb) * p.ld);
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int c = sub + it * LPR;
+            if constexpr (EXACT) {
+                la[it] = wa[c];
+                lb[it] = wb[c];
+            } else {
+                const int cc = min(c, n4 - 1);
+                la[it] = wa[cc];
+                lb[it] = wb[cc];
+                if (c >= n4) { la[it] = zero4; lb[it] = zero4; }
+            }
+        }
+    };
+    // The first pair's weight loads go out before the prologue, so the x
+    // fetch and RMSNorm arithmetic overlap the weight latency.
+    if (nrows > 0) load_pair(0);
+
+    // ---- prologue: this lane's x chunks (and RMSNorm weights) -> registers.
+    // Every load the prologue and epilogue need is issued here, together,
+    // so they cost one memory round trip overlapping the weight fetch.
     const float *xs = p.x;
     if constexpr (PRO == PRO_EMBED_RMSNORM) xs = p.x + (long)(*p.token) * p.n;
-    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 xr[IT];
+    int pos = 0;
+    if constexpr (EPI == EPI_QKV_ROPE) pos = *p.pos;
+    float4 xr[IT], nw[IT];
 #pragma unroll
     for (int it = 0; it < IT; it++) {
         const int c = sub + it * LPR;
-        if constexpr (EXACT) {
-            xr[it] = reinterpret_cast<const float4 *>(xs)[c];
-        } else {
-            xr[it] = reinterpret_cast<const float4 *>(xs)[min(c, n4 - 1)];
-            if (c >= n4) xr[it] = zero4;
-        }
+        const int cc = EXACT ? c : min(c, n4 - 1);
+        xr[it] = reinterpret_cast<const float4 *>(xs)[cc];
+        if constexpr (PRO != PRO_NONE) nw[it] = reinterpret_cast<const float4 *>(p.norm_w)[cc];
+        if (!EXACT && c >= n4) xr[it] = zero4;
     }
     if (PRO == PRO_EMBED_RMSNORM && blockIdx.x == 0 && wave == 0 && slot == 0) {
 #pragma unroll
@@ -128,38 +154,17 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
         const float inv = 1.0f / d_sqrtf(ss / (float)p.n + 1e-5f);
 #pragma unroll
         for (int it = 0; it < IT; it++) {
-            const int c = sub + it * LPR;
-            if (c < n4) {
-                const float4 w = reinterpret_cast<const float4 *>(p.norm_w)[c];
-                xr[it].x = xr[it].x * inv * w.x;
-                xr[it].y = xr[it].y * inv * w.y;
-                xr[it].z = xr[it].z * inv * w.z;
-                xr[it].w = xr[it].w * inv * w.w;
-            }
+            xr[it].x = xr[it].x * inv * nw[it].x;
+            xr[it].y = xr[it].y * inv * nw[it].y;
+            xr[it].z = xr[it].z * inv * nw[it].z;
+            xr[it].w = xr[it].w * inv * nw[it].w;
         }
     }
 
-    // ---- main loop: two passes (2*RPP rows) per iteration ----
-    // Rows past the end re-read the wave's last row; their sums are dropped.
     for (int base = 0; base < nrows; base += 2 * RPP) {
+        if (base > 0) load_pair(base);
         const int ra = base + slot, rb = base + RPP + slot;
         const bool va = ra < nrows, vb = rb < nrows;
-        const float4 *wa = reinterpret_cast<const float4 *>(p.W + (long)(row0 + min(ra, nrows - 1)) * p.ld);
-        const float4 *wb = reinterpret_cast<const float4 *>(p.W + (long)(row0 + min(rb, nrows - 1)) * p.ld);
-        float4 la[IT], lb[IT];
-#pragma unroll
-        for (int it = 0; it < IT; it++) {
-            const int c = sub + it * LPR;
-            if constexpr (EXACT) {
-                la[it] = wa[c];
-                lb[it] = wb[c];
-            } else {
-                const int cc = min(c, n4 - 1);
-                la[it] = wa[cc];
-                lb[it] = wb[cc];
-                if (c >= n4) { la[it] = zero4; lb[it] = zero4; }
-            }
-        }
         float acc_a = 0.0f, acc_b = 0.0f;
 #pragma unroll
         for (int it = 0; it < IT; it++) {
@@ -174,7 +179,7 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
         }
     }
     __syncthreads();
-    if (active) run_epilogue<EPI>(p, ybuf[wave], row0, nrows, lane);
+    if (active) run_epilogue<EPI>(p, ybuf[wave], row0, nrows, lane, pos);
 }
 
 // Long rows (n > 64*9*4): one wave per row pair, x read through the cache

@@ -17,8 +17,8 @@ struct DecodeCtl {
 
 struct TrainState;   // defined by the training unit
 
-constexpr int kAttnChunk = 64;      // positions per attention workgroup
 constexpr int kMaxHeadDim = 128;
+constexpr int kMaxSeqLen = 16384;   // attention scores of one head fit in LDS
 
 }  // namespace ptmi
 
@@ -31,13 +31,11 @@ struct ptmi_model {
     float *mem = nullptr;
     float *x = nullptr, *xb = nullptr, *q = nullptr, *hb = nullptr, *logits = nullptr;
     float *kc = nullptr, *vc = nullptr;
-    float *part_o = nullptr, *part_ml = nullptr;
-    unsigned *attn_cnt = nullptr;
     ptmi::DecodeCtl *ctl = nullptr;
     int *prompt = nullptr, *out_tokens = nullptr;
-    int n_chunks = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    bool eager = false;                  // PTMI_DECODE_EAGER=1: no graph
     ptmi::TrainState *train = nullptr;
 };
 

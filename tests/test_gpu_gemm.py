@@ -1,0 +1,116 @@
+"""GPU parity of the fp32 MFMA training GEMMs against the oracle.
+
+* integer-valued inputs (1..16): every product and partial sum is exact in
+  fp32 (|sum| < 2^24), so GPU == oracle BIT FOR BIT for any summation order —
+  this also pins the MFMA operand/result lane layout;
+* U(-1,1) inputs: |C - C_fp64| <= gamma_K * (|A||B|) elementwise (the fp32
+  forward-error bound for a K-term dot product).
+Shapes: the reference's GEMM unit-test sizes (dev/tests/gemm/test_gemm.c:
+82-83) and every training GEMM of the 15M config at T=256 (R=255).
+"""
+import numpy as np
+import pytest
+
+import pitorch_amd as pa
+from pitorch_amd._hip import DeviceArray
+from tests._oracle import P, oracle
+from tests.test_oracle import lcg_ints
+
+pytestmark = pytest.mark.gpu
+R = 255
+DW = [(288, 288), (768, 288), (288, 768), (32000, 288)]      # dW[out,in] += dY^T X, K = R
+DX = [(288, 288), (768, 288), (288, 768), (32000, 288)]      # dX[R,in] = dY[R,out] W[out,in], K = out
+
+
+def ints(shape, seed):
+    return np.random.default_rng(seed).integers(1, 17, shape).astype(np.float32)
+
+
+def bound_ok(C, A64_B64_exact, absAB, K):
+    gamma = K * 2.0 ** -24 / (1 - K * 2.0 ** -24)
+    return np.all(np.abs(C - A64_B64_exact) <= gamma * absAB + 1e-30)
+
+
+@pytest.mark.parametrize("n", [16, 32])
+def test_sgemm_square_exact(n):
+    A = lcg_ints(n * n, 42, 16).reshape(n, n)
+    B = lcg_ints(n * n, 137, 16).reshape(n, n)
+    C = np.zeros((n, n), np.float32)
+    L = pa.load_ptmi()
+    assert L.ptmi_sgemm_rect(P(A), P(B), P(C), n, n, n, 0) == 0
+    ref = np.zeros((n, n), np.float32)
+    oracle().po_sgemm(P(A), P(B), P(ref), n, n, n)
+    assert np.array_equal(C, ref)
+
+
+@pytest.mark.parametrize("out_dim,in_dim", DW)
+def test_backward_weight_batched_exact(out_dim, in_dim):
+    dY, X = ints((R, out_dim), 1), ints((R, in_dim), 2)
+    dW = ints((out_dim, in_dim), 3)
+    ref = dW.copy()
+    L = pa.load_ptmi()
+    assert L.ptmi_matmul_backward_weight_batched(P(dW), P(dY), P(X), out_dim, in_dim, R) == 0
+    oracle().po_matmul_backward_weight_batched(P(ref), P(dY), P(X), out_dim, in_dim, R)
+    assert np.array_equal(dW, ref)
+
+
+@pytest.mark.parametrize("out_dim,in_dim", DX)
+def test_backward_input_batched_exact(out_dim, in_dim):
+    dY, W = ints((R, out_dim), 4), ints((out_dim, in_dim), 5)
+    dX = np.zeros((R, in_dim), np.float32)
+    L = pa.load_ptmi()
+    assert L.ptmi_matmul_backward_input_batched(P(dX), P(W), P(dY), out_dim, in_dim, R, 0) == 0
+    ref = np.zeros((R, in_dim), np.float32)
+    for t in range(R):
+        oracle().po_matmul_backward_input(P(ref[t]), P(W), P(dY[t]), out_dim, in_dim)
+    assert np.array_equal(dX, ref)
+
+
+@pytest.mark.parametrize("M,K,N", [(255, 288, 288), (255, 32000, 288), (300, 77, 130), (1, 5, 3)])
+def test_sgemm_rect_random_bounded(M, K, N):
+    rng = np.random.default_rng(M + K + N)
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
+    C = C0.copy()
+    L = pa.load_ptmi()
+    assert L.ptmi_sgemm_rect(P(A), P(B), P(C), M, K, N, 1) == 0
+    exact = C0.astype(np.float64) + A.astype(np.float64) @ B.astype(np.float64)
+    assert bound_ok(C, exact, np.abs(C0) + np.abs(A) @ np.abs(B), K + 1)
+
+
+@pytest.mark.parametrize("op", [0, 1, 2])
+def test_gemm_dev_ops_with_strides(op):
+    """Device-pointer entry: NN, TN, NT with padded leading dimensions."""
+    rng = np.random.default_rng(op)
+    M, N, K = 200, 96, 130
+    pad = 4
+    if op == 0:
+        A = rng.uniform(-1, 1, (M, K + pad)); B = rng.uniform(-1, 1, (K, N + pad))
+        Aop, Bop = A[:, :K], B[:, :N]
+    elif op == 1:
+        A = rng.uniform(-1, 1, (K, M + pad)); B = rng.uniform(-1, 1, (K, N + pad))
+        Aop, Bop = A[:, :M].T, B[:, :N]
+    else:
+        A = rng.uniform(-1, 1, (M, K + pad)); B = rng.uniform(-1, 1, (N, K + pad))
+        Aop, Bop = A[:, :K], B[:, :K].T
+    A, B = A.astype(np.float32), B.astype(np.float32)
+    C = np.zeros((M, N + pad), np.float32)
+    dA, dB, dC = DeviceArray.from_host(A), DeviceArray.from_host(B), DeviceArray.from_host(C)
+    L = pa.load_ptmi()
+    assert L.ptmi_gemm_dev(op, dA.ptr, A.shape[1], dB.ptr, B.shape[1], dC.ptr, N + pad, M, N, K, 0, None) == 0
+    assert L.ptmi_sync() == 0
+    got = dC.download().reshape(M, N + pad)
+    exact = Aop.astype(np.float32).astype(np.float64) @ Bop.astype(np.float32).astype(np.float64)
+    absab = np.abs(Aop.astype(np.float32)) @ np.abs(Bop.astype(np.float32))
+    assert bound_ok(got[:, :N], exact, absab, K)
+    assert np.all(got[:, N:] == 0)          # padding columns untouched
+    for a in (dA, dB, dC):
+        a.free()
+
+
+def test_gemm_errors():
+    L = pa.load_ptmi()
+    A = np.ones((4, 4), np.float32)
+    assert L.ptmi_sgemm_rect(P(A), P(A), P(A), 0, 4, 4, 0) == 1
+    assert L.ptmi_gemm_dev(3, P(A), 4, P(A), 4, P(A), 4, 4, 4, 4, 0, None) == 1

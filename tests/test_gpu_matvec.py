@@ -119,17 +119,16 @@ def test_registered_weights_resolve_to_device_layout():
         L.ptmi_unregister_weights(P(blob))
 
 
-def test_device_pointer_entry_on_caller_stream():
-    torch = pytest.importorskip("torch")
+def test_device_pointer_entry_with_row_stride():
+    from pitorch_amd._hip import DeviceArray
     L = pa.load_ptmi()
     d, n = 4096, 768
     W = pa.seed_uniform(5, d * (n + 4)).reshape(d, n + 4)         # ld = n + 4
     x = pa.seed_uniform(6, n)
-    dW = torch.from_numpy(W).cuda()
-    dx = torch.from_numpy(x).cuda()
-    dy = torch.empty(d, device="cuda")
-    s = torch.cuda.current_stream()
-    assert L.ptmi_matvec_dev(dW.data_ptr(), n + 4, dx.data_ptr(), dy.data_ptr(), d, n, s.cuda_stream) == 0
-    s.synchronize()
+    dW, dx, dy = DeviceArray.from_host(W), DeviceArray.from_host(x), DeviceArray(d)
+    assert L.ptmi_matvec_dev(dW.ptr, n + 4, dx.ptr, dy.ptr, d, n, None) == 0
+    assert L.ptmi_sync() == 0
     Wc = np.ascontiguousarray(W[:, :n])
-    check_close(dy.cpu().numpy(), oracle_mv(Wc, x), Wc, x)
+    check_close(dy.download(), oracle_mv(Wc, x), Wc, x)
+    for a in (dW, dx, dy):
+        a.free()
