@@ -75,6 +75,86 @@ def cpu_baseline(blob, prompt, budget_s=12.0, max_tokens=96):
                       f"1 thread, {cpu_model()}, host nproc={os.cpu_count()}"}
 
 
+MFMA_FP32_PEAK_TFLOPS = 157.3
+
+
+def train_gemm_shapes(cfg, T):
+    """Every GEMM of one pt_train_step at this config (op, M, N, K, count):
+    forward Y = X W^T (NT), backward dX = dY W (NN) and dW += dY^T X (TN),
+    R = T-1 backward rows; QKV and w1|w3 are fused as in the device layout."""
+    D, H, L, _, _, V, _ = cfg
+    R = T - 1
+    QS = 3 * D
+    fwd = [(2, T, QS, D, L), (2, T, D, D, L), (2, T, 2 * H, D, L), (2, T, D, H, L), (2, T, V, D, 1)]
+    dx = [(0, R, D, V, 1), (0, R, H, D, L), (0, R, D, 2 * H, L), (0, R, D, D, L), (0, R, D, QS, L)]
+    dw = [(1, V, D, R, 1), (1, D, H, R, L), (1, 2 * H, D, R, L), (1, D, D, R, L), (1, QS, D, R, L)]
+    return fwd + dx + dw
+
+
+def bench_train(pa, reps=5):
+    """stories15M training step (config 5): ms/step of the device pt_train_step
+    and fp32-MFMA utilisation of its GEMMs, each GEMM shape timed with HIP
+    events on the library stream."""
+    import numpy as np
+    from pitorch_amd._hip import DeviceArray, Event
+
+    L = pa.load_ptmi()
+    name, T, lr = "stories15M", 256, 1e-3
+    cfg = pa.STORIES[name]
+    blob = pa.synth_model(cfg, pa.SEED_MODEL[name])
+    tokens = pa.seed_tokens(pa.SEED_TRAIN, T, cfg[5])
+    m = pa.Model(blob, max_T=T)
+    m.train_step(tokens, lr)
+    t0 = time.perf_counter()
+    losses = [m.train_step(tokens, lr) for _ in range(17)]
+    step_ms = (time.perf_counter() - t0) * 1e3 / 17
+    m.close()
+    stream = L.ptmi_stream()
+    shapes = train_gemm_shapes(cfg, T)
+    maxA = max(M * K for _, M, N, K, _ in shapes)
+    maxB = max(K * N for _, M, N, K, _ in shapes)
+    maxC = max(M * N for _, M, N, K, _ in shapes)
+    A = DeviceArray.from_host(pa.seed_uniform(1, maxA))
+    B = DeviceArray.from_host(pa.seed_uniform(2, maxB))
+    C = DeviceArray(maxC)
+    total_flop, total_ms, rows = 0.0, 0.0, []
+    for op, M, N, K, count in shapes:
+        lda = K if op != 1 else M
+        ldb = N if op != 2 else K
+        pa._ffi.check(L.ptmi_gemm_dev(op, A.ptr, lda, B.ptr, ldb, C.ptr, N, M, N, K, 0, None))
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        for _ in range(reps):
+            pa._ffi.check(L.ptmi_gemm_dev(op, A.ptr, lda, B.ptr, ldb, C.ptr, N, M, N, K, 1, None))
+        e1.record(stream)
+        ms = e0.elapsed_ms(e1) / reps
+        flop = 2.0 * M * N * K
+        total_flop += flop * count
+        total_ms += ms * count
+        rows.append({"op": "NN TN NT".split()[op], "M": M, "N": N, "K": K, "count": count,
+                     "us": round(ms * 1e3, 2), "TFLOPs": round(flop / (ms * 1e-3) / 1e12, 2)})
+    for a in (A, B, C):
+        a.free()
+    tflops = total_flop / (total_ms * 1e-3) / 1e12
+    return {"workload": "stories15M training step, T=256, lr=1e-3 (config 5)", "ms_per_step": round(step_ms, 3),
+            "losses_first_last": [round(losses[0], 6), round(losses[-1], 6)],
+            "gemm_gflop_per_step": round(total_flop / 1e9, 3), "gemm_ms_per_step": round(total_ms, 4),
+            "gemm_tflops": round(tflops, 2), "gemm_frac_fp32_mfma": round(tflops / MFMA_FP32_PEAK_TFLOPS, 4),
+            "by_shape": rows}
+
+
+def calib_copy(pa, mb=256):
+    """One device-to-device copy of known size: the reference point for the
+    FETCH_SIZE / WRITE_SIZE counters of the HBM-traffic profiles."""
+    from pitorch_amd._hip import DeviceArray, hip
+    n = mb * (1 << 20) // 4
+    a, b = DeviceArray(n), DeviceArray(n)
+    hip().hipMemcpy(b.ptr, a.ptr, n * 4, 3)
+    hip().hipDeviceSynchronize()
+    a.free()
+    b.free()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -83,6 +163,7 @@ def main():
     ap.add_argument("--config", default="stories110M")
     ap.add_argument("--profile-steps", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-train", action="store_true", help="skip the training-GEMM leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -151,8 +232,15 @@ def main():
     for r, e in breakdown.items():
         print(f"[bench] {r:12s} {json.dumps(e)}", file=sys.stderr, flush=True)
 
-    cpu = None if args.no_cpu else cpu_baseline(blob, prompt)
     m.close()
+    del blob
+    calib_copy(pa)
+    train = None if args.no_train else bench_train(pa)
+    if train:
+        print(f"[bench] train {json.dumps({k: v for k, v in train.items() if k != 'by_shape'})}", file=sys.stderr,
+              flush=True)
+    blob = pa.synth_model(cfg, pa.SEED_MODEL[name])
+    cpu = None if args.no_cpu else cpu_baseline(blob, prompt)
 
     line = {
         "metric": "decode tok/s + matvec HBM GB/s (% peak), stories110M-shape fp32, 1 GPU",
@@ -175,6 +263,7 @@ def main():
                      "traffic": None, "bytes_per_launch": dom["bytes_per_launch"], "avg_us": dom["avg_us"]},
         "cpu_baseline": cpu,
         "breakdown": breakdown,
+        "train": train,
     }
     print(json.dumps(line), flush=True)
 

@@ -16,6 +16,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <vector>
 
 namespace ptmi {
@@ -25,10 +26,12 @@ namespace {
 struct AttnParams {
     const float *q;         // [D] post-RoPE query
     const float *kc, *vc;   // this layer's caches [seq_len, kv_dim]
-    float *out;             // [D] attention output (xb)
+    float *part_o;          // [heads][chunks][head_dim] unnormalised weighted V sums
+    float *part_ml;         // [heads][chunks][2] chunk max, chunk sum of e^(s - max)
     const DecodeCtl *ctl;
-    int head_dim, kv_dim, kv_mul;
+    int head_dim, kv_dim, kv_mul, n_heads, chunk, n_chunks;
     float scale;
+    PrefetchDesc pf;        // blocks past n_heads*n_chunks prefetch the next weights
 };
 
 __device__ __forceinline__ float dot4(float4 a, float4 b, float acc) {
@@ -38,27 +41,36 @@ __device__ __forceinline__ float dot4(float4 a, float4 b, float acc) {
     return fmaf(a.w, b.w, acc);
 }
 
-constexpr int kAttnWaves = 16;
+constexpr int kAttnWaves = 4;
 constexpr int kAttnUnroll = 8;
+constexpr int kMaxAttnChunk = 512;
 
-// llama2.c:153-177: one workgroup per head over positions 0..pos.
-// G lanes hold one K/V row (G*4 >= head_dim) so a wave's load instruction
-// covers 64/G positions; kAttnUnroll such loads are issued before any is
-// consumed.  Scores live in LDS ([seq_len] floats, dynamic), the softmax is
-// block-wide, and the weighted V sum is reduced over row slots by shuffles
-// and over waves through LDS.  No cross-workgroup communication.
+// llama2.c:153-177, split over (head, chunk of positions) workgroups so the
+// KV-cache read is spread over many CUs (one CU streams only ~30 GB/s).
+// Each workgroup leaves its chunk's max m, sum l = sum e^(s-m) and the
+// unnormalised sum o = sum e^(s-m) v; the Wo matvec combines the chunks.
+// G lanes hold one K/V row (G*4 >= head_dim); a wave's load covers 64/G
+// positions and kAttnUnroll loads are in flight before any is consumed.
 template <int G>
-__global__ __launch_bounds__(kAttnWaves * 64) void k_attn_head(AttnParams a) {
-    constexpr int RPI = 64 / G;                 // rows per load instruction
-    constexpr int BATCH = RPI * kAttnUnroll;     // positions per wave per batch
-    extern __shared__ float sc[];
+__global__ __launch_bounds__(kAttnWaves * 64) void k_attn_chunk(AttnParams a) {
+    constexpr int RPI = 64 / G;
+    constexpr int BATCH = RPI * kAttnUnroll;
+    __shared__ float sc[kMaxAttnChunk];
     __shared__ float red[kAttnWaves][kMaxHeadDim];
     __shared__ float wred[kAttnWaves];
 
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if ((int)blockIdx.x >= a.n_heads * a.n_chunks) {
+        run_prefetch(a.pf);
+        return;
+    }
+    const int h = blockIdx.x % a.n_heads, c = blockIdx.x / a.n_heads;
+    const int n = a.ctl->pos + 1;
+    const int t0 = c * a.chunk;
+    if (t0 >= n) return;                               // uniform per block
+    const int t1 = min(t0 + a.chunk, n);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / G, sub = lane % G;
     const int hd = a.head_dim, hd4 = hd >> 2;
-    const int n = a.ctl->pos + 1;
     const long ko = (long)(h / a.kv_mul) * hd;
     const bool has = sub < hd4;
     const int sub_c = has ? sub : 0;
@@ -66,12 +78,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void k_attn_head(AttnParams a) {
     float4 q4 = reinterpret_cast<const float4 *>(a.q + h * hd)[sub_c];
     if (!has) q4 = zero4;
 
-    // scores
-    for (int base = wave * BATCH; base < n; base += kAttnWaves * BATCH) {
+    for (int base = t0 + wave * BATCH; base < t1; base += kAttnWaves * BATCH) {
         float4 k4[kAttnUnroll];
 #pragma unroll
         for (int u = 0; u < kAttnUnroll; u++) {
-            const int t = min(base + u * RPI + slot, n - 1);
+            const int t = min(base + u * RPI + slot, t1 - 1);
             k4[u] = reinterpret_cast<const float4 *>(a.kc + (long)t * a.kv_dim + ko)[sub_c];
         }
 #pragma unroll
@@ -79,13 +90,13 @@ __global__ __launch_bounds__(kAttnWaves * 64) void k_attn_head(AttnParams a) {
             float s = has ? dot4(k4[u], q4, 0.0f) : 0.0f;
             s = group_sum<G>(s);
             const int t = base + u * RPI + slot;
-            if (sub == 0 && t < n) sc[t] = s * a.scale;
+            if (sub == 0 && t < t1) sc[t - t0] = s * a.scale;
         }
     }
     __syncthreads();
-    // block max
+    const int cnt = t1 - t0;
     float mx = -INFINITY;
-    for (int t = tid; t < n; t += kAttnWaves * 64) mx = fmaxf(mx, sc[t]);
+    for (int i = tid; i < cnt; i += kAttnWaves * 64) mx = fmaxf(mx, sc[i]);
     mx = group_max<64>(mx);
     if (lane == 0) wred[wave] = mx;
     __syncthreads();
@@ -93,39 +104,33 @@ __global__ __launch_bounds__(kAttnWaves * 64) void k_attn_head(AttnParams a) {
 #pragma unroll
     for (int w = 1; w < kAttnWaves; w++) mx = fmaxf(mx, wred[w]);
     __syncthreads();
-    // exponentials (the reference's pt_expf) and their sum
     float sum = 0.0f;
-    for (int t = tid; t < n; t += kAttnWaves * 64) {
-        const float e = d_expf(sc[t] - mx);
-        sc[t] = e;
+    for (int i = tid; i < cnt; i += kAttnWaves * 64) {
+        const float e = d_expf(sc[i] - mx);
+        sc[i] = e;
         sum += e;
     }
     sum = group_sum<64>(sum);
     if (lane == 0) wred[wave] = sum;
     __syncthreads();
-    sum = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kAttnWaves; w++) sum += wred[w];
-    // weighted V rows
     float4 acc = zero4;
-    for (int base = wave * BATCH; base < n; base += kAttnWaves * BATCH) {
+    for (int base = t0 + wave * BATCH; base < t1; base += kAttnWaves * BATCH) {
         float4 v4[kAttnUnroll];
 #pragma unroll
         for (int u = 0; u < kAttnUnroll; u++) {
-            const int t = min(base + u * RPI + slot, n - 1);
+            const int t = min(base + u * RPI + slot, t1 - 1);
             v4[u] = reinterpret_cast<const float4 *>(a.vc + (long)t * a.kv_dim + ko)[sub_c];
         }
 #pragma unroll
         for (int u = 0; u < kAttnUnroll; u++) {
             const int t = base + u * RPI + slot;
-            const float e = t < n ? sc[t] : 0.0f;
+            const float e = t < t1 ? sc[t - t0] : 0.0f;
             acc.x = fmaf(e, v4[u].x, acc.x);
             acc.y = fmaf(e, v4[u].y, acc.y);
             acc.z = fmaf(e, v4[u].z, acc.z);
             acc.w = fmaf(e, v4[u].w, acc.w);
         }
     }
-    // reduce over the RPI row slots of the wave (lanes sub, sub+G, ...)
 #pragma unroll
     for (int m = G; m < 64; m <<= 1) {
         acc.x += __shfl_xor(acc.x, m);
@@ -140,11 +145,19 @@ __global__ __launch_bounds__(kAttnWaves * 64) void k_attn_head(AttnParams a) {
         red[wave][4 * sub + 3] = acc.w;
     }
     __syncthreads();
+    const long slot_id = (long)h * a.n_chunks + c;
     if (tid < hd) {
         float o = 0.0f;
 #pragma unroll
         for (int w = 0; w < kAttnWaves; w++) o += red[w][tid];
-        a.out[h * hd + tid] = o / sum;
+        a.part_o[slot_id * hd + tid] = o;
+    }
+    if (tid == 0) {
+        float l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; w++) l += wred[w];
+        a.part_ml[2 * slot_id] = mx;
+        a.part_ml[2 * slot_id + 1] = l;
     }
 }
 
@@ -153,7 +166,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void k_attn_head(AttnParams a) {
 // in flight per thread; each thread scans ascending indices, ties resolve
 // to the smaller index.
 __global__ __launch_bounds__(1024) void k_argmax_step(const float *logits, int n, DecodeCtl *ctl,
-                                                      const int *prompt, int *out_tokens) {
+                                                      const int *prompt, int *out_tokens, PrefetchDesc pf) {
+    if (blockIdx.x > 0) {
+        run_prefetch(pf);
+        return;
+    }
     __shared__ float sv[16];
     __shared__ int si[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -251,11 +268,27 @@ struct StepTimer {
         if (tm && (st = tm->end(s))) return st;                 \
     } while (0)
 
+// Producer-side prefetch of consumer matvec weights W[rows, n] (ld = n).
+PrefetchDesc pf_matvec(const ptmi_model *m, const float *W, int rows, int n, int first_block) {
+    if (!m->prefetch) return PrefetchDesc{};
+    return prefetch_for(W, n, rows, n, first_block, m->sink);
+}
+
+int matvec_compute_blocks(int rows, int n) {
+    MatvecGeom g;
+    return matvec_geometry(rows, n, &g) ? 8 * g.blocks_per_xcd : 0;
+}
+
 // Enqueue one decode step on s (used both for capture and eager runs).
+// Each stage prefetches the weights of a later matvec into the L2 of the
+// XCDs that will read them:
+//   QKV_l -> Wo_l,  attention_l -> w13_l,  Wo_l -> w2_l,
+//   w13_l -> QKV_{l+1},  classifier -> QKV_0 (next token).
 int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
     const Config &c = m->c;
     const Resident *r = m->res;
     const long D = c.dim, H = c.hidden, KV = c.kv_dim, S = c.seq_len;
+    const int QR = (int)(D + 2 * KV);
     int st = PTMI_OK;
     for (int l = 0; l < c.n_layers; l++) {
         float *kc = m->kc + (long)l * S * KV, *vc = m->vc + (long)l * S * KV;
@@ -267,27 +300,36 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         p.norm_w = r->rms_att + l * D;
         p.y = m->q; p.epi = EPI_QKV_ROPE; p.pos = &m->ctl->pos;
         p.q_rows = (int)D; p.kv_rows = (int)KV; p.head_dim = c.head_dim; p.k_cache = kc; p.v_cache = vc;
+        p.pf = pf_matvec(m, r->wo + (long)l * D * D, (int)D, (int)D, matvec_compute_blocks(QR, (int)D));
         TIMED(0, if ((st = launch_matvec(p, s))) return st);
 
         AttnParams a = {};
-        a.q = m->q; a.kc = kc; a.vc = vc; a.out = m->xb; a.ctl = m->ctl; a.head_dim = c.head_dim;
-        a.kv_dim = (int)KV; a.kv_mul = c.n_heads / c.n_kv_heads;
+        a.q = m->q; a.kc = kc; a.vc = vc; a.part_o = m->part_o; a.part_ml = m->part_ml; a.ctl = m->ctl;
+        a.head_dim = c.head_dim; a.kv_dim = (int)KV; a.kv_mul = c.n_heads / c.n_kv_heads;
+        a.n_heads = c.n_heads; a.chunk = m->attn_chunk; a.n_chunks = m->attn_chunks;
         a.scale = host_att_scale(c.head_dim);
-        const size_t lds = (size_t)S * sizeof(float);
         const int hd4 = c.head_dim / 4;
-        auto attn = hd4 <= 8 ? k_attn_head<8> : hd4 <= 16 ? k_attn_head<16> : k_attn_head<32>;
-        TIMED(1, hipLaunchKernelGGL(attn, dim3(c.n_heads), dim3(kAttnWaves * 64), lds, s, a));
+        auto attn = hd4 <= 8 ? k_attn_chunk<8> : hd4 <= 16 ? k_attn_chunk<16> : k_attn_chunk<32>;
+        const int attn_blocks = c.n_heads * m->attn_chunks;
+        a.pf = pf_matvec(m, r->w13 + (long)l * 2 * H * D, (int)(2 * H), (int)D, attn_blocks);
+        a.pf.first_block = attn_blocks;
+        TIMED(1, hipLaunchKernelGGL(attn, dim3(attn_blocks + a.pf.blocks), dim3(kAttnWaves * 64), 0, s, a));
         PTMI_HIP(hipGetLastError());
 
         p = MatvecParams{};
         p.W = r->wo + (long)l * D * D; p.ld = D; p.rows = (int)D; p.n = (int)D;
-        p.x = m->xb; p.y = m->x; p.pro = PRO_NONE; p.epi = EPI_RESIDUAL;
+        p.x = m->xb; p.y = m->x; p.pro = PRO_ATTN_COMBINE; p.epi = EPI_RESIDUAL;
+        p.pos = &m->ctl->pos; p.att_o = m->part_o; p.att_ml = m->part_ml;
+        p.att_chunks = m->attn_chunks; p.att_chunk = m->attn_chunk; p.att_heads = c.n_heads;
+        p.pf = pf_matvec(m, r->w2 + (long)l * D * H, (int)D, (int)H, matvec_compute_blocks((int)D, (int)D));
         TIMED(2, if ((st = launch_matvec(p, s))) return st);
 
         p = MatvecParams{};
         p.W = r->w13 + (long)l * 2 * H * D; p.ld = D; p.rows = (int)(2 * H); p.n = (int)D;
         p.x = m->x; p.pro = PRO_RMSNORM; p.norm_w = r->rms_ffn + l * D;
         p.y = m->hb; p.epi = EPI_SWIGLU;
+        if (l + 1 < c.n_layers)
+            p.pf = pf_matvec(m, r->wqkv + (long)(l + 1) * QR * D, QR, (int)D, matvec_compute_blocks((int)(2 * H), (int)D));
         TIMED(3, if ((st = launch_matvec(p, s))) return st);
 
         p = MatvecParams{};
@@ -298,9 +340,11 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
     MatvecParams p = {};
     p.W = r->wcls; p.ld = D; p.rows = c.vocab; p.n = (int)D;
     p.x = m->x; p.pro = PRO_RMSNORM; p.norm_w = r->rms_final; p.y = m->logits; p.epi = EPI_STORE;
+    p.pf = pf_matvec(m, r->wqkv, QR, (int)D, matvec_compute_blocks(c.vocab, (int)D));
     TIMED(5, if ((st = launch_matvec(p, s))) return st);
+    const PrefetchDesc none = {};
     TIMED(6, hipLaunchKernelGGL(k_argmax_step, dim3(1), dim3(1024), 0, s, m->logits, c.vocab, m->ctl,
-                                m->prompt, m->out_tokens));
+                                m->prompt, m->out_tokens, none));
     PTMI_HIP(hipGetLastError());
     return PTMI_OK;
 }
@@ -359,7 +403,8 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
     Resident *r = register_blob(blob, bytes, &st);
     if (!r) return st;
     const Config &c = r->c;
-    if (c.dim % 4 || c.hidden % 4 || c.head_dim % 4 || c.head_dim > kMaxHeadDim || c.seq_len > kMaxSeqLen)
+    if (c.dim % 4 || c.hidden % 4 || c.head_dim % 4 || c.head_dim > kMaxHeadDim || c.seq_len > kMaxSeqLen ||
+        c.dim > kMaxCombineDim)
         return set_error(PTMI_ERR_ARG, "unsupported shape: dim=%d hidden=%d head_dim=%d", c.dim, c.hidden,
                          c.head_dim);
     if (max_T < 0 || max_T > c.seq_len) return set_error(PTMI_ERR_ARG, "max_T=%d outside [0, seq_len]", max_T);
@@ -368,25 +413,33 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
     m->c = c;
     m->max_T = max_T;
     const size_t D = c.dim, H = c.hidden, V = c.vocab, S = c.seq_len, KV = c.kv_dim, L = c.n_layers;
-    size_t sizes[] = {D, D, D, H, V, L * S * KV, L * S * KV};
-    float **dst[] = {&m->x, &m->xb, &m->q, &m->hb, &m->logits, &m->kc, &m->vc};
+    // attention chunks: <= 8 per head, 64..kMaxAttnChunk positions each
+    const int per = (c.seq_len + 7) / 8;
+    m->attn_chunk = std::min(kMaxAttnChunk, std::max(64, (per + 63) / 64 * 64));
+    m->attn_chunks = (c.seq_len + m->attn_chunk - 1) / m->attn_chunk;
+    const size_t NH = c.n_heads, NC = m->attn_chunks, hd = c.head_dim;
+    size_t sizes[] = {D, D, D, H, V, L * S * KV, L * S * KV, NH * NC * hd, NH * NC * 2};
+    float **dst[] = {&m->x, &m->xb, &m->q, &m->hb, &m->logits, &m->kc, &m->vc, &m->part_o, &m->part_ml};
     size_t total = 0;
     for (size_t s : sizes) total += align_up(s, 64);
-    const size_t ints = align_up(sizeof(DecodeCtl) / 4, 64) + 2 * align_up(S, 64);
+    const size_t ints = align_up(sizeof(DecodeCtl) / 4, 64) + 2 * align_up(S, 64) + 64;
     total += ints;
     hipError_t e = hipMalloc(&m->mem, total * sizeof(float));
     if (e != hipSuccess) { delete m; return hip_check(e, "hipMalloc(decode state)"); }
     size_t o = 0;
-    for (int i = 0; i < 7; i++) { *dst[i] = m->mem + o; o += align_up(sizes[i], 64); }
+    for (int i = 0; i < 9; i++) { *dst[i] = m->mem + o; o += align_up(sizes[i], 64); }
     m->ctl = (DecodeCtl *)(m->mem + o); o += align_up(sizeof(DecodeCtl) / 4, 64);
     m->prompt = (int *)(m->mem + o); o += align_up(S, 64);
-    m->out_tokens = (int *)(m->mem + o);
+    m->out_tokens = (int *)(m->mem + o); o += align_up(S, 64);
+    m->sink = m->mem + o;
     hipStream_t s = lib_stream();
     e = hipMemsetAsync(m->mem, 0, total * sizeof(float), s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) { (void)hipFree(m->mem); delete m; return hip_check(e, "zero decode state"); }
     const char *eager = getenv("PTMI_DECODE_EAGER");
     m->eager = eager && eager[0] == '1';
+    const char *nopf = getenv("PTMI_NO_PREFETCH");
+    m->prefetch = !(nopf && nopf[0] == '1');
     if (!m->eager && (st = build_graph(m))) { (void)hipFree(m->mem); delete m; return st; }
     if (max_T > 0 && (st = train_create(m))) {
         if (m->exec) (void)hipGraphExecDestroy(m->exec);

@@ -5,15 +5,15 @@
 //   dX = dY W    (NN) — backward_input_pretrans, pt_train.c:442-453
 //   Y  = X W^T   (NT) — the batched form of the training forward's matvecs
 //
-// Block tile 64x64, K step 16, 256 threads = 4 waves in a 2x2 grid, each
+// Block tile 64x64, K step 32, 256 threads = 4 waves in a 2x2 grid, each
 // wave a 32x32 sub-tile of 2x2 MFMA 16x16 blocks.  Tiles are staged in LDS
 // k-major (As[k][m], Bs[k][n]) so every MFMA operand read is 16 consecutive
 // floats; the next K tile is fetched into registers while the current one
 // feeds the matrix cores.  Operand layout of the 16x16x4 f32 MFMA (CDNA3/4):
 // lane l supplies A[l%16][l/16] and B[l/16][l%16]; result register r of lane
 // l is C[4*(l/16)+r][l%16].
-// Small-M*N shapes with long K split K over blockIdx.z into a workspace and
-// reduce in split order afterwards (deterministic, no atomics).
+// Grids smaller than the CU count split K over blockIdx.z into a workspace
+// and reduce in split order afterwards (deterministic, no atomics).
 #include "ptmi_internal.h"
 
 #include <algorithm>
@@ -24,7 +24,8 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 64, BN = 64, BK = 16;
+constexpr int BM = 64, BN = 64, BK = 32;
+constexpr int LDP = BM + 4;        // LDS row pitch (floats)
 
 struct GemmArgs {
     const float *A; long lda;
@@ -37,78 +38,69 @@ struct GemmArgs {
     bool a_vec, b_vec;     // 16-byte aligned rows: float4 global loads
 };
 
-// A(m, k): AT ? A[k*lda + m] : A[m*lda + k];  B(k, n): BT ? B[n*ldb + k] : B[k*ldb + n]
-template <bool AT>
-__device__ __forceinline__ void load_a(const GemmArgs &g, int m0, int k0, int kend, int tid, float (&r)[4]) {
-    if (AT) {   // rows of k, m contiguous: thread -> (k = tid/16, m = 4*(tid%16)+c)
-        const int k = k0 + tid / 16, m = m0 + 4 * (tid % 16);
+// One operand tile (64 rows of the M or N side x 32 k) per K step; each of
+// the 256 threads moves 8 floats as two float4 (or 8 predicated scalars at
+// ragged edges).  KMAJOR: the operand is stored with k as the row index
+// (A^T for TN, B for NN/TN); otherwise k is the contiguous index.
+//   KMAJOR:  thread -> (k = tid/8,  idx = 8*(tid%8) + c)
+//   !KMAJOR: thread -> (idx = tid/4, k = 8*(tid%4) + c)
+template <bool KMAJOR>
+__device__ __forceinline__ void load_tile(const float *P, long ld, int idx_lim, int i0, int k0, int kend, bool vec,
+                                          int tid, float (&r)[8]) {
+    if (KMAJOR) {
+        const int k = k0 + tid / 8, i = i0 + 8 * (tid % 8);
         const bool kin = k < kend;
-        const float *p = g.A + (long)min(k, kend - 1) * g.lda;
-        if (g.a_vec && m + 3 < g.M) {
-            float4 v = *reinterpret_cast<const float4 *>(p + m);
-            r[0] = kin ? v.x : 0.f; r[1] = kin ? v.y : 0.f; r[2] = kin ? v.z : 0.f; r[3] = kin ? v.w : 0.f;
+        const float *p = P + (long)min(k, kend - 1) * ld;
+        if (vec && i + 7 < idx_lim) {
+            const float4 v0 = *reinterpret_cast<const float4 *>(p + i);
+            const float4 v1 = *reinterpret_cast<const float4 *>(p + i + 4);
+            r[0] = v0.x; r[1] = v0.y; r[2] = v0.z; r[3] = v0.w;
+            r[4] = v1.x; r[5] = v1.y; r[6] = v1.z; r[7] = v1.w;
+            if (!kin) {
+#pragma unroll
+                for (int c = 0; c < 8; c++) r[c] = 0.f;
+            }
         } else {
 #pragma unroll
-            for (int c = 0; c < 4; c++) r[c] = (kin && m + c < g.M) ? p[m + c] : 0.f;
+            for (int c = 0; c < 8; c++) r[c] = (kin && i + c < idx_lim) ? p[i + c] : 0.f;
         }
-    } else {    // rows of m, k contiguous: thread -> (m = tid/4, k = 4*(tid%4)+c)
-        const int m = m0 + tid / 4, k = k0 + 4 * (tid % 4);
-        const bool min_ = m < g.M;
-        const float *p = g.A + (long)min(m, g.M - 1) * g.lda;
-        if (g.a_vec && k + 3 < kend) {
-            float4 v = *reinterpret_cast<const float4 *>(p + k);
-            r[0] = min_ ? v.x : 0.f; r[1] = min_ ? v.y : 0.f; r[2] = min_ ? v.z : 0.f; r[3] = min_ ? v.w : 0.f;
+    } else {
+        const int i = i0 + tid / 4, k = k0 + 8 * (tid % 4);
+        const bool iin = i < idx_lim;
+        const float *p = P + (long)min(i, idx_lim - 1) * ld;
+        if (vec && k + 7 < kend) {
+            const float4 v0 = *reinterpret_cast<const float4 *>(p + k);
+            const float4 v1 = *reinterpret_cast<const float4 *>(p + k + 4);
+            r[0] = v0.x; r[1] = v0.y; r[2] = v0.z; r[3] = v0.w;
+            r[4] = v1.x; r[5] = v1.y; r[6] = v1.z; r[7] = v1.w;
+            if (!iin) {
+#pragma unroll
+                for (int c = 0; c < 8; c++) r[c] = 0.f;
+            }
         } else {
 #pragma unroll
-            for (int c = 0; c < 4; c++) r[c] = (min_ && k + c < kend) ? p[k + c] : 0.f;
+            for (int c = 0; c < 8; c++) r[c] = (iin && k + c < kend) ? p[k + c] : 0.f;
         }
     }
 }
 
-template <bool BT>
-__device__ __forceinline__ void load_b(const GemmArgs &g, int n0, int k0, int kend, int tid, float (&r)[4]) {
-    if (!BT) {  // rows of k, n contiguous
-        const int k = k0 + tid / 16, n = n0 + 4 * (tid % 16);
-        const bool kin = k < kend;
-        const float *p = g.B + (long)min(k, kend - 1) * g.ldb;
-        if (g.b_vec && n + 3 < g.N) {
-            float4 v = *reinterpret_cast<const float4 *>(p + n);
-            r[0] = kin ? v.x : 0.f; r[1] = kin ? v.y : 0.f; r[2] = kin ? v.z : 0.f; r[3] = kin ? v.w : 0.f;
-        } else {
+template <bool KMAJOR>
+__device__ __forceinline__ void store_tile(float (*S)[LDP], int tid, const float (&r)[8]) {
+    if (KMAJOR) {
+        const int k = tid / 8, i = 8 * (tid % 8);
 #pragma unroll
-            for (int c = 0; c < 4; c++) r[c] = (kin && n + c < g.N) ? p[n + c] : 0.f;
-        }
-    } else {    // rows of n, k contiguous
-        const int n = n0 + tid / 4, k = k0 + 4 * (tid % 4);
-        const bool nin = n < g.N;
-        const float *p = g.B + (long)min(n, g.N - 1) * g.ldb;
-        if (g.b_vec && k + 3 < kend) {
-            float4 v = *reinterpret_cast<const float4 *>(p + k);
-            r[0] = nin ? v.x : 0.f; r[1] = nin ? v.y : 0.f; r[2] = nin ? v.z : 0.f; r[3] = nin ? v.w : 0.f;
-        } else {
+        for (int c = 0; c < 8; c++) S[k][i + c] = r[c];
+    } else {
+        const int i = tid / 4, k = 8 * (tid % 4);
 #pragma unroll
-            for (int c = 0; c < 4; c++) r[c] = (nin && k + c < kend) ? p[k + c] : 0.f;
-        }
-    }
-}
-
-template <bool KMAJOR_ROWS>
-__device__ __forceinline__ void store_tile(float (*S)[BM + 4], int tid, const float (&r)[4]) {
-    if (KMAJOR_ROWS) {          // thread holds (k = tid/16, idx = 4*(tid%16)+c)
-        const int k = tid / 16, i = 4 * (tid % 16);
-#pragma unroll
-        for (int c = 0; c < 4; c++) S[k][i + c] = r[c];
-    } else {                    // thread holds (idx = tid/4, k = 4*(tid%4)+c)
-        const int i = tid / 4, k = 4 * (tid % 4);
-#pragma unroll
-        for (int c = 0; c < 4; c++) S[k + c][i] = r[c];
+        for (int c = 0; c < 8; c++) S[k + c][i] = r[c];
     }
 }
 
 template <bool AT, bool BT>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
-    __shared__ float As[2][BK][BM + 4];
-    __shared__ float Bs[2][BK][BN + 4];
+    __shared__ float As[2][BK][LDP];
+    __shared__ float Bs[2][BK][LDP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int li = lane & 15, lk = lane >> 4;
@@ -122,10 +114,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    float ra[4], rb[4];
+    float ra[8], rb[8];
     if (kb < kend) {
-        load_a<AT>(g, m0, kb, kend, tid, ra);
-        load_b<BT>(g, n0, kb, kend, tid, rb);
+        load_tile<AT>(g.A, g.lda, g.M, m0, kb, kend, g.a_vec, tid, ra);
+        load_tile<!BT>(g.B, g.ldb, g.N, n0, kb, kend, g.b_vec, tid, rb);
         store_tile<AT>(As[0], tid, ra);
         store_tile<!BT>(Bs[0], tid, rb);
     }
@@ -134,8 +126,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     for (int k0 = kb; k0 < kend; k0 += BK) {
         const bool more = k0 + BK < kend;
         if (more) {                                  // next tile -> registers
-            load_a<AT>(g, m0, k0 + BK, kend, tid, ra);
-            load_b<BT>(g, n0, k0 + BK, kend, tid, rb);
+            load_tile<AT>(g.A, g.lda, g.M, m0, k0 + BK, kend, g.a_vec, tid, ra);
+            load_tile<!BT>(g.B, g.ldb, g.N, n0, k0 + BK, kend, g.b_vec, tid, rb);
         }
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 4) {
@@ -213,9 +205,12 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
     g.b_vec = al16(B) && ldb % 4 == 0;
     const int gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM;
     const long blocks = (long)gx * gy;
+    // Split K when the tile grid leaves CUs idle: aim for >= 1024 blocks (four
+    // per CU, so one block's load latency hides behind another's MFMAs),
+    // keeping at least two K steps per split.
     int splits = 1;
-    if (blocks < 256 && K >= 4 * 256) {
-        splits = (int)std::min<long>((512 + blocks - 1) / blocks, K / 256);
+    if (blocks < 1024 && K >= 4 * BK) {
+        splits = (int)std::min<long>((1024 + blocks - 1) / blocks, K / (2 * BK));
         while (splits > 1 && (size_t)splits * M * N > ws_floats) splits--;
     }
     g.k_per_split = ((K + splits - 1) / splits + BK - 1) / BK * BK;

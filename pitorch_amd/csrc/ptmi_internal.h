@@ -144,8 +144,36 @@ __device__ __forceinline__ float group_max(float v) {
 }
 
 // ── matvec launch description ───────────────────────────────────────────
-enum Prologue { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_EMBED_RMSNORM = 2 };
+enum Prologue { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_EMBED_RMSNORM = 2, PRO_ATTN_COMBINE = 3 };
+constexpr int kMaxCombineDim = 4096;   // PRO_ATTN_COMBINE: x staged in LDS
+constexpr int kMaxCombineHeads = 64;
+constexpr int kMaxAttnChunks = 8;      // attention chunks per head
 enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_QKV_ROPE = 2, EPI_SWIGLU = 3 };
+
+// Prefetch of a later stage's weights into L2, XCD by XCD: the rows that
+// blocks on XCD x will read in the consumer kernel (its row stripe x) are
+// loaded by extra blocks of the producer kernel that run on XCD x.
+// Workgroup b runs on XCD b % 8 (round-robin dispatch).
+struct PrefetchDesc {
+    const float *base;     // consumer weights, rows of row_floats floats
+    long row_floats;
+    int rows;              // consumer rows
+    int stripe;            // consumer rows per XCD stripe
+    int blocks;            // prefetch blocks (multiple of 8), 0 = none
+    int first_block;       // blockIdx.x of the first prefetch block
+    float *sink;           // never written in practice; keeps loads live
+};
+
+// Rows of one matvec per XCD stripe and per wave (shared by the launcher
+// and by producers that prefetch for it).
+struct MatvecGeom {
+    int lpr, it, exact, step, stripe, rows_per_wave, blocks_per_xcd;
+};
+bool matvec_geometry(int rows, int n, MatvecGeom *g);
+
+// Describe a prefetch of consumer matvec (W rows x ld) for a producer
+// whose own blocks end at `first_block`.
+PrefetchDesc prefetch_for(const float *W, long ld, int rows, int n, int first_block, float *sink);
 
 struct MatvecParams {
     const float *W;        // row r starts at W + r*ld
@@ -161,8 +189,42 @@ struct MatvecParams {
     const int *pos;        // EPI_QKV_ROPE: decode position (device scalar)
     int q_rows, kv_rows, head_dim;
     float *k_cache, *v_cache;   // this layer's [seq_len, kv_rows] caches
+    // PRO_ATTN_COMBINE: x = softmax-combined attention partials of all heads
+    const float *att_o;    // [heads][chunks][head_dim] unnormalised sums
+    const float *att_ml;   // [heads][chunks][2] (chunk max, chunk sum)
+    int att_chunks, att_chunk, att_heads;
     int rows_per_wave;     // filled by the launcher
+    int stripe, blocks_per_xcd;
+    PrefetchDesc pf;       // optional L2 prefetch for the next stage
 };
+
+// Prefetch blocks' body (any kernel): loads its share of stripe
+// (blockIdx.x % 8) of the consumer weights and discards it.
+__device__ __forceinline__ void run_prefetch(const PrefetchDesc &pf) {
+    const int q = (int)blockIdx.x - pf.first_block;
+    const int xcd = (int)(blockIdx.x & 7), rank = q >> 3, per_xcd = pf.blocks >> 3;
+    const long r0 = (long)xcd * pf.stripe;
+    const long r1 = r0 + pf.stripe < (long)pf.rows ? r0 + pf.stripe : (long)pf.rows;
+    if (r0 >= r1) return;
+    const long f0 = r0 * pf.row_floats / 4, f1 = r1 * pf.row_floats / 4;
+    const long chunk = (f1 - f0 + per_xcd - 1) / per_xcd;
+    const long a = f0 + rank * chunk;
+    const long e = a + chunk < f1 ? a + chunk : f1;
+    const float4 *src = reinterpret_cast<const float4 *>(pf.base);
+    float acc = 0.0f;
+    const long step = (long)blockDim.x * 8;
+    for (long i = a + threadIdx.x; i < e; i += step) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const long j = i + (long)u * blockDim.x;
+            v[u] = src[j < e ? j : e - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc += v[u].x;
+    }
+    if (acc == -1.2345e-37f) pf.sink[0] = acc;
+}
 
 // Launch y = epilogue(W . prologue(x)); validates shapes, picks a kernel.
 int launch_matvec(MatvecParams p, hipStream_t s);

@@ -83,6 +83,7 @@ __device__ __forceinline__ void run_epilogue(const MatvecParams &p, const float 
 template <int LPR, int IT, bool EXACT, int PRO, int EPI>
 __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
     constexpr int RPP = 64 / LPR;                  // rows per pass
+    constexpr bool kNorm = PRO == PRO_RMSNORM || PRO == PRO_EMBED_RMSNORM;
     __shared__ float ybuf[kWaves][kMaxRowsPerWave];
 
     const int lane = threadIdx.x & 63;
@@ -90,11 +91,18 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
     const int slot = lane / LPR;
     const int sub = lane % LPR;
     const int n4 = p.n >> 2;
-    const long wave_id = (long)blockIdx.x * kWaves + wave;
-    const long row0l = wave_id * p.rows_per_wave;
-    const bool active = row0l < p.rows;
+    // Blocks past the compute grid prefetch the next stage's weights.
+    if ((int)blockIdx.x >= 8 * p.blocks_per_xcd) {
+        run_prefetch(p.pf);
+        return;
+    }
+    // XCD-striped rows: block b (on XCD b%8) works inside stripe b%8.
+    const long s0 = (long)(blockIdx.x & 7) * p.stripe;
+    const long s1 = s0 + p.stripe < (long)p.rows ? s0 + p.stripe : (long)p.rows;
+    const long row0l = s0 + ((long)(blockIdx.x >> 3) * kWaves + wave) * p.rows_per_wave;
+    const bool active = row0l < s1;
     const int row0 = active ? (int)row0l : 0;
-    const int nrows = active ? min(p.rows_per_wave, p.rows - row0) : 0;
+    const int nrows = active ? (int)min((long)p.rows_per_wave, s1 - row0l) : 0;
 
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
     // ---- main loop: two passes (2*RPP rows) per iteration ----
@@ -128,14 +136,59 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
     const float *xs = p.x;
     if constexpr (PRO == PRO_EMBED_RMSNORM) xs = p.x + (long)(*p.token) * p.n;
     int pos = 0;
-    if constexpr (EPI == EPI_QKV_ROPE) pos = *p.pos;
+    if constexpr (EPI == EPI_QKV_ROPE || PRO == PRO_ATTN_COMBINE) pos = *p.pos;
+    if constexpr (PRO == PRO_ATTN_COMBINE) {
+        // x[i] = sum_c w[h][c] o_c[i], w[h][c] = e^(m_c - M) / sum_c' l_c' e^(m_c' - M)
+        // over the active chunks of head h = i/hd, once per workgroup into
+        // LDS.  Both phases issue all their loads before using any.
+        __shared__ float xcomb[kMaxCombineDim];
+        __shared__ float wts[kMaxCombineHeads][kMaxAttnChunks];
+        const int hd = p.n / p.att_heads;
+        const int active = pos / p.att_chunk + 1;
+        for (int h = threadIdx.x; h < p.att_heads; h += kWaves * 64) {
+            const float *ml = p.att_ml + 2L * h * p.att_chunks;
+            float mv[kMaxAttnChunks], lv[kMaxAttnChunks];
+#pragma unroll
+            for (int c = 0; c < kMaxAttnChunks; c++) {
+                const int cc = min(c, active - 1);
+                mv[c] = ml[2 * cc];
+                lv[c] = ml[2 * cc + 1];
+            }
+            float M = mv[0];
+#pragma unroll
+            for (int c = 1; c < kMaxAttnChunks; c++) if (c < active) M = fmaxf(M, mv[c]);
+            float f[kMaxAttnChunks], L = 0.0f;
+#pragma unroll
+            for (int c = 0; c < kMaxAttnChunks; c++) {
+                f[c] = c < active ? d_expf(mv[c] - M) : 0.0f;
+                L = fmaf(lv[c], f[c], L);
+            }
+            const float inv = 1.0f / L;
+#pragma unroll
+            for (int c = 0; c < kMaxAttnChunks; c++) wts[h][c] = f[c] * inv;
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < p.n; i += kWaves * 64) {
+            const int h = i / hd, d = i - h * hd;
+            const float *o = p.att_o + (long)h * p.att_chunks * hd + d;
+            float ov[kMaxAttnChunks];
+#pragma unroll
+            for (int c = 0; c < kMaxAttnChunks; c++) ov[c] = o[(long)min(c, active - 1) * hd];
+            float v = 0.0f;
+#pragma unroll
+            for (int c = 0; c < kMaxAttnChunks; c++) v = fmaf(ov[c], wts[h][c], v);   // w = 0 past active
+            xcomb[i] = v;
+        }
+        __syncthreads();
+        xs = xcomb;
+    }
     float4 xr[IT], nw[IT];
 #pragma unroll
     for (int it = 0; it < IT; it++) {
         const int c = sub + it * LPR;
         const int cc = EXACT ? c : min(c, n4 - 1);
         xr[it] = reinterpret_cast<const float4 *>(xs)[cc];
-        if constexpr (PRO != PRO_NONE) nw[it] = reinterpret_cast<const float4 *>(p.norm_w)[cc];
+        if constexpr (kNorm) nw[it] = reinterpret_cast<const float4 *>(p.norm_w)[cc];
         if (!EXACT && c >= n4) xr[it] = zero4;
     }
     if (PRO == PRO_EMBED_RMSNORM && blockIdx.x == 0 && wave == 0 && slot == 0) {
@@ -145,7 +198,7 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
             if (c < n4) reinterpret_cast<float4 *>(p.x_out)[c] = xr[it];
         }
     }
-    if constexpr (PRO != PRO_NONE) {              // rmsnorm, pt_ops.c:5-12
+    if constexpr (kNorm) {                        // rmsnorm, pt_ops.c:5-12
         float ss = 0.0f;
 #pragma unroll
         for (int it = 0; it < IT; it++)
@@ -259,6 +312,7 @@ KernelFn pick_role(int it, int pro, int epi) {
     if (pro == PRO_RMSNORM && epi == EPI_QKV_ROPE) return pick_it<LPR, EXACT, PRO_RMSNORM, EPI_QKV_ROPE>(it);
     if (pro == PRO_EMBED_RMSNORM && epi == EPI_QKV_ROPE)
         return pick_it<LPR, EXACT, PRO_EMBED_RMSNORM, EPI_QKV_ROPE>(it);
+    if (pro == PRO_ATTN_COMBINE && epi == EPI_RESIDUAL) return pick_it<LPR, EXACT, PRO_ATTN_COMBINE, EPI_RESIDUAL>(it);
     return nullptr;
 }
 
@@ -271,16 +325,59 @@ inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
 
-// Host-side launcher.  Chooses lanes-per-row so that each lane holds at
-// most 9 float4 of x, and rows-per-wave so that the grid has ~2048 waves
-// (8 per CU) when the matrix is large enough.
+// Lanes-per-row so that each lane holds at most 9 float4 of x; rows split
+// into 8 XCD stripes (multiples of the row-pair step); rows-per-wave so
+// that each XCD runs ~256 waves (8 per CU) when the matrix is big enough.
+bool matvec_geometry(int rows, int n, MatvecGeom *g) {
+    const int n4 = n / 4;
+    if (n % 4 || n4 > 64 * 9 || rows <= 0) return false;
+    g->lpr = n4 <= 8 * 9 ? 8 : n4 <= 16 * 9 ? 16 : n4 <= 32 * 9 ? 32 : 64;
+    g->it = (n4 + g->lpr - 1) / g->lpr;
+    g->exact = n4 == g->lpr * g->it;
+    g->step = 2 * (64 / g->lpr);
+    const int per = (rows + 7) / 8;
+    g->stripe = (per + g->step - 1) / g->step * g->step;
+    int rpw = (g->stripe + 255) / 256;
+    rpw = (rpw + g->step - 1) / g->step * g->step;
+    rpw = std::max(rpw, g->step);
+    rpw = std::min(rpw, kMaxRowsPerWave);
+    g->rows_per_wave = rpw;
+    const int waves = (g->stripe + rpw - 1) / rpw;
+    g->blocks_per_xcd = (waves + kWaves - 1) / kWaves;
+    return true;
+}
+
+PrefetchDesc prefetch_for(const float *W, long ld, int rows, int n, int first_block, float *sink) {
+    PrefetchDesc pf = {};
+    MatvecGeom g;
+    if (!W || ld % 4 || !matvec_geometry(rows, n, &g)) return pf;
+    pf.base = W; pf.row_floats = ld; pf.rows = rows; pf.stripe = g.stripe;
+    // ~64 KB per prefetch block: two rounds of eight 16-byte loads per lane
+    const long bytes_per_xcd = (long)g.stripe * ld * 4;
+    const int per_xcd = (int)std::max<long>(1, std::min<long>(64, (bytes_per_xcd + 65535) / 65536));
+    pf.blocks = 8 * per_xcd;
+    pf.first_block = first_block;
+    pf.sink = sink;
+    return pf;
+}
+
+// Host-side launcher: validates shapes and picks the kernel.
 int launch_matvec(MatvecParams p, hipStream_t s) {
     if (p.rows <= 0 || p.n <= 0) return set_error(PTMI_ERR_ARG, "matvec: rows=%d n=%d", p.rows, p.n);
     if (!p.W || !p.x || !p.y) return set_error(PTMI_ERR_ARG, "matvec: null pointer");
     if (p.ld < p.n) return set_error(PTMI_ERR_ARG, "matvec: ld=%ld < n=%d", p.ld, p.n);
     const int n4 = p.n / 4;
+    if (p.pro == PRO_ATTN_COMBINE &&
+        (!p.att_o || !p.att_ml || !p.pos || p.att_heads <= 0 || p.att_heads > kMaxCombineHeads ||
+         p.n % p.att_heads || p.n > kMaxCombineDim || p.att_chunk <= 0 || p.att_chunks <= 0 ||
+         p.att_chunks > kMaxAttnChunks))
+        return set_error(PTMI_ERR_ARG, "matvec: bad attention-combine description");
+    const bool norm = p.pro == PRO_RMSNORM || p.pro == PRO_EMBED_RMSNORM;
+    if (norm && !p.norm_w) return set_error(PTMI_ERR_ARG, "matvec: RMSNorm prologue without weights");
+    if (p.pro == PRO_EMBED_RMSNORM && (!p.token || !p.x_out))
+        return set_error(PTMI_ERR_ARG, "matvec: embedding prologue without token/x_out");
     const bool vec_ok = (p.n % 4 == 0) && (p.ld % 4 == 0) && aligned16(p.W) && aligned16(p.x) &&
-                        (p.pro == PRO_NONE || aligned16(p.norm_w)) &&
+                        (!norm || aligned16(p.norm_w)) &&
                         (p.pro != PRO_EMBED_RMSNORM || aligned16(p.x_out));
     const bool fused = p.pro != PRO_NONE || p.epi == EPI_QKV_ROPE || p.epi == EPI_SWIGLU;
     if (p.epi == EPI_QKV_ROPE &&
@@ -291,23 +388,26 @@ int launch_matvec(MatvecParams p, hipStream_t s) {
 
     KernelFn fn = nullptr;
     int rpp = 1;
-    if (vec_ok && n4 <= 64 * 9) {
-        int lpr, it;
-        if (n4 <= 8 * 9) lpr = 8;
-        else if (n4 <= 16 * 9) lpr = 16;
-        else if (n4 <= 32 * 9) lpr = 32;
-        else lpr = 64;
-        it = (n4 + lpr - 1) / lpr;
-        const bool exact = n4 == lpr * it;
-        switch (lpr) {
-        case 8: fn = pick<8>(it, exact, p.pro, p.epi); break;
-        case 16: fn = pick<16>(it, exact, p.pro, p.epi); break;
-        case 32: fn = pick<32>(it, exact, p.pro, p.epi); break;
-        default: fn = pick<64>(it, exact, p.pro, p.epi); break;
+    MatvecGeom geo;
+    if (vec_ok && matvec_geometry(p.rows, p.n, &geo)) {
+        switch (geo.lpr) {
+        case 8: fn = pick<8>(geo.it, geo.exact, p.pro, p.epi); break;
+        case 16: fn = pick<16>(geo.it, geo.exact, p.pro, p.epi); break;
+        case 32: fn = pick<32>(geo.it, geo.exact, p.pro, p.epi); break;
+        default: fn = pick<64>(geo.it, geo.exact, p.pro, p.epi); break;
         }
         if (!fn) return set_error(PTMI_ERR_ARG, "matvec: unsupported prologue/epilogue pair %d/%d", p.pro, p.epi);
-        rpp = 64 / lpr;
+        p.stripe = geo.stripe;
+        p.rows_per_wave = geo.rows_per_wave;
+        p.blocks_per_xcd = geo.blocks_per_xcd;
+        const int compute_blocks = 8 * geo.blocks_per_xcd;
+        if (p.pf.blocks && p.pf.first_block != compute_blocks)
+            return set_error(PTMI_ERR_ARG, "matvec: prefetch descriptor built for another grid");
+        hipLaunchKernelGGL(fn, dim3((unsigned)(compute_blocks + p.pf.blocks)), dim3(kWaves * 64), 0, s, p);
+        PTMI_HIP(hipGetLastError());
+        return PTMI_OK;
     } else if (vec_ok) {
+        if (p.pf.blocks) return set_error(PTMI_ERR_ARG, "matvec: prefetch needs the register-resident kernel");
         if (p.pro != PRO_NONE || p.epi != EPI_STORE)
             return set_error(PTMI_ERR_ARG, "matvec: fused variants need n <= %d", 64 * 9 * 4);
         fn = k_matvec_long;

@@ -18,7 +18,7 @@ struct DecodeCtl {
 struct TrainState;   // defined by the training unit
 
 constexpr int kMaxHeadDim = 128;
-constexpr int kMaxSeqLen = 16384;   // attention scores of one head fit in LDS
+constexpr int kMaxSeqLen = 4096;    // 8 attention chunks of <= 512 positions
 
 }  // namespace ptmi
 
@@ -31,11 +31,15 @@ struct ptmi_model {
     float *mem = nullptr;
     float *x = nullptr, *xb = nullptr, *q = nullptr, *hb = nullptr, *logits = nullptr;
     float *kc = nullptr, *vc = nullptr;
+    float *part_o = nullptr, *part_ml = nullptr;   // attention chunk partials
+    int attn_chunk = 0, attn_chunks = 0;
     ptmi::DecodeCtl *ctl = nullptr;
     int *prompt = nullptr, *out_tokens = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool eager = false;                  // PTMI_DECODE_EAGER=1: no graph
+    bool prefetch = true;                // PTMI_NO_PREFETCH=1: no L2 prefetch blocks
+    float *sink = nullptr;               // prefetch load sink
     ptmi::TrainState *train = nullptr;
 };
 
