@@ -27,16 +27,61 @@ def matvec_bytes(d, n):
     return 4 * (d * n + n + d)
 
 
-def role_bytes(cfg):
-    D, H, _, _, _, V, _ = cfg
+def role_bytes(cfg, positions):
+    """Algorithmic bytes per launch of each decode kernel, averaged over the
+    given positions (attention reads K and V rows 0..pos of every head)."""
+    D, H, _, NH, _, V, _ = cfg
     KV = D
+    mean_ctx = sum(p + 1 for p in positions) / len(positions)
     return {
         "qkv": matvec_bytes(D + 2 * KV, D),
+        "attention": int(4 * (2 * KV * mean_ctx + D)),
         "wo": matvec_bytes(D, D),
         "w13": matvec_bytes(2 * H, D),
         "w2": matvec_bytes(D, H),
         "classifier": matvec_bytes(V, D),
+        "argmax": 4 * V,
     }
+
+
+def decode_bytes_per_token(cfg, positions):
+    """Weights + average KV traffic per token (4*P_proj + 8*L*D*(p+1) + 8*L*D)."""
+    D, H, L, _, _, V, _ = cfg
+    proj = L * (4 * D * D + 3 * H * D) + V * D
+    kv = sum(8 * L * D * (p + 1) + 8 * L * D for p in positions) / len(positions)
+    return 4 * proj + kv
+
+
+SWEEP = [(288, 288), (768, 288), (288, 768), (32000, 288), (2048, 768), (768, 2048), (32000, 768),
+         (2304, 768), (4096, 768)]
+
+
+def matvec_sweep(pa, footprint_mb=1536, reps_max=2048):
+    """Config 2: standalone y = W x at each shape, W rotated through a
+    footprint well above the 256 MB MALL so every launch reads HBM; HIP
+    events around the whole batch of launches on the library stream."""
+    from pitorch_amd._hip import DeviceArray, Event
+    L = pa.load_ptmi()
+    stream = L.ptmi_stream()
+    big = DeviceArray(footprint_mb * (1 << 20) // 4)
+    x = DeviceArray.from_host(pa.seed_uniform(3, 2048))
+    y = DeviceArray(32000)
+    out = []
+    for d, n in SWEEP:
+        stride = (d * n + 63) // 64 * 64
+        copies = max(1, min(big.n // stride, reps_max))
+        pa._ffi.check(L.ptmi_matvec_dev(big.ptr, n, x.ptr, y.ptr, d, n, None))
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        for i in range(copies):
+            pa._ffi.check(L.ptmi_matvec_dev(big.ptr + 4 * i * stride, n, x.ptr, y.ptr, d, n, None))
+        e1.record(stream)
+        us = e0.elapsed_ms(e1) * 1e3 / copies
+        gbs = matvec_bytes(d, n) / (us * 1e-6) / 1e9
+        out.append({"d": d, "n": n, "us": round(us, 2), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    for a in (big, x, y):
+        a.free()
+    return out
 
 
 def cpu_model():
@@ -161,7 +206,7 @@ def main():
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--config", default="stories110M")
-    ap.add_argument("--profile-steps", type=int, default=64)
+    ap.add_argument("--profile-steps", type=int, default=1024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-train", action="store_true", help="skip the training-GEMM leg")
     args = ap.parse_args()
@@ -207,33 +252,35 @@ def main():
     print(f"[bench] decode {args.steps} steps in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s", file=sys.stderr,
           flush=True)
 
-    # per-role kernel timing (HIP events on the library stream, eager steps)
+    # per-kernel durations: eager steps over the same positions, each launch
+    # bracketed by HIP events that the command processor stamps at the
+    # kernel's own start and end (hipExtLaunchKernelGGL), library stream
     m.reset_kv()
-    prof = m.profile(int(prompt[0]), min(args.profile_steps, S))
-    rb = role_bytes(cfg)
+    n_prof = min(args.profile_steps, S)
+    prof = m.profile(int(prompt[0]), n_prof)
+    rb = role_bytes(cfg, range(n_prof))
     breakdown = {}
     for role, (ms, cnt) in prof.items():
         if cnt == 0:
             continue
         avg_us = ms * 1e3 / cnt
-        e = {"avg_us": round(avg_us, 3), "launches": cnt, "total_ms": round(ms, 4)}
-        if role in rb:
-            e["bytes_per_launch"] = rb[role]
-            e["GBps"] = round(rb[role] / (avg_us * 1e-6) / 1e9, 1)
+        e = {"avg_us": round(avg_us, 3), "launches": cnt, "total_ms": round(ms, 4),
+             "bytes_per_launch": rb[role], "GBps": round(rb[role] / (avg_us * 1e-6) / 1e9, 1)}
         breakdown[role] = e
-    mv_roles = [r for r in rb if r in breakdown]
-    dominant = max(mv_roles, key=lambda r: breakdown[r]["total_ms"])
+    dominant = max(breakdown, key=lambda r: breakdown[r]["total_ms"])
     dom = breakdown[dominant]
     achieved = dom["GBps"]
-    per_tok_bytes = sum(rb[r] * breakdown[r]["launches"] for r in mv_roles) / (args.profile_steps)
-    mv_ms = sum(breakdown[r]["total_ms"] for r in mv_roles) / args.profile_steps
-    breakdown["all_matvec"] = {"bytes_per_token": int(per_tok_bytes), "ms_per_token": round(mv_ms, 4),
-                               "GBps": round(per_tok_bytes / (mv_ms * 1e-3) / 1e9, 1)}
+    kernel_ms = sum(e["total_ms"] for e in breakdown.values()) / n_prof
     for r, e in breakdown.items():
         print(f"[bench] {r:12s} {json.dumps(e)}", file=sys.stderr, flush=True)
+    step_bytes = decode_bytes_per_token(cfg, [p % S for p in range(args.steps)])
+    step_gbs = step_bytes / (dt / args.steps) / 1e9
 
     m.close()
     del blob
+    sweep = matvec_sweep(pa)
+    for e in sweep:
+        print(f"[bench] sweep {json.dumps(e)}", file=sys.stderr, flush=True)
     calib_copy(pa)
     train = None if args.no_train else bench_train(pa)
     if train:
@@ -258,9 +305,12 @@ def main():
         "config": {"workload": f"{name}-shaped greedy decode, hipGraph per token", "model_shape": list(cfg),
                    "positions": f"0..{min(args.steps, S) - 1} (KV cache restarts every {S})",
                    "batch": 1},
-        "roofline": {"bound": "hbm", "kernel": f"matvec[{dominant}]", "achieved": achieved,
+        "roofline": {"bound": "hbm", "kernel": f"decode[{dominant}]", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": None, "bytes_per_launch": dom["bytes_per_launch"], "avg_us": dom["avg_us"]},
+        "step_roofline": {"bytes_per_token": int(step_bytes), "achieved_GBps": round(step_gbs, 1),
+                          "frac": round(step_gbs / HBM_PEAK_GBS, 4), "kernel_ms_per_token": round(kernel_ms, 4)},
+        "matvec_sweep": sweep,
         "cpu_baseline": cpu,
         "breakdown": breakdown,
         "train": train,

@@ -233,12 +233,14 @@ float host_att_scale(int head_dim) {
     return 1.0f / y;
 }
 
-// Optional per-launch HIP events (eager profiling runs only).
+// Optional per-launch HIP events (eager profiling runs only): each launch
+// gets a start/stop pair timestamped by the command processor around the
+// kernel itself (hipExtLaunchKernelGGL), i.e. the kernel's own duration.
 struct StepTimer {
     std::vector<hipEvent_t> ev;     // 2 per launch
     std::vector<int> role;
     size_t used = 0;
-    int begin(hipStream_t s, int r) {
+    int next(int r, hipEvent_t *e0, hipEvent_t *e1) {
         if (used + 2 > ev.size()) {
             hipEvent_t a, b;
             PTMI_HIP(hipEventCreate(&a));
@@ -248,11 +250,8 @@ struct StepTimer {
             role.push_back(0);
         }
         role[used / 2] = r;
-        PTMI_HIP(hipEventRecord(ev[used], s));
-        return PTMI_OK;
-    }
-    int end(hipStream_t s) {
-        PTMI_HIP(hipEventRecord(ev[used + 1], s));
+        *e0 = ev[used];
+        *e1 = ev[used + 1];
         used += 2;
         return PTMI_OK;
     }
@@ -263,9 +262,9 @@ struct StepTimer {
 
 #define TIMED(role_, launch_)                                   \
     do {                                                        \
-        if (tm && (st = tm->begin(s, role_))) return st;        \
+        hipEvent_t e0 = nullptr, e1 = nullptr;                  \
+        if (tm && (st = tm->next(role_, &e0, &e1))) return st;  \
         launch_;                                                \
-        if (tm && (st = tm->end(s))) return st;                 \
     } while (0)
 
 // Producer-side prefetch of consumer matvec weights W[rows, n] (ld = n).
@@ -301,7 +300,7 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         p.y = m->q; p.epi = EPI_QKV_ROPE; p.pos = &m->ctl->pos;
         p.q_rows = (int)D; p.kv_rows = (int)KV; p.head_dim = c.head_dim; p.k_cache = kc; p.v_cache = vc;
         p.pf = pf_matvec(m, r->wo + (long)l * D * D, (int)D, (int)D, matvec_compute_blocks(QR, (int)D));
-        TIMED(0, if ((st = launch_matvec(p, s))) return st);
+        TIMED(0, if ((st = launch_matvec(p, s, e0, e1))) return st);
 
         AttnParams a = {};
         a.q = m->q; a.kc = kc; a.vc = vc; a.part_o = m->part_o; a.part_ml = m->part_ml; a.ctl = m->ctl;
@@ -313,7 +312,7 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         const int attn_blocks = c.n_heads * m->attn_chunks;
         a.pf = pf_matvec(m, r->w13 + (long)l * 2 * H * D, (int)(2 * H), (int)D, attn_blocks);
         a.pf.first_block = attn_blocks;
-        TIMED(1, hipLaunchKernelGGL(attn, dim3(attn_blocks + a.pf.blocks), dim3(kAttnWaves * 64), 0, s, a));
+        TIMED(1, launch_k(attn, dim3(attn_blocks + a.pf.blocks), dim3(kAttnWaves * 64), 0, s, e0, e1, a));
         PTMI_HIP(hipGetLastError());
 
         p = MatvecParams{};
@@ -322,7 +321,7 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         p.pos = &m->ctl->pos; p.att_o = m->part_o; p.att_ml = m->part_ml;
         p.att_chunks = m->attn_chunks; p.att_chunk = m->attn_chunk; p.att_heads = c.n_heads;
         p.pf = pf_matvec(m, r->w2 + (long)l * D * H, (int)D, (int)H, matvec_compute_blocks((int)D, (int)D));
-        TIMED(2, if ((st = launch_matvec(p, s))) return st);
+        TIMED(2, if ((st = launch_matvec(p, s, e0, e1))) return st);
 
         p = MatvecParams{};
         p.W = r->w13 + (long)l * 2 * H * D; p.ld = D; p.rows = (int)(2 * H); p.n = (int)D;
@@ -330,21 +329,21 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         p.y = m->hb; p.epi = EPI_SWIGLU;
         if (l + 1 < c.n_layers)
             p.pf = pf_matvec(m, r->wqkv + (long)(l + 1) * QR * D, QR, (int)D, matvec_compute_blocks((int)(2 * H), (int)D));
-        TIMED(3, if ((st = launch_matvec(p, s))) return st);
+        TIMED(3, if ((st = launch_matvec(p, s, e0, e1))) return st);
 
         p = MatvecParams{};
         p.W = r->w2 + (long)l * D * H; p.ld = H; p.rows = (int)D; p.n = (int)H;
         p.x = m->hb; p.y = m->x; p.pro = PRO_NONE; p.epi = EPI_RESIDUAL;
-        TIMED(4, if ((st = launch_matvec(p, s))) return st);
+        TIMED(4, if ((st = launch_matvec(p, s, e0, e1))) return st);
     }
     MatvecParams p = {};
     p.W = r->wcls; p.ld = D; p.rows = c.vocab; p.n = (int)D;
     p.x = m->x; p.pro = PRO_RMSNORM; p.norm_w = r->rms_final; p.y = m->logits; p.epi = EPI_STORE;
     p.pf = pf_matvec(m, r->wqkv, QR, (int)D, matvec_compute_blocks(c.vocab, (int)D));
-    TIMED(5, if ((st = launch_matvec(p, s))) return st);
+    TIMED(5, if ((st = launch_matvec(p, s, e0, e1))) return st);
     const PrefetchDesc none = {};
-    TIMED(6, hipLaunchKernelGGL(k_argmax_step, dim3(1), dim3(1024), 0, s, m->logits, c.vocab, m->ctl,
-                                m->prompt, m->out_tokens, none));
+    TIMED(6, launch_k(k_argmax_step, dim3(1), dim3(1024), 0, s, e0, e1, m->logits, c.vocab, m->ctl, m->prompt,
+                      m->out_tokens, none));
     PTMI_HIP(hipGetLastError());
     return PTMI_OK;
 }

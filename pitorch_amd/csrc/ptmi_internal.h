@@ -5,6 +5,7 @@
 // reference's host build.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -226,8 +227,16 @@ __device__ __forceinline__ void run_prefetch(const PrefetchDesc &pf) {
     if (acc == -1.2345e-37f) pf.sink[0] = acc;
 }
 
+// Kernel launch, optionally bracketed by HIP events that the command
+// processor timestamps at the kernel's own start and end (profiling).
+template <typename F, typename... A>
+inline void launch_k(F f, dim3 g, dim3 b, size_t shmem, hipStream_t s, hipEvent_t e0, hipEvent_t e1, A... a) {
+    if (e0) hipExtLaunchKernelGGL(f, g, b, (uint32_t)shmem, s, e0, e1, 0, a...);
+    else hipLaunchKernelGGL(f, g, b, shmem, s, a...);
+}
+
 // Launch y = epilogue(W . prologue(x)); validates shapes, picks a kernel.
-int launch_matvec(MatvecParams p, hipStream_t s);
+int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 
 // C[M,N] (+)= op(A).op(B) on the matrix cores; op 0 NN, 1 TN (A stored
 // [K][M]), 2 NT (B stored [N][K]).  ws: split-K workspace (may be null).

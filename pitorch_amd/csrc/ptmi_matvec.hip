@@ -362,7 +362,7 @@ PrefetchDesc prefetch_for(const float *W, long ld, int rows, int n, int first_bl
 }
 
 // Host-side launcher: validates shapes and picks the kernel.
-int launch_matvec(MatvecParams p, hipStream_t s) {
+int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     if (p.rows <= 0 || p.n <= 0) return set_error(PTMI_ERR_ARG, "matvec: rows=%d n=%d", p.rows, p.n);
     if (!p.W || !p.x || !p.y) return set_error(PTMI_ERR_ARG, "matvec: null pointer");
     if (p.ld < p.n) return set_error(PTMI_ERR_ARG, "matvec: ld=%ld < n=%d", p.ld, p.n);
@@ -403,7 +403,7 @@ int launch_matvec(MatvecParams p, hipStream_t s) {
         const int compute_blocks = 8 * geo.blocks_per_xcd;
         if (p.pf.blocks && p.pf.first_block != compute_blocks)
             return set_error(PTMI_ERR_ARG, "matvec: prefetch descriptor built for another grid");
-        hipLaunchKernelGGL(fn, dim3((unsigned)(compute_blocks + p.pf.blocks)), dim3(kWaves * 64), 0, s, p);
+        launch_k(fn, dim3((unsigned)(compute_blocks + p.pf.blocks)), dim3(kWaves * 64), 0, s, e0, e1, p);
         PTMI_HIP(hipGetLastError());
         return PTMI_OK;
     } else if (vec_ok) {
@@ -416,7 +416,7 @@ int launch_matvec(MatvecParams p, hipStream_t s) {
         if (fused) return set_error(PTMI_ERR_ARG, "matvec: fused variants need 16-byte aligned rows, n%%4==0");
         p.rows_per_wave = 1;
         const int blocks = (p.rows + kWaves - 1) / kWaves;
-        hipLaunchKernelGGL(k_matvec_scalar, dim3(blocks), dim3(kWaves * 64), 0, s, p);
+        launch_k(k_matvec_scalar, dim3(blocks), dim3(kWaves * 64), 0, s, e0, e1, p);
         PTMI_HIP(hipGetLastError());
         return PTMI_OK;
     }
@@ -431,7 +431,7 @@ int launch_matvec(MatvecParams p, hipStream_t s) {
     p.rows_per_wave = (int)rpw;
     const long waves = (p.rows + rpw - 1) / rpw;
     const long blocks = (waves + kWaves - 1) / kWaves;
-    hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kWaves * 64), 0, s, p);
+    launch_k(fn, dim3((unsigned)blocks), dim3(kWaves * 64), 0, s, e0, e1, p);
     PTMI_HIP(hipGetLastError());
     return PTMI_OK;
 }
