@@ -64,27 +64,30 @@ __global__ __launch_bounds__(kAttnWaves * 64) void k_attn_chunk(AttnParams a) {
         return;
     }
     const int h = blockIdx.x % a.n_heads, c = blockIdx.x / a.n_heads;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int slot = lane / G, sub = lane % G;
+    const int hd = a.head_dim, hd4 = hd >> 2;
+    const bool has = sub < hd4;
+    const int sub_c = has ? sub : 0;
+    // q does not depend on the position: its load overlaps the pos fetch.
+    float4 q4 = reinterpret_cast<const float4 *>(a.q + h * hd)[sub_c];
     const int n = a.ctl->pos + 1;
     const int t0 = c * a.chunk;
     if (t0 >= n) return;                               // uniform per block
     const int t1 = min(t0 + a.chunk, n);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int slot = lane / G, sub = lane % G;
-    const int hd = a.head_dim, hd4 = hd >> 2;
     const long ko = (long)(h / a.kv_mul) * hd;
-    const bool has = sub < hd4;
-    const int sub_c = has ? sub : 0;
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 q4 = reinterpret_cast<const float4 *>(a.q + h * hd)[sub_c];
     if (!has) q4 = zero4;
+    const int cnt = t1 - t0;
+    const float4 *kbase = reinterpret_cast<const float4 *>(a.kc + ko) + sub_c;
+    const float4 *vbase = reinterpret_cast<const float4 *>(a.vc + ko) + sub_c;
+    const long row4 = a.kv_dim >> 2;                     // float4 per cache row
 
-    for (int base = t0 + wave * BATCH; base < t1; base += kAttnWaves * BATCH) {
-        float4 k4[kAttnUnroll];
+    auto load_rows = [&](const float4 *src, int base, float4 (&dst)[kAttnUnroll]) {
 #pragma unroll
-        for (int u = 0; u < kAttnUnroll; u++) {
-            const int t = min(base + u * RPI + slot, t1 - 1);
-            k4[u] = reinterpret_cast<const float4 *>(a.kc + (long)t * a.kv_dim + ko)[sub_c];
-        }
+        for (int u = 0; u < kAttnUnroll; u++) dst[u] = src[(long)min(base + u * RPI + slot, t1 - 1) * row4];
+    };
+    auto score_rows = [&](int base, const float4 (&k4)[kAttnUnroll]) {
 #pragma unroll
         for (int u = 0; u < kAttnUnroll; u++) {
             float s = has ? dot4(k4[u], q4, 0.0f) : 0.0f;
@@ -92,35 +95,32 @@ __global__ __launch_bounds__(kAttnWaves * 64) void k_attn_chunk(AttnParams a) {
             const int t = base + u * RPI + slot;
             if (sub == 0 && t < t1) sc[t - t0] = s * a.scale;
         }
-    }
-    __syncthreads();
-    const int cnt = t1 - t0;
-    float mx = -INFINITY;
-    for (int i = tid; i < cnt; i += kAttnWaves * 64) mx = fmaxf(mx, sc[i]);
-    mx = group_max<64>(mx);
-    if (lane == 0) wred[wave] = mx;
-    __syncthreads();
-    mx = wred[0];
+    };
+    // chunk softmax over sc[0..cnt): sc <- e^(s - max); returns the max,
+    // leaves each wave's partial sum in wred
+    auto softmax = [&]() {
+        __syncthreads();
+        float mx = -INFINITY;
+        for (int i = tid; i < cnt; i += kAttnWaves * 64) mx = fmaxf(mx, sc[i]);
+        mx = group_max<64>(mx);
+        if (lane == 0) wred[wave] = mx;
+        __syncthreads();
+        mx = wred[0];
 #pragma unroll
-    for (int w = 1; w < kAttnWaves; w++) mx = fmaxf(mx, wred[w]);
-    __syncthreads();
-    float sum = 0.0f;
-    for (int i = tid; i < cnt; i += kAttnWaves * 64) {
-        const float e = d_expf(sc[i] - mx);
-        sc[i] = e;
-        sum += e;
-    }
-    sum = group_sum<64>(sum);
-    if (lane == 0) wred[wave] = sum;
-    __syncthreads();
-    float4 acc = zero4;
-    for (int base = t0 + wave * BATCH; base < t1; base += kAttnWaves * BATCH) {
-        float4 v4[kAttnUnroll];
-#pragma unroll
-        for (int u = 0; u < kAttnUnroll; u++) {
-            const int t = min(base + u * RPI + slot, t1 - 1);
-            v4[u] = reinterpret_cast<const float4 *>(a.vc + (long)t * a.kv_dim + ko)[sub_c];
+        for (int w = 1; w < kAttnWaves; w++) mx = fmaxf(mx, wred[w]);
+        __syncthreads();
+        float sum = 0.0f;
+        for (int i = tid; i < cnt; i += kAttnWaves * 64) {
+            const float e = d_expf(sc[i] - mx);
+            sc[i] = e;
+            sum += e;
         }
+        sum = group_sum<64>(sum);
+        if (lane == 0) wred[wave] = sum;
+        __syncthreads();
+        return mx;
+    };
+    auto accumulate = [&](int base, const float4 (&v4)[kAttnUnroll], float4 &acc) {
 #pragma unroll
         for (int u = 0; u < kAttnUnroll; u++) {
             const int t = base + u * RPI + slot;
@@ -129,6 +129,33 @@ __global__ __launch_bounds__(kAttnWaves * 64) void k_attn_chunk(AttnParams a) {
             acc.y = fmaf(e, v4[u].y, acc.y);
             acc.z = fmaf(e, v4[u].z, acc.z);
             acc.w = fmaf(e, v4[u].w, acc.w);
+        }
+    };
+
+    float4 acc = zero4;
+    float mx;
+    if (cnt <= kAttnWaves * BATCH) {
+        // One batch per wave: the V rows are loaded together with the K
+        // rows, so the softmax does not wait for a second round trip.
+        // Waves past the chunk's end re-read row t1-1 and add nothing.
+        const int base = t0 + wave * BATCH;
+        float4 k4[kAttnUnroll], v4[kAttnUnroll];
+        load_rows(kbase, base, k4);
+        load_rows(vbase, base, v4);
+        score_rows(base, k4);
+        mx = softmax();
+        accumulate(base, v4, acc);
+    } else {
+        for (int base = t0 + wave * BATCH; base < t1; base += kAttnWaves * BATCH) {
+            float4 k4[kAttnUnroll];
+            load_rows(kbase, base, k4);
+            score_rows(base, k4);
+        }
+        mx = softmax();
+        for (int base = t0 + wave * BATCH; base < t1; base += kAttnWaves * BATCH) {
+            float4 v4[kAttnUnroll];
+            load_rows(vbase, base, v4);
+            accumulate(base, v4, acc);
         }
     }
 #pragma unroll
@@ -268,14 +295,11 @@ struct StepTimer {
     } while (0)
 
 // Producer-side prefetch of consumer matvec weights W[rows, n] (ld = n).
-PrefetchDesc pf_matvec(const ptmi_model *m, const float *W, int rows, int n, int first_block) {
+// The producer's own grid is `first_block` blocks of `threads` threads.
+PrefetchDesc pf_matvec(const ptmi_model *m, const float *W, int rows, int n, int pro, int epi, int first_block,
+                       int threads) {
     if (!m->prefetch) return PrefetchDesc{};
-    return prefetch_for(W, n, rows, n, first_block, m->sink);
-}
-
-int matvec_compute_blocks(int rows, int n) {
-    MatvecGeom g;
-    return matvec_geometry(rows, n, &g) ? 8 * g.blocks_per_xcd : 0;
+    return prefetch_for(W, n, rows, n, pro, epi, first_block, threads, m->sink);
 }
 
 // Enqueue one decode step on s (used both for capture and eager runs).
@@ -299,7 +323,9 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         p.norm_w = r->rms_att + l * D;
         p.y = m->q; p.epi = EPI_QKV_ROPE; p.pos = &m->ctl->pos;
         p.q_rows = (int)D; p.kv_rows = (int)KV; p.head_dim = c.head_dim; p.k_cache = kc; p.v_cache = vc;
-        p.pf = pf_matvec(m, r->wo + (long)l * D * D, (int)D, (int)D, matvec_compute_blocks(QR, (int)D));
+        p.pf = pf_matvec(m, r->wo + (long)l * D * D, (int)D, (int)D, PRO_ATTN_COMBINE, EPI_RESIDUAL,
+                         matvec_compute_blocks(QR, (int)D, p.pro, EPI_QKV_ROPE),
+                         matvec_block_threads(QR, (int)D, p.pro, EPI_QKV_ROPE));
         TIMED(0, if ((st = launch_matvec(p, s, e0, e1))) return st);
 
         AttnParams a = {};
@@ -310,7 +336,8 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         const int hd4 = c.head_dim / 4;
         auto attn = hd4 <= 8 ? k_attn_chunk<8> : hd4 <= 16 ? k_attn_chunk<16> : k_attn_chunk<32>;
         const int attn_blocks = c.n_heads * m->attn_chunks;
-        a.pf = pf_matvec(m, r->w13 + (long)l * 2 * H * D, (int)(2 * H), (int)D, attn_blocks);
+        a.pf = pf_matvec(m, r->w13 + (long)l * 2 * H * D, (int)(2 * H), (int)D, PRO_RMSNORM, EPI_SWIGLU, attn_blocks,
+                         kAttnWaves * 64);
         a.pf.first_block = attn_blocks;
         TIMED(1, launch_k(attn, dim3(attn_blocks + a.pf.blocks), dim3(kAttnWaves * 64), 0, s, e0, e1, a));
         PTMI_HIP(hipGetLastError());
@@ -320,7 +347,9 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         p.x = m->xb; p.y = m->x; p.pro = PRO_ATTN_COMBINE; p.epi = EPI_RESIDUAL;
         p.pos = &m->ctl->pos; p.att_o = m->part_o; p.att_ml = m->part_ml;
         p.att_chunks = m->attn_chunks; p.att_chunk = m->attn_chunk; p.att_heads = c.n_heads;
-        p.pf = pf_matvec(m, r->w2 + (long)l * D * H, (int)D, (int)H, matvec_compute_blocks((int)D, (int)D));
+        p.pf = pf_matvec(m, r->w2 + (long)l * D * H, (int)D, (int)H, PRO_NONE, EPI_RESIDUAL,
+                         matvec_compute_blocks((int)D, (int)D, PRO_ATTN_COMBINE, EPI_RESIDUAL),
+                         matvec_block_threads((int)D, (int)D, PRO_ATTN_COMBINE, EPI_RESIDUAL));
         TIMED(2, if ((st = launch_matvec(p, s, e0, e1))) return st);
 
         p = MatvecParams{};
@@ -328,7 +357,9 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         p.x = m->x; p.pro = PRO_RMSNORM; p.norm_w = r->rms_ffn + l * D;
         p.y = m->hb; p.epi = EPI_SWIGLU;
         if (l + 1 < c.n_layers)
-            p.pf = pf_matvec(m, r->wqkv + (long)(l + 1) * QR * D, QR, (int)D, matvec_compute_blocks((int)(2 * H), (int)D));
+            p.pf = pf_matvec(m, r->wqkv + (long)(l + 1) * QR * D, QR, (int)D, PRO_RMSNORM, EPI_QKV_ROPE,
+                             matvec_compute_blocks((int)(2 * H), (int)D, PRO_RMSNORM, EPI_SWIGLU),
+                             matvec_block_threads((int)(2 * H), (int)D, PRO_RMSNORM, EPI_SWIGLU));
         TIMED(3, if ((st = launch_matvec(p, s, e0, e1))) return st);
 
         p = MatvecParams{};
@@ -339,7 +370,9 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
     MatvecParams p = {};
     p.W = r->wcls; p.ld = D; p.rows = c.vocab; p.n = (int)D;
     p.x = m->x; p.pro = PRO_RMSNORM; p.norm_w = r->rms_final; p.y = m->logits; p.epi = EPI_STORE;
-    p.pf = pf_matvec(m, r->wqkv, QR, (int)D, matvec_compute_blocks(c.vocab, (int)D));
+    p.pf = pf_matvec(m, r->wqkv, QR, (int)D, PRO_EMBED_RMSNORM, EPI_QKV_ROPE,
+                     matvec_compute_blocks(c.vocab, (int)D, PRO_RMSNORM, EPI_STORE),
+                     matvec_block_threads(c.vocab, (int)D, PRO_RMSNORM, EPI_STORE));
     TIMED(5, if ((st = launch_matvec(p, s, e0, e1))) return st);
     const PrefetchDesc none = {};
     TIMED(6, launch_k(k_argmax_step, dim3(1), dim3(1024), 0, s, e0, e1, m->logits, c.vocab, m->ctl, m->prompt,

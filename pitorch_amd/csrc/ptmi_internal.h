@@ -167,14 +167,22 @@ struct PrefetchDesc {
 
 // Rows of one matvec per XCD stripe and per wave (shared by the launcher
 // and by producers that prefetch for it).
+// lpr lanes per row, it float4 of x per lane, rows_per_wave rows per wave
+// in one (two_pass = 0) or two interleaved passes of 64/lpr rows, wpb
+// waves per block, blocks_per_xcd blocks on each XCD's stripe of rows.
 struct MatvecGeom {
-    int lpr, it, exact, step, stripe, rows_per_wave, blocks_per_xcd;
+    int lpr, it, exact, step, stripe, rows_per_wave, blocks_per_xcd, wpb, two_pass;
 };
-bool matvec_geometry(int rows, int n, MatvecGeom *g);
+bool matvec_geometry(int rows, int n, int pro, int epi, MatvecGeom *g);
 
-// Describe a prefetch of consumer matvec (W rows x ld) for a producer
-// whose own blocks end at `first_block`.
-PrefetchDesc prefetch_for(const float *W, long ld, int rows, int n, int first_block, float *sink);
+// Describe a prefetch of consumer matvec (W rows x ld, with the given
+// prologue/epilogue) for a producer whose own blocks end at `first_block`
+// and run `producer_threads` threads each.
+PrefetchDesc prefetch_for(const float *W, long ld, int rows, int n, int pro, int epi, int first_block,
+                          int producer_threads, float *sink);
+// Geometry of the matvec the launcher will run for this shape and fusion.
+int matvec_compute_blocks(int rows, int n, int pro, int epi);
+int matvec_block_threads(int rows, int n, int pro, int epi);
 
 struct MatvecParams {
     const float *W;        // row r starts at W + r*ld
@@ -195,7 +203,7 @@ struct MatvecParams {
     const float *att_ml;   // [heads][chunks][2] (chunk max, chunk sum)
     int att_chunks, att_chunk, att_heads;
     int rows_per_wave;     // filled by the launcher
-    int stripe, blocks_per_xcd;
+    int stripe, blocks_per_xcd, two_pass;
     PrefetchDesc pf;       // optional L2 prefetch for the next stage
 };
 

@@ -36,16 +36,17 @@ __device__ __forceinline__ float dot4(float4 w, float4 x, float acc) {
 
 // Epilogue for rows [row0, row0 + nrows) whose sums sit in vals[0..nrows).
 // Runs on one wave; lane i handles row row0+i (pairs handled by even lanes).
+// EPI_RESIDUAL: `res` is y[row0 + lane], loaded in the prologue.
 template <int EPI>
 __device__ __forceinline__ void run_epilogue(const MatvecParams &p, const float *vals,
-                                             int row0, int nrows, int lane, int pos = 0) {
+                                             int row0, int nrows, int lane, int pos, float res) {
     if (lane >= nrows) return;
     const int r = row0 + lane;
     const float v = vals[lane];
     if constexpr (EPI == EPI_STORE) {
         p.y[r] = v;
     } else if constexpr (EPI == EPI_RESIDUAL) {   // vec_add(x, x, xb2): llama2.c:180,190
-        p.y[r] = p.y[r] + v;
+        p.y[r] = res + v;
     } else if constexpr (EPI == EPI_SWIGLU) {     // rows interleaved w1[i], w3[i]
         if (lane & 1) return;                     // llama2.c:187-188 (silu, vec_mul)
         const float h1 = v, h3 = vals[lane + 1];
@@ -99,14 +100,17 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
     // XCD-striped rows: block b (on XCD b%8) works inside stripe b%8.
     const long s0 = (long)(blockIdx.x & 7) * p.stripe;
     const long s1 = s0 + p.stripe < (long)p.rows ? s0 + p.stripe : (long)p.rows;
-    const long row0l = s0 + ((long)(blockIdx.x >> 3) * kWaves + wave) * p.rows_per_wave;
+    const int wpb = blockDim.x >> 6;
+    const long row0l = s0 + ((long)(blockIdx.x >> 3) * wpb + wave) * p.rows_per_wave;
     const bool active = row0l < s1;
     const int row0 = active ? (int)row0l : 0;
     const int nrows = active ? (int)min((long)p.rows_per_wave, s1 - row0l) : 0;
 
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    // ---- main loop: two passes (2*RPP rows) per iteration ----
+    // ---- main loop: one or two passes (RPP rows each) per iteration ----
     // Rows past the end re-read the wave's last row; their sums are dropped.
+    const bool two = p.two_pass != 0;              // uniform
+    const int iter_rows = two ? 2 * RPP : RPP;
     float4 la[IT], lb[IT];
     auto load_pair = [&](int base) {
         const int ra = min(base + slot, nrows - 1), rb = min(base + RPP + slot, nrows - 1);
@@ -115,20 +119,28 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
 #pragma unroll
         for (int it = 0; it < IT; it++) {
             const int c = sub + it * LPR;
-            if constexpr (EXACT) {
-                la[it] = wa[c];
-                lb[it] = wb[c];
-            } else {
-                const int cc = min(c, n4 - 1);
-                la[it] = wa[cc];
+            const int cc = EXACT ? c : min(c, n4 - 1);
+            la[it] = wa[cc];
+            if (!EXACT && c >= n4) la[it] = zero4;
+        }
+        if (two) {
+#pragma unroll
+            for (int it = 0; it < IT; it++) {
+                const int c = sub + it * LPR;
+                const int cc = EXACT ? c : min(c, n4 - 1);
                 lb[it] = wb[cc];
-                if (c >= n4) { la[it] = zero4; lb[it] = zero4; }
+                if (!EXACT && c >= n4) lb[it] = zero4;
             }
         }
     };
     // The first pair's weight loads go out before the prologue, so the x
     // fetch and RMSNorm arithmetic overlap the weight latency.
     if (nrows > 0) load_pair(0);
+    // The residual this wave's epilogue adds to (its rows only).
+    float res = 0.0f;
+    if constexpr (EPI == EPI_RESIDUAL) {
+        if (lane < nrows) res = p.y[row0 + lane];
+    }
 
     // ---- prologue: this lane's x chunks (and RMSNorm weights) -> registers.
     // Every load the prologue and epilogue need is issued here, together,
@@ -140,44 +152,79 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
     if constexpr (PRO == PRO_ATTN_COMBINE) {
         // x[i] = sum_c w[h][c] o_c[i], w[h][c] = e^(m_c - M) / sum_c' l_c' e^(m_c' - M)
         // over the active chunks of head h = i/hd, once per workgroup into
-        // LDS.  Both phases issue all their loads before using any.
+        // LDS.  The chunk statistics and partial sums of every allocated
+        // chunk are loaded together with the position (one memory round
+        // trip); chunks past the active ones are dropped by selects, so
+        // whatever they hold never reaches the result.
         __shared__ float xcomb[kMaxCombineDim];
         __shared__ float wts[kMaxCombineHeads][kMaxAttnChunks];
         const int hd = p.n / p.att_heads;
-        const int active = pos / p.att_chunk + 1;
-        for (int h = threadIdx.x; h < p.att_heads; h += kWaves * 64) {
-            const float *ml = p.att_ml + 2L * h * p.att_chunks;
-            float mv[kMaxAttnChunks], lv[kMaxAttnChunks];
+        const int nch = p.att_chunks;
+        constexpr int kFastI = 6;                        // n <= 6 * threads in one round trip
+        const int nthr = blockDim.x;
+        const bool fast = p.n <= kFastI * nthr;          // uniform
+        float ov[kFastI][kMaxAttnChunks];
+        if (fast) {
 #pragma unroll
-            for (int c = 0; c < kMaxAttnChunks; c++) {
-                const int cc = min(c, active - 1);
-                mv[c] = ml[2 * cc];
-                lv[c] = ml[2 * cc + 1];
+            for (int k = 0; k < kFastI; k++) {
+                if (k * nthr >= p.n) break;              // uniform: slots past n load nothing
+                const int i = min((int)threadIdx.x + k * nthr, p.n - 1);
+                const int h = i / hd, d = i - h * hd;
+                const float *o = p.att_o + (long)h * nch * hd + d;
+#pragma unroll
+                for (int c = 0; c < kMaxAttnChunks; c++) ov[k][c] = o[(long)min(c, nch - 1) * hd];
             }
+        }
+        float mv[kMaxAttnChunks], lv[kMaxAttnChunks];
+        const int h_ml = min((int)threadIdx.x, p.att_heads - 1);
+        const float *ml = p.att_ml + 2L * h_ml * nch;
+#pragma unroll
+        for (int c = 0; c < kMaxAttnChunks; c++) {
+            const int cc = min(c, nch - 1);
+            mv[c] = ml[2 * cc];
+            lv[c] = ml[2 * cc + 1];
+        }
+        const int active = pos / p.att_chunk + 1;
+        if ((int)threadIdx.x < p.att_heads) {
             float M = mv[0];
 #pragma unroll
-            for (int c = 1; c < kMaxAttnChunks; c++) if (c < active) M = fmaxf(M, mv[c]);
+            for (int c = 1; c < kMaxAttnChunks; c++) M = c < active ? fmaxf(M, mv[c]) : M;
             float f[kMaxAttnChunks], L = 0.0f;
 #pragma unroll
             for (int c = 0; c < kMaxAttnChunks; c++) {
                 f[c] = c < active ? d_expf(mv[c] - M) : 0.0f;
-                L = fmaf(lv[c], f[c], L);
+                L = c < active ? fmaf(lv[c], f[c], L) : L;
             }
             const float inv = 1.0f / L;
 #pragma unroll
-            for (int c = 0; c < kMaxAttnChunks; c++) wts[h][c] = f[c] * inv;
+            for (int c = 0; c < kMaxAttnChunks; c++) wts[threadIdx.x][c] = f[c] * inv;
         }
         __syncthreads();
-        for (int i = threadIdx.x; i < p.n; i += kWaves * 64) {
-            const int h = i / hd, d = i - h * hd;
-            const float *o = p.att_o + (long)h * p.att_chunks * hd + d;
-            float ov[kMaxAttnChunks];
+        if (fast) {
 #pragma unroll
-            for (int c = 0; c < kMaxAttnChunks; c++) ov[c] = o[(long)min(c, active - 1) * hd];
-            float v = 0.0f;
+            for (int k = 0; k < kFastI; k++) {
+                if (k * nthr >= p.n) break;
+                const int i = (int)threadIdx.x + k * nthr;
+                if (i < p.n) {
+                    const int h = i / hd;
+                    float v = 0.0f;
 #pragma unroll
-            for (int c = 0; c < kMaxAttnChunks; c++) v = fmaf(ov[c], wts[h][c], v);   // w = 0 past active
-            xcomb[i] = v;
+                    for (int c = 0; c < kMaxAttnChunks; c++) v = c < active ? fmaf(ov[k][c], wts[h][c], v) : v;
+                    xcomb[i] = v;
+                }
+            }
+        } else {
+            for (int i = threadIdx.x; i < p.n; i += nthr) {
+                const int h = i / hd, d = i - h * hd;
+                const float *o = p.att_o + (long)h * nch * hd + d;
+                float ovs[kMaxAttnChunks];
+#pragma unroll
+                for (int c = 0; c < kMaxAttnChunks; c++) ovs[c] = o[(long)min(c, nch - 1) * hd];
+                float v = 0.0f;
+#pragma unroll
+                for (int c = 0; c < kMaxAttnChunks; c++) v = c < active ? fmaf(ovs[c], wts[h][c], v) : v;
+                xcomb[i] = v;
+            }
         }
         __syncthreads();
         xs = xcomb;
@@ -214,25 +261,24 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
         }
     }
 
-    for (int base = 0; base < nrows; base += 2 * RPP) {
+    for (int base = 0; base < nrows; base += iter_rows) {
         if (base > 0) load_pair(base);
         const int ra = base + slot, rb = base + RPP + slot;
-        const bool va = ra < nrows, vb = rb < nrows;
-        float acc_a = 0.0f, acc_b = 0.0f;
+        float acc_a = 0.0f;
 #pragma unroll
-        for (int it = 0; it < IT; it++) {
-            acc_a = dot4(la[it], xr[it], acc_a);
-            acc_b = dot4(lb[it], xr[it], acc_b);
-        }
+        for (int it = 0; it < IT; it++) acc_a = dot4(la[it], xr[it], acc_a);
         acc_a = group_sum<LPR>(acc_a);
-        acc_b = group_sum<LPR>(acc_b);
-        if (sub == 0) {
-            if (va) ybuf[wave][ra] = acc_a;
-            if (vb) ybuf[wave][rb] = acc_b;
+        if (sub == 0 && ra < nrows) ybuf[wave][ra] = acc_a;
+        if (two) {
+            float acc_b = 0.0f;
+#pragma unroll
+            for (int it = 0; it < IT; it++) acc_b = dot4(lb[it], xr[it], acc_b);
+            acc_b = group_sum<LPR>(acc_b);
+            if (sub == 0 && rb < nrows) ybuf[wave][rb] = acc_b;
         }
     }
     __syncthreads();
-    if (active) run_epilogue<EPI>(p, ybuf[wave], row0, nrows, lane, pos);
+    if (active) run_epilogue<EPI>(p, ybuf[wave], row0, nrows, lane, pos, res);
 }
 
 // Long rows (n > 64*9*4): one wave per row pair, x read through the cache
@@ -267,7 +313,7 @@ __global__ __launch_bounds__(256) void k_matvec_long(MatvecParams p) {
         }
     }
     __syncthreads();
-    if (active) run_epilogue<EPI_STORE>(p, ybuf[wave], row0, nrows, lane);
+    if (active) run_epilogue<EPI_STORE>(p, ybuf[wave], row0, nrows, lane, 0, 0.0f);
 }
 
 // Any alignment / any n: one wave per row, scalar loads.
@@ -328,33 +374,78 @@ inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 // Lanes-per-row so that each lane holds at most 9 float4 of x; rows split
 // into 8 XCD stripes (multiples of the row-pair step); rows-per-wave so
 // that each XCD runs ~256 waves (8 per CU) when the matrix is big enough.
-bool matvec_geometry(int rows, int n, MatvecGeom *g) {
+// Kernel geometry, chosen from measurements on MI355X (graph-replayed
+// launches, weights in HBM or MALL):
+//  * With a prologue (RMSNorm, embedding, attention combine), whose cost is
+//    paid per wave or per workgroup: the fewest lanes per row that keep a
+//    lane's x slice within 9 float4, two row passes per iteration, ~256
+//    waves per XCD (8 per CU), 4 waves per block.  More workgroups make
+//    these kernels slower.
+//  * Without a prologue: many small workgroups win (768x768: 2.57 vs
+//    3.18 us; 2304x768: 3.19 vs 3.64 us).  For rows of >= 192 floats, ~4096
+//    single-wave blocks with as many lanes per row as that allows; for
+//    shorter rows, ~1024 waves of two-pass rows.
+bool matvec_geometry(int rows, int n, int pro, int epi, MatvecGeom *g) {
     const int n4 = n / 4;
     if (n % 4 || n4 > 64 * 9 || rows <= 0) return false;
-    g->lpr = n4 <= 8 * 9 ? 8 : n4 <= 16 * 9 ? 16 : n4 <= 32 * 9 ? 32 : 64;
-    g->it = (n4 + g->lpr - 1) / g->lpr;
-    g->exact = n4 == g->lpr * g->it;
-    g->step = 2 * (64 / g->lpr);
+    const int gran = (epi == EPI_SWIGLU || epi == EPI_QKV_ROPE) ? 2 : 1;   // row pairs stay in one wave
+    const int lpr_min = n4 <= 8 * 9 ? 8 : n4 <= 16 * 9 ? 16 : n4 <= 32 * 9 ? 32 : 64;
     const int per = (rows + 7) / 8;
-    g->stripe = (per + g->step - 1) / g->step * g->step;
-    int rpw = (g->stripe + 255) / 256;
-    rpw = (rpw + g->step - 1) / g->step * g->step;
-    rpw = std::max(rpw, g->step);
-    rpw = std::min(rpw, kMaxRowsPerWave);
+    int lpr = lpr_min, rpw, wpb;
+    bool two;
+    if (pro != PRO_NONE) {
+        const int step = 2 * (64 / lpr);
+        g->stripe = (per + step - 1) / step * step;
+        rpw = (g->stripe + 255) / 256;
+        rpw = (rpw + step - 1) / step * step;
+        rpw = std::min(std::max(rpw, step), kMaxRowsPerWave);
+        two = true;
+        wpb = kWaves;
+    } else {
+        const int target = n4 > 8 * 9 ? 4096 : 1024;
+        rpw = std::max((rows + target - 1) / target, gran);
+        while (lpr < 64 && lpr < n4 && 64 / lpr > rpw) lpr *= 2;
+        const int rpp = 64 / lpr;
+        rpw = std::min(std::max(rpw, rpp), kMaxRowsPerWave);
+        rpw = (rpw + gran - 1) / gran * gran;
+        two = rpw > rpp;
+        g->stripe = (per + gran - 1) / gran * gran;
+        const int waves = (g->stripe + rpw - 1) / rpw;
+        wpb = n4 > 8 * 9 ? 1 : waves >= 128 ? 4 : waves >= 64 ? 2 : 1;
+    }
+    g->lpr = lpr;
+    g->it = (n4 + lpr - 1) / lpr;
+    g->exact = n4 == lpr * g->it;
+    g->step = gran;
     g->rows_per_wave = rpw;
+    g->two_pass = two;
+    g->wpb = wpb;
     const int waves = (g->stripe + rpw - 1) / rpw;
-    g->blocks_per_xcd = (waves + kWaves - 1) / kWaves;
+    g->blocks_per_xcd = (waves + wpb - 1) / wpb;
     return true;
 }
 
-PrefetchDesc prefetch_for(const float *W, long ld, int rows, int n, int first_block, float *sink) {
+int matvec_compute_blocks(int rows, int n, int pro, int epi) {
+    MatvecGeom g;
+    return matvec_geometry(rows, n, pro, epi, &g) ? 8 * g.blocks_per_xcd : 0;
+}
+
+int matvec_block_threads(int rows, int n, int pro, int epi) {
+    MatvecGeom g;
+    return matvec_geometry(rows, n, pro, epi, &g) ? 64 * g.wpb : 0;
+}
+
+PrefetchDesc prefetch_for(const float *W, long ld, int rows, int n, int pro, int epi, int first_block,
+                          int producer_threads, float *sink) {
     PrefetchDesc pf = {};
     MatvecGeom g;
-    if (!W || ld % 4 || !matvec_geometry(rows, n, &g)) return pf;
+    if (!W || ld % 4 || !matvec_geometry(rows, n, pro, epi, &g)) return pf;
     pf.base = W; pf.row_floats = ld; pf.rows = rows; pf.stripe = g.stripe;
-    // ~64 KB per prefetch block: two rounds of eight 16-byte loads per lane
+    // 256 bytes per prefetch thread (two rounds of eight 16-byte loads);
+    // prefetch blocks run with the producer kernel's block size.
+    const long bytes_per_block = 256L * producer_threads;
     const long bytes_per_xcd = (long)g.stripe * ld * 4;
-    const int per_xcd = (int)std::max<long>(1, std::min<long>(64, (bytes_per_xcd + 65535) / 65536));
+    const int per_xcd = (int)std::max<long>(1, std::min<long>(256, (bytes_per_xcd + bytes_per_block - 1) / bytes_per_block));
     pf.blocks = 8 * per_xcd;
     pf.first_block = first_block;
     pf.sink = sink;
@@ -389,7 +480,7 @@ int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     KernelFn fn = nullptr;
     int rpp = 1;
     MatvecGeom geo;
-    if (vec_ok && matvec_geometry(p.rows, p.n, &geo)) {
+    if (vec_ok && matvec_geometry(p.rows, p.n, p.pro, p.epi, &geo)) {
         switch (geo.lpr) {
         case 8: fn = pick<8>(geo.it, geo.exact, p.pro, p.epi); break;
         case 16: fn = pick<16>(geo.it, geo.exact, p.pro, p.epi); break;
@@ -400,10 +491,11 @@ int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
         p.stripe = geo.stripe;
         p.rows_per_wave = geo.rows_per_wave;
         p.blocks_per_xcd = geo.blocks_per_xcd;
+        p.two_pass = geo.two_pass;
         const int compute_blocks = 8 * geo.blocks_per_xcd;
         if (p.pf.blocks && p.pf.first_block != compute_blocks)
             return set_error(PTMI_ERR_ARG, "matvec: prefetch descriptor built for another grid");
-        launch_k(fn, dim3((unsigned)(compute_blocks + p.pf.blocks)), dim3(kWaves * 64), 0, s, e0, e1, p);
+        launch_k(fn, dim3((unsigned)(compute_blocks + p.pf.blocks)), dim3(geo.wpb * 64), 0, s, e0, e1, p);
         PTMI_HIP(hipGetLastError());
         return PTMI_OK;
     } else if (vec_ok) {
