@@ -9,12 +9,12 @@
 // The device weight layout fuses [wq;wk;wv] and row-interleaves [w1|w3],
 // so QKV and w1|w3 are one GEMM each in both directions.
 //
-// Non-GEMM ops follow the reference's arithmetic order: reductions that are
-// short (RMSNorm sums over dim, attention softmax sums over positions,
-// attention backward dot products) run sequentially in one lane, exactly as
-// the reference loops do; per-column gradient accumulations over positions
-// run in ascending t like the reference.  Only the GEMMs (and the 32000-wide
-// loss softmax sums) reorder additions.
+// Non-GEMM ops keep the reference's element-wise arithmetic; their sums
+// (RMSNorm squares, softmax sums, attention dot products, column gradient
+// accumulations) are block reductions, so their addition order differs
+// from the reference's sequential loops, as in the GEMMs.  The embedding
+// gradient keeps the reference's order exactly (one lane per column and
+// token, positions ascending).
 #include "ptmi_model.h"
 
 #include <cmath>
@@ -38,6 +38,34 @@ namespace {
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// ── block reductions (every thread gets the result) ──────────────────────
+
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = group_sum<64>(v);
+    __syncthreads();                       // red may still be read by a previous call
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) s += red[w];
+    return s;
+}
+
+template <int NW>
+__device__ __forceinline__ float block_max(float v, float *red) {
+    v = group_max<64>(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) m = fmaxf(m, red[w]);
+    return m;
+}
+
+__device__ __forceinline__ float dot4(float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
+
 // ── forward kernels ──────────────────────────────────────────────────────
 
 __global__ void k_embed_rows(const int *tok, const float *emb, float *out, int D) {   // pt_train.c:189-191
@@ -46,19 +74,15 @@ __global__ void k_embed_rows(const int *tok, const float *emb, float *out, int D
     for (int i = threadIdx.x; i < D; i += blockDim.x) out[(long)t * D + i] = src[i];
 }
 
-// rmsnorm (pt_ops.c:5-12) per row; the sum of squares is one sequential
-// chain as in the reference.
-__global__ void k_rmsnorm_rows(const float *in, const float *w, float *out, int D) {
-    __shared__ float inv_s;
+// rmsnorm (pt_ops.c:5-12) per row.
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *in, const float *w, float *out, int D) {
+    __shared__ float red[4];
     const float *x = in + (long)blockIdx.x * D;
-    if (threadIdx.x == 0) {
-        float ss = 0.0f;
-        for (int i = 0; i < D; i++) ss += x[i] * x[i];
-        inv_s = 1.0f / d_sqrtf(ss / D + 1e-5f);
-    }
-    __syncthreads();
-    const float inv = inv_s;
-    for (int i = threadIdx.x; i < D; i += blockDim.x) out[(long)blockIdx.x * D + i] = x[i] * inv * w[i];
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < D; i += 256) ss += x[i] * x[i];
+    ss = block_sum<4>(ss, red);
+    const float inv = 1.0f / d_sqrtf(ss / D + 1e-5f);
+    for (int i = threadIdx.x; i < D; i += 256) out[(long)blockIdx.x * D + i] = x[i] * inv * w[i];
 }
 
 // rope (pt_ops.c:33-49) on the q and k columns of each position's qkv row.
@@ -77,49 +101,109 @@ __global__ void k_rope_rows(float *qkv, int T, int D, int QS, int hd) {
     k[1] = k0 * s + k1 * c;
 }
 
+// Attention blocks: 256 threads; G lanes (G*4 >= head_dim) hold one
+// position's head row as float4, so a wave covers 64/G positions per load
+// and the block 256/G.
+constexpr int kAttnThreads = 256;
+
+// Per-position dot products s[t2] = a . B[t2] (B rows at b + t2*ld) for t2
+// in [0, n), G lanes per row; lane sub's float4 of `a` is a4.
+template <int G>
+__device__ __forceinline__ void row_dots(const float *b, long ld, float4 a4, int hd4, int n, float *out, float mul) {
+    constexpr int S = kAttnThreads / G;
+    const int slot = threadIdx.x / G, sub = threadIdx.x % G;
+    const bool has = sub < hd4;
+    for (int base = 0; base < n; base += 4 * S) {
+        float4 r[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int t2 = min(base + u * S + slot, n - 1);
+            r[u] = has ? reinterpret_cast<const float4 *>(b + (long)t2 * ld)[sub] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            float v = has ? dot4(a4, r[u]) : 0.0f;
+            v = group_sum<G>(v);
+            const int t2 = base + u * S + slot;
+            if (sub == 0 && t2 < n) out[t2] = v * mul;
+        }
+    }
+}
+
+// o[i] = sum_{t2 < n} w[t2] B[t2][i] for i < hd (B rows at b + t2*ld); the
+// 256/G slots take interleaved positions and their partial sums meet in
+// LDS `part` (at least (256/G)*hd floats).  Thread i < hd returns o[i].
+constexpr int kAttnPart = 1024;   // (256/G) * hd <= 1024 for hd <= 4*G
+template <int G>
+__device__ __forceinline__ float weighted_rows(const float *b, long ld, const float *w, int hd4, int n, float *part) {
+    constexpr int S = kAttnThreads / G;
+    const int slot = threadIdx.x / G, sub = threadIdx.x % G;
+    const bool has = sub < hd4;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int base = 0; base < n; base += 4 * S) {
+        float4 r[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int t2 = min(base + u * S + slot, n - 1);
+            r[u] = has ? reinterpret_cast<const float4 *>(b + (long)t2 * ld)[sub] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int t2 = base + u * S + slot;
+            const float e = t2 < n ? w[t2] : 0.0f;
+            acc.x += e * r[u].x;
+            acc.y += e * r[u].y;
+            acc.z += e * r[u].z;
+            acc.w += e * r[u].w;
+        }
+    }
+    const int hd = 4 * hd4;
+    __syncthreads();                      // earlier readers of part are done
+    if (has) reinterpret_cast<float4 *>(part + slot * hd)[sub] = acc;
+    __syncthreads();
+    float o = 0.0f;
+    if ((int)threadIdx.x < hd) {
+        o = part[threadIdx.x];
+        for (int k = 1; k < S; k++) o += part[k * hd + threadIdx.x];
+    }
+    return o;
+}
+
 // Causal attention for one (position t, head h): pt_train.c:224-255.
-__global__ void k_attn_fwd(const float *qkv, float *att, float *att_out, int T, int D, int QS, int KV, int hd,
-                           int kv_mul, float scale) {
+// Dynamic LDS: sc[T].
+template <int G>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_fwd(const float *qkv, float *att, float *att_out, int T, int D,
+                                                           int QS, int KV, int hd, int kv_mul, float scale) {
     extern __shared__ float sc[];
-    __shared__ float inv_s;
-    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-    const float *q = qkv + (long)t * QS + h * hd;
+    __shared__ float part[kAttnPart];
+    __shared__ float red[4];
+    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, hd4 = hd >> 2, sub = tid % G;
     const int ko = D + (h / kv_mul) * hd, vo = D + KV + (h / kv_mul) * hd;
-    for (int t2 = tid; t2 <= t; t2 += blockDim.x) {
-        const float *k = qkv + (long)t2 * QS + ko;
-        float s = 0.0f;
-        for (int i = 0; i < hd; i++) s += q[i] * k[i];
-        sc[t2] = s * scale;
+    const float4 q4 = sub < hd4 ? reinterpret_cast<const float4 *>(qkv + (long)t * QS + h * hd)[sub]
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    const int n = t + 1;
+    row_dots<G>(qkv + ko, QS, q4, hd4, n, sc, scale);
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int t2 = tid; t2 < n; t2 += kAttnThreads) mx = fmaxf(mx, sc[t2]);
+    mx = block_max<4>(mx, red);
+    float sum = 0.0f;
+    for (int t2 = tid; t2 < n; t2 += kAttnThreads) {
+        const float e = d_expf(sc[t2] - mx);
+        sc[t2] = e;
+        sum += e;
     }
-    __syncthreads();
-    if (tid == 0) {
-        float mx = sc[0];
-        for (int t2 = 1; t2 <= t; t2++) if (sc[t2] > mx) mx = sc[t2];
-        inv_s = mx;
-    }
-    __syncthreads();
-    const float mx = inv_s;
-    for (int t2 = tid; t2 <= t; t2 += blockDim.x) sc[t2] = d_expf(sc[t2] - mx);
-    __syncthreads();
-    if (tid == 0) {
-        float sum = 0.0f;
-        for (int t2 = 0; t2 <= t; t2++) sum += sc[t2];
-        inv_s = 1.0f / sum;
-    }
-    __syncthreads();
-    const float inv = inv_s;
+    sum = block_sum<4>(sum, red);
+    const float inv = 1.0f / sum;
     float *arow = att + ((long)h * T + t) * T;
-    for (int t2 = tid; t2 < T; t2 += blockDim.x) {
-        const float a = t2 <= t ? sc[t2] * inv : 0.0f;
+    for (int t2 = tid; t2 < T; t2 += kAttnThreads) {
+        const float a = t2 < n ? sc[t2] * inv : 0.0f;
         arow[t2] = a;
-        if (t2 <= t) sc[t2] = a;
+        if (t2 < n) sc[t2] = a;
     }
     __syncthreads();
-    for (int i = tid; i < hd; i += blockDim.x) {
-        float o = 0.0f;
-        for (int t2 = 0; t2 <= t; t2++) o += sc[t2] * qkv[(long)t2 * QS + vo + i];
-        att_out[(long)t * D + h * hd + i] = o;
-    }
+    const float o = weighted_rows<G>(qkv + vo, QS, sc, hd4, n, part);
+    if (tid < hd) att_out[(long)t * D + h * hd + tid] = o;
 }
 
 // silu(h1)*h3 in the training form (h1*sigmoid(h1))*h3, pt_train.c:280-284.
@@ -133,87 +217,110 @@ __global__ void k_swiglu_fwd(const float *h13, float *sh, long n, int H) {
 }
 
 // Cross-entropy row t < T-1 (pt_train.c:310-325) and, in place, its loss
-// gradient (pt_train.c:609-621); the last row's gradient is zero.
-__global__ __launch_bounds__(256) void k_loss_rows(float *lg_dl, const int *tok, int T, int V, float inv_T1,
-                                                   float *row_loss) {
-    __shared__ float red[256];
-    __shared__ float bcast[2];
+// gradient (pt_train.c:609-621); the last row's gradient is zero.  Pass 1
+// keeps a running (max, sum of e^(x-max)) per thread, merged over the block.
+constexpr int kLossThreads = 1024;
+__global__ __launch_bounds__(kLossThreads) void k_loss_rows(float *lg_dl, const int *tok, int T, int V, float inv_T1,
+                                                            float *row_loss) {
+    __shared__ float red[kLossThreads / 64];
     const int t = blockIdx.x, tid = threadIdx.x;
     float *row = lg_dl + (long)t * V;
+    const bool vec = (V % 4) == 0;
+    const int n4 = vec ? V / 4 : 0;
+    float4 *row4 = reinterpret_cast<float4 *>(row);
     if (t == T - 1) {
-        for (int v = tid; v < V; v += 256) row[v] = 0.0f;
+        for (int v = tid; v < n4; v += kLossThreads) row4[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int v = 4 * n4 + tid; v < V; v += kLossThreads) row[v] = 0.0f;
         return;
     }
     const int target = tok[t + 1];
-    float mx = -INFINITY;
-    for (int v = tid; v < V; v += 256) mx = fmaxf(mx, row[v]);
-    red[tid] = mx;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
-        __syncthreads();
+    float m = -INFINITY, s = 0.0f;
+    auto add = [&](float x) {
+        if (x > m) {
+            s = s * d_expf(m - x) + 1.0f;      // e^(-inf) = 0 on the first element
+            m = x;
+        } else {
+            s += d_expf(x - m);
+        }
+    };
+    for (int v = tid; v < n4; v += kLossThreads) {
+        const float4 x = row4[v];
+        add(x.x); add(x.y); add(x.z); add(x.w);
     }
-    mx = red[0];
-    __syncthreads();
-    float sum = 0.0f;
-    for (int v = tid; v < V; v += 256) sum += d_expf(row[v] - mx);
-    red[tid] = sum;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (tid < s) red[tid] += red[tid + s];
-        __syncthreads();
+    for (int v = 4 * n4 + tid; v < V; v += kLossThreads) add(row[v]);
+    const float mx = block_max<kLossThreads / 64>(m, red);
+    const float part = m == -INFINITY ? 0.0f : s * d_expf(m - mx);
+    const float sum = block_sum<kLossThreads / 64>(part, red);
+    if (tid == 0) row_loss[t] = -(row[target] - mx - d_logf(sum));
+    __syncthreads();                           // row[target] is read before it is overwritten
+    const float scale = (1.0f / sum) * inv_T1;
+    for (int v = tid; v < n4; v += kLossThreads) {
+        const float4 x = row4[v];
+        float4 d;
+        d.x = d_expf(x.x - mx) * scale;
+        d.y = d_expf(x.y - mx) * scale;
+        d.z = d_expf(x.z - mx) * scale;
+        d.w = d_expf(x.w - mx) * scale;
+        const int b = 4 * v;
+        if (target >= b && target < b + 4) (&d.x)[target - b] -= inv_T1;
+        row4[v] = d;
     }
-    if (tid == 0) {
-        sum = red[0];
-        row_loss[t] = -(row[target] - mx - d_logf(sum));
-        bcast[0] = 1.0f / sum;
-    }
-    __syncthreads();
-    const float scale = bcast[0] * inv_T1;
-    for (int v = tid; v < V; v += 256) {
+    for (int v = 4 * n4 + tid; v < V; v += kLossThreads) {
         float d = d_expf(row[v] - mx) * scale;
         if (v == target) d -= inv_T1;
         row[v] = d;
     }
 }
 
-__global__ void k_loss_reduce(const float *row_loss, int T, float *loss) {
+__global__ __launch_bounds__(256) void k_loss_reduce(const float *row_loss, int T, float *loss) {
+    __shared__ float red[4];
     float l = 0.0f;
-    for (int t = 0; t < T - 1; t++) l += row_loss[t];
-    *loss = l / (float)(T - 1);
+    for (int t = threadIdx.x; t < T - 1; t += 256) l += row_loss[t];
+    l = block_sum<4>(l, red);
+    if (threadIdx.x == 0) *loss = l / (float)(T - 1);
 }
 
 // ── backward kernels ─────────────────────────────────────────────────────
 
 // rmsnorm_backward (pt_backward_ops.c:4-30), the d_x half, per row.
-__global__ void k_rmsnorm_bwd_rows(float *d_x, const float *d_o, const float *x, const float *w, float *inv_out,
-                                   int D) {
-    __shared__ float sh_inv, sh_c;
+__global__ __launch_bounds__(256) void k_rmsnorm_bwd_rows(float *d_x, const float *d_o, const float *x, const float *w,
+                                                          float *inv_out, int D) {
+    __shared__ float red[4];
     const long r = (long)blockIdx.x * D;
-    if (threadIdx.x == 0) {
-        float ss = 0.0f;
-        for (int i = 0; i < D; i++) ss += x[r + i] * x[r + i];
-        ss = ss / D + 1e-5f;
-        const float inv = 1.0f / d_sqrtf(ss);
-        float dot = 0.0f;
-        for (int i = 0; i < D; i++) dot += d_o[r + i] * w[i] * x[r + i];
-        const float coeff = inv * inv * inv / (float)D;
-        sh_inv = inv;
-        sh_c = coeff * dot;
-        inv_out[blockIdx.x] = inv;
+    float ss = 0.0f, dot = 0.0f;
+    for (int i = threadIdx.x; i < D; i += 256) {
+        const float xi = x[r + i];
+        ss += xi * xi;
+        dot += d_o[r + i] * w[i] * xi;
     }
-    __syncthreads();
-    const float inv = sh_inv, cd = sh_c;
-    for (int i = threadIdx.x; i < D; i += blockDim.x) d_x[r + i] += inv * d_o[r + i] * w[i] - cd * x[r + i];
+    ss = block_sum<4>(ss, red);
+    dot = block_sum<4>(dot, red);
+    ss = ss / D + 1e-5f;
+    const float inv = 1.0f / d_sqrtf(ss);
+    const float cd = inv * inv * inv / (float)D * dot;
+    if (threadIdx.x == 0) inv_out[blockIdx.x] = inv;
+    for (int i = threadIdx.x; i < D; i += 256) d_x[r + i] += inv * d_o[r + i] * w[i] - cd * x[r + i];
 }
 
-// The d_w half: d_w[i] += d_o[t][i]*x[t][i]*inv[t], t ascending.
-__global__ void k_rmsnorm_bwd_dw(float *d_w, const float *d_o, const float *x, const float *inv, int R, int D) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= D) return;
-    float acc = d_w[i];
-    for (int t = 0; t < R; t++) acc += d_o[(long)t * D + i] * x[(long)t * D + i] * inv[t];
-    d_w[i] = acc;
+// The d_w half: d_w[i] += sum_t d_o[t][i]*x[t][i]*inv[t]; 64 columns per
+// block, 16 interleaved row slices summed in LDS.
+__global__ __launch_bounds__(1024) void k_rmsnorm_bwd_dw(float *d_w, const float *d_o, const float *x,
+                                                         const float *inv, int R, int D) {
+    __shared__ float part[16][64];
+    const int c = threadIdx.x & 63, sl = threadIdx.x >> 6;
+    const int i = blockIdx.x * 64 + c;
+    float acc = 0.0f;
+    if (i < D) {
+#pragma unroll 4
+        for (int t = sl; t < R; t += 16) acc += d_o[(long)t * D + i] * x[(long)t * D + i] * inv[t];
+    }
+    part[sl][c] = acc;
+    __syncthreads();
+    if (sl == 0 && i < D) {
+        float g = d_w[i];
+        for (int k = 0; k < 16; k++) g += part[k][c];
+        d_w[i] = g;
+    }
 }
 
 // silu*gate backward (pt_train.c:696-721) into interleaved [d_hid | d_hid2]
@@ -234,58 +341,60 @@ __global__ void k_swiglu_bwd(const float *h13, const float *d_sh, float *d_h13, 
 
 // Attention backward, row half (pt_train.c:780-811): for (t < R, head h):
 // d_att_s, the softmax backward dot, ds = d_pre*scale (kept for the column
-// half) and d_q[t] = sum_t2 ds[t2] k[t2].
-__global__ void k_attn_bwd_rows(const float *qkv, const float *att, const float *d_aout, float *ds, float *d_q,
-                                int T, int D, int QS, int KV, int hd, int kv_mul, float scale) {
-    extern __shared__ float sm[];
-    float *das = sm, *dpre = sm + T;
-    __shared__ float dot_s;
-    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-    const float *dao = d_aout + (long)t * D + h * hd;
+// half) and d_q[t] = sum_t2 ds[t2] k[t2].  Dynamic LDS: das[T].
+template <int G>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_rows(const float *qkv, const float *att,
+                                                                const float *d_aout, float *ds, float *d_q, int T,
+                                                                int D, int QS, int KV, int hd, int kv_mul,
+                                                                float scale) {
+    extern __shared__ float das[];
+    __shared__ float part[kAttnPart];
+    __shared__ float red[4];
+    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, hd4 = hd >> 2, sub = tid % G;
     const float *arow = att + ((long)h * T + t) * T;
     const int ko = D + (h / kv_mul) * hd, vo = D + KV + (h / kv_mul) * hd;
-    for (int t2 = tid; t2 <= t; t2 += blockDim.x) {
-        const float *v = qkv + (long)t2 * QS + vo;
-        float s = 0.0f;
-        for (int i = 0; i < hd; i++) s += dao[i] * v[i];
-        das[t2] = s;
-    }
+    const float4 g4 = sub < hd4 ? reinterpret_cast<const float4 *>(d_aout + (long)t * D + h * hd)[sub]
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    const int n = t + 1;
+    row_dots<G>(qkv + vo, QS, g4, hd4, n, das, 1.0f);
     __syncthreads();
-    if (tid == 0) {
-        float dot = 0.0f;
-        for (int t2 = 0; t2 <= t; t2++) dot += das[t2] * arow[t2];
-        dot_s = dot;
-    }
-    __syncthreads();
-    const float dot = dot_s;
+    float dot = 0.0f;
+    for (int t2 = tid; t2 < n; t2 += kAttnThreads) dot += das[t2] * arow[t2];
+    dot = block_sum<4>(dot, red);
     float *dsrow = ds + ((long)h * T + t) * T;
-    for (int t2 = tid; t2 <= t; t2 += blockDim.x) {
+    for (int t2 = tid; t2 < n; t2 += kAttnThreads) {
         const float d = arow[t2] * (das[t2] - dot) * scale;
-        dpre[t2] = d;
+        das[t2] = d;
         dsrow[t2] = d;
     }
     __syncthreads();
-    for (int i = tid; i < hd; i += blockDim.x) {
-        float acc = 0.0f;
-        for (int t2 = 0; t2 <= t; t2++) acc += dpre[t2] * qkv[(long)t2 * QS + ko + i];
-        d_q[(long)t * D + h * hd + i] = acc;
-    }
+    const float o = weighted_rows<G>(qkv + ko, QS, das, hd4, n, part);
+    if (tid < hd) d_q[(long)t * D + h * hd + tid] = o;
 }
 
-// Attention backward, column half: for (t2 < R, head h), t ascending:
-// d_v[t2] = sum_t att[t][t2] d_aout[t],  d_k[t2] = sum_t ds[t][t2] q[t].
-__global__ void k_attn_bwd_cols(const float *qkv, const float *att, const float *ds, const float *d_aout, float *d_k,
-                                float *d_v, int T, int R, int D, int QS, int KV, int hd, int kv_mul) {
-    const int t2 = blockIdx.x, h = blockIdx.y;
-    const int kvo = (h / kv_mul) * hd;
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
-        float dv = 0.0f, dk = 0.0f;
-        for (int t = t2; t < R; t++) {
-            dv += att[((long)h * T + t) * T + t2] * d_aout[(long)t * D + h * hd + i];
-            dk += ds[((long)h * T + t) * T + t2] * qkv[(long)t * QS + h * hd + i];
-        }
-        d_v[(long)t2 * KV + kvo + i] = dv;
-        d_k[(long)t2 * KV + kvo + i] = dk;
+// Attention backward, column half: for (t2 < R, head h):
+// d_v[t2] = sum_{t>=t2} att[t][t2] d_aout[t],  d_k[t2] = sum_{t>=t2} ds[t][t2] q[t].
+// Dynamic LDS: w[2*T].
+template <int G>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_cols(const float *qkv, const float *att, const float *ds,
+                                                                const float *d_aout, float *d_k, float *d_v, int T,
+                                                                int R, int D, int QS, int KV, int hd, int kv_mul) {
+    extern __shared__ float sm[];
+    __shared__ float part[kAttnPart];
+    float *wa = sm, *wd = sm + T;
+    const int t2 = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, hd4 = hd >> 2;
+    const int kvo = (h / kv_mul) * hd, n = R - t2;
+    for (int k = tid; k < n; k += kAttnThreads) {
+        const long a = ((long)h * T + t2 + k) * T + t2;
+        wa[k] = att[a];
+        wd[k] = ds[a];
+    }
+    __syncthreads();
+    const float dv = weighted_rows<G>(d_aout + (long)t2 * D + h * hd, D, wa, hd4, n, part);
+    const float dk = weighted_rows<G>(qkv + (long)t2 * QS + h * hd, QS, wd, hd4, n, part);
+    if (tid < hd) {
+        d_v[(long)t2 * KV + kvo + tid] = dv;
+        d_k[(long)t2 * KV + kvo + tid] = dk;
     }
 }
 
@@ -310,11 +419,23 @@ __global__ void k_rope_bwd_pack(const float *d_q, const float *d_k, const float 
     o[D + KV + i + 1] = d_v[(long)t * KV + i + 1];
 }
 
-// embedding_backward (pt_backward_ops.c:90-95) for t ascending, per column.
-__global__ void k_embed_bwd(const int *tok, const float *d_res, float *g_emb, int R, int D) {
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= D) return;
-    for (int t = 0; t < R; t++) g_emb[(long)tok[t] * D + j] += d_res[(long)t * D + j];
+// embedding_backward (pt_backward_ops.c:90-95) in the reference's order:
+// the block of the first position holding a token accumulates, per column,
+// every position with that token in ascending t.  Dynamic LDS: tok[R].
+__global__ __launch_bounds__(256) void k_embed_bwd(const int *tok, const float *d_res, float *g_emb, int R, int D) {
+    extern __shared__ int stok[];
+    const int t = blockIdx.x;
+    for (int k = threadIdx.x; k < R; k += 256) stok[k] = tok[k];
+    __syncthreads();
+    const int tk = stok[t];
+    for (int k = 0; k < t; k++)
+        if (stok[k] == tk) return;                  // uniform: an earlier block owns this token
+    for (int j = threadIdx.x; j < D; j += 256) {
+        float acc = g_emb[(long)tk * D + j];
+        for (int k = t; k < R; k++)
+            if (stok[k] == tk) acc += d_res[(long)k * D + j];
+        g_emb[(long)tk * D + j] = acc;
+    }
 }
 
 // sgd_step (pt_train.c:870-873) over the whole device weight buffer.
@@ -388,7 +509,7 @@ int gemm(hipStream_t s, TrainState *ts, int op, const float *A, long lda, const 
 int rmsnorm_bwd(hipStream_t s, TrainState *ts, float *d_x, const float *d_o, const float *x, const float *w,
                 float *d_w, int R, int D) {
     hipLaunchKernelGGL(k_rmsnorm_bwd_rows, dim3(R), dim3(256), 0, s, d_x, d_o, x, w, ts->row_inv, D);
-    hipLaunchKernelGGL(k_rmsnorm_bwd_dw, dim3(blocks_for(D, 256)), dim3(256), 0, s, d_w, d_o, x, ts->row_inv, R, D);
+    hipLaunchKernelGGL(k_rmsnorm_bwd_dw, dim3(blocks_for(D, 64)), dim3(1024), 0, s, d_w, d_o, x, ts->row_inv, R, D);
     PTMI_HIP(hipGetLastError());
     return PTMI_OK;
 }
@@ -404,6 +525,11 @@ int enqueue_train(ptmi_model *m, int T, float lr, hipStream_t s) {
     auto G = [&](const float *p) { return ts->gmem + (p - r->mem); };   // grad of a weight tensor
     int st;
     const size_t att_lds = (size_t)T * sizeof(float);
+    // G lanes per head row: the smallest of 8/16/32 with 4*G >= head_dim
+    const int hd4 = hd / 4;
+    auto attn_fwd = hd4 <= 8 ? k_attn_fwd<8> : hd4 <= 16 ? k_attn_fwd<16> : k_attn_fwd<32>;
+    auto attn_bwd_rows = hd4 <= 8 ? k_attn_bwd_rows<8> : hd4 <= 16 ? k_attn_bwd_rows<16> : k_attn_bwd_rows<32>;
+    auto attn_bwd_cols = hd4 <= 8 ? k_attn_bwd_cols<8> : hd4 <= 16 ? k_attn_bwd_cols<16> : k_attn_bwd_cols<32>;
 
     PTMI_HIP(hipMemsetAsync(ts->gmem, 0, r->mem_floats * sizeof(float), s));        // pt_zero_grads
     // ── forward ──
@@ -415,7 +541,8 @@ int enqueue_train(ptmi_model *m, int T, float lr, hipStream_t s) {
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, rin, r->rms_att + (long)l * D, xa, D);
         if ((st = gemm(s, ts, 2, xa, D, r->wqkv + (long)l * QS * D, D, qkv, QS, T, QS, D, 0))) return st;
         hipLaunchKernelGGL(k_rope_rows, dim3(blocks_for((long)T * D / 2, 256)), dim3(256), 0, s, qkv, T, D, QS, hd);
-        hipLaunchKernelGGL(k_attn_fwd, dim3(T, NH), dim3(64), att_lds, s, qkv, att, ao, T, D, QS, KV, hd, kv_mul, scale);
+        hipLaunchKernelGGL(attn_fwd, dim3(T, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ao, T, D, QS, KV, hd, kv_mul,
+                           scale);
         PTMI_HIP(hipMemcpyAsync(rmid, rin, TD * sizeof(float), hipMemcpyDeviceToDevice, s));
         if ((st = gemm(s, ts, 2, ao, D, r->wo + (long)l * D * D, D, rmid, D, T, D, D, 1))) return st;
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, rmid, r->rms_ffn + (long)l * D, xf, D);
@@ -426,9 +553,9 @@ int enqueue_train(ptmi_model *m, int T, float lr, hipStream_t s) {
     }
     hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, ts->res + L * TD, r->rms_final, ts->x_final, D);
     if ((st = gemm(s, ts, 2, ts->x_final, D, r->wcls, D, ts->logits, V, T, V, D, 0))) return st;
-    hipLaunchKernelGGL(k_loss_rows, dim3(T), dim3(256), 0, s, ts->logits, ts->tok, T, V, 1.0f / (float)(T - 1),
+    hipLaunchKernelGGL(k_loss_rows, dim3(T), dim3(kLossThreads), 0, s, ts->logits, ts->tok, T, V, 1.0f / (float)(T - 1),
                        ts->row_loss);
-    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(1), 0, s, ts->row_loss, T, ts->loss);
+    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, s, ts->row_loss, T, ts->loss);
     PTMI_HIP(hipGetLastError());
 
     // ── backward ── (ts->logits now holds d_logits)
@@ -455,9 +582,10 @@ int enqueue_train(ptmi_model *m, int T, float lr, hipStream_t s) {
         if ((st = gemm(s, ts, 0, ts->d_res, D, wo, D, ts->d_aout, D, R, D, D, 0))) return st;
         if ((st = gemm(s, ts, 1, ts->d_res, D, ao, D, G(wo), D, D, D, R, 1))) return st;
         // attention
-        hipLaunchKernelGGL(k_attn_bwd_rows, dim3(R, NH), dim3(64), 2 * att_lds, s, qkv, att, ts->d_aout, ts->ds, ts->d_q,
+        hipLaunchKernelGGL(attn_bwd_rows, dim3(R, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ts->d_aout, ts->ds, ts->d_q,
                            T, D, QS, KV, hd, kv_mul, scale);
-        hipLaunchKernelGGL(k_attn_bwd_cols, dim3(R, NH), dim3(64), 0, s, qkv, att, ts->ds, ts->d_aout, ts->d_k, ts->d_v,
+        hipLaunchKernelGGL(attn_bwd_cols, dim3(R, NH), dim3(kAttnThreads), 2 * att_lds, s, qkv, att, ts->ds, ts->d_aout,
+                           ts->d_k, ts->d_v,
                            T, R, D, QS, KV, hd, kv_mul);
         hipLaunchKernelGGL(k_rope_bwd_pack, dim3(blocks_for((long)R * D / 2, 256)), dim3(256), 0, s, ts->d_q, ts->d_k,
                            ts->d_v, ts->d_qkv, R, D, KV, QS, hd);
@@ -468,7 +596,7 @@ int enqueue_train(ptmi_model *m, int T, float lr, hipStream_t s) {
         if ((st = rmsnorm_bwd(s, ts, ts->d_res, ts->d_xb, rin, r->rms_att + (long)l * D,
                               G(r->rms_att + (long)l * D), R, D))) return st;
     }
-    hipLaunchKernelGGL(k_embed_bwd, dim3(blocks_for(D, 256)), dim3(256), 0, s, ts->tok, ts->d_res, G(r->emb), R, D);
+    hipLaunchKernelGGL(k_embed_bwd, dim3(R), dim3(256), (size_t)R * sizeof(int), s, ts->tok, ts->d_res, G(r->emb), R, D);
     // ── SGD ──
     hipLaunchKernelGGL(k_sgd, dim3(blocks_for((long)r->mem_floats, 256)), dim3(256), 0, s, r->mem, ts->gmem, lr,
                        (long)r->mem_floats);
