@@ -136,12 +136,14 @@ def train_gemm_shapes(cfg, T):
     return fwd + dx + dw
 
 
-def bench_train(pa, reps=5):
+def bench_train(pa, reps=20):
     """stories15M training step (config 5): ms/step of the device pt_train_step
-    and fp32-MFMA utilisation of its GEMMs, each GEMM shape timed with HIP
-    events on the library stream."""
+    (hipGraph per step) and fp32-MFMA utilisation of its GEMMs; each GEMM
+    shape is captured `reps` times back to back in a hipGraph on the library
+    stream and timed with HIP events around graph replays, so host launch
+    cost is not in the figure."""
     import numpy as np
-    from pitorch_amd._hip import DeviceArray, Event
+    from pitorch_amd._hip import DeviceArray, Event, Graph
 
     L = pa.load_ptmi()
     name, T, lr = "stories15M", 256, 1e-3
@@ -167,12 +169,21 @@ def bench_train(pa, reps=5):
         lda = K if op != 1 else M
         ldb = N if op != 2 else K
         pa._ffi.check(L.ptmi_gemm_dev(op, A.ptr, lda, B.ptr, ldb, C.ptr, N, M, N, K, 0, None))
+        pa._ffi.check(L.ptmi_sync())
+
+        def enqueue():
+            for _ in range(reps):
+                pa._ffi.check(L.ptmi_gemm_dev(op, A.ptr, lda, B.ptr, ldb, C.ptr, N, M, N, K, 1, stream))
+
+        g = Graph(stream, enqueue)
+        g.launch()
         e0, e1 = Event(), Event()
         e0.record(stream)
-        for _ in range(reps):
-            pa._ffi.check(L.ptmi_gemm_dev(op, A.ptr, lda, B.ptr, ldb, C.ptr, N, M, N, K, 1, None))
+        for _ in range(3):
+            g.launch()
         e1.record(stream)
-        ms = e0.elapsed_ms(e1) / reps
+        ms = e0.elapsed_ms(e1) / (3 * reps)
+        g.free()
         flop = 2.0 * M * N * K
         total_flop += flop * count
         total_ms += ms * count

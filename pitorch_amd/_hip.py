@@ -36,6 +36,12 @@ def hip():
     H.hipEventSynchronize.argtypes = [vp]
     H.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
     H.hipEventDestroy.argtypes = [vp]
+    H.hipStreamBeginCapture.argtypes = [vp, i]
+    H.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+    H.hipGraphInstantiate.argtypes = [ctypes.POINTER(vp), vp, vp, vp, sz]
+    H.hipGraphLaunch.argtypes = [vp, vp]
+    H.hipGraphExecDestroy.argtypes = [vp]
+    H.hipGraphDestroy.argtypes = [vp]
     _hip = H
     return H
 
@@ -97,3 +103,33 @@ class Event:
         ms = ctypes.c_float()
         assert hip().hipEventElapsedTime(ctypes.byref(ms), self.h, later.h) == 0
         return ms.value
+
+
+class Graph:
+    """Stream capture of whatever `fn()` enqueues on `stream`, replayable."""
+
+    CAPTURE_THREAD_LOCAL = 1
+
+    def __init__(self, stream, fn):
+        H = hip()
+        self.stream = stream
+        assert H.hipStreamBeginCapture(stream, self.CAPTURE_THREAD_LOCAL) == 0
+        try:
+            fn()
+        finally:
+            g = ctypes.c_void_p()
+            st = H.hipStreamEndCapture(stream, ctypes.byref(g))
+        assert st == 0, f"hipStreamEndCapture failed ({st})"
+        self.graph = g.value
+        e = ctypes.c_void_p()
+        assert H.hipGraphInstantiate(ctypes.byref(e), self.graph, None, None, 0) == 0
+        self.exec = e.value
+
+    def launch(self):
+        assert hip().hipGraphLaunch(self.exec, self.stream) == 0
+
+    def free(self):
+        if self.exec:
+            hip().hipGraphExecDestroy(self.exec)
+            hip().hipGraphDestroy(self.graph)
+            self.exec = self.graph = None

@@ -5,15 +5,18 @@
 //   dX = dY W    (NN) — backward_input_pretrans, pt_train.c:442-453
 //   Y  = X W^T   (NT) — the batched form of the training forward's matvecs
 //
-// Block tile 64x64, K step 32, 256 threads = 4 waves in a 2x2 grid, each
-// wave a 32x32 sub-tile of 2x2 MFMA 16x16 blocks.  Tiles are staged in LDS
-// k-major (As[k][m], Bs[k][n]) so every MFMA operand read is 16 consecutive
-// floats; the next K tile is fetched into registers while the current one
-// feeds the matrix cores.  Operand layout of the 16x16x4 f32 MFMA (CDNA3/4):
+// Block tile TMxTN (64x64, or 32x32 for small output grids), K step 32,
+// 256 threads = 4 waves in a 2x2 grid, each wave a (TM/2)x(TN/2) sub-tile
+// of 16x16 MFMA blocks.  Tiles are staged in LDS k-major (As[k][m],
+// Bs[k][n]) so every MFMA operand read is 16 consecutive floats.  Two K
+// tiles are in flight in registers while a third feeds the matrix cores
+// from LDS (double-buffered), so each tile's global latency is covered by
+// two K steps of MFMAs.  Operand layout of the 16x16x4 f32 MFMA (CDNA3/4):
 // lane l supplies A[l%16][l/16] and B[l/16][l%16]; result register r of lane
 // l is C[4*(l/16)+r][l%16].
-// Grids smaller than the CU count split K over blockIdx.z into a workspace
-// and reduce in split order afterwards (deterministic, no atomics).
+// Long-K GEMMs with small output grids split K over blockIdx.z into a
+// workspace and reduce in split order afterwards (deterministic, no
+// atomics).
 #include "ptmi_internal.h"
 
 #include <algorithm>
@@ -24,13 +27,13 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 64, BN = 64, BK = 32;
-constexpr int LDP = BM + 4;        // LDS row pitch (floats)
+constexpr int BK = 32;
 
 struct GemmArgs {
     const float *A; long lda;
     const float *B; long ldb;
     float *C; long ldc;
+    const float *Cin;      // accumulate: C = Cin + op(A).op(B) (Cin == C in place), same ldc
     int M, N, K;
     int accumulate;
     float *partial;        // split-K workspace [splits][M][N] or null
@@ -38,149 +41,169 @@ struct GemmArgs {
     bool a_vec, b_vec;     // 16-byte aligned rows: float4 global loads
 };
 
-// One operand tile (64 rows of the M or N side x 32 k) per K step; each of
-// the 256 threads moves 8 floats as two float4 (or 8 predicated scalars at
-// ragged edges).  KMAJOR: the operand is stored with k as the row index
-// (A^T for TN, B for NN/TN); otherwise k is the contiguous index.
-//   KMAJOR:  thread -> (k = tid/8,  idx = 8*(tid%8) + c)
-//   !KMAJOR: thread -> (idx = tid/4, k = 8*(tid%4) + c)
-template <bool KMAJOR>
+// One operand tile (R rows of the M or N side x 32 k) per K step; each of
+// the 256 threads moves E = R*32/256 floats (8 or 4) as float4s (or
+// predicated scalars at ragged edges).  KMAJOR: the operand is stored with
+// k as the row index (A^T for TN, B for NN/TN); otherwise k is the
+// contiguous index.
+//   KMAJOR:  thread -> (k = tid/8,         idx = E*(tid%8) + c)
+//   !KMAJOR: thread -> (idx = tid/(32/E),  k = E*(tid%(32/E)) + c)
+template <bool KMAJOR, int R>
 __device__ __forceinline__ void load_tile(const float *P, long ld, int idx_lim, int i0, int k0, int kend, bool vec,
-                                          int tid, float (&r)[8]) {
+                                          int tid, float (&r)[R * BK / 256]) {
+    constexpr int E = R * BK / 256;
     if (KMAJOR) {
-        const int k = k0 + tid / 8, i = i0 + 8 * (tid % 8);
+        const int k = k0 + tid / 8, i = i0 + E * (tid % 8);
         const bool kin = k < kend;
         const float *p = P + (long)min(k, kend - 1) * ld;
-        if (vec && i + 7 < idx_lim) {
-            const float4 v0 = *reinterpret_cast<const float4 *>(p + i);
-            const float4 v1 = *reinterpret_cast<const float4 *>(p + i + 4);
-            r[0] = v0.x; r[1] = v0.y; r[2] = v0.z; r[3] = v0.w;
-            r[4] = v1.x; r[5] = v1.y; r[6] = v1.z; r[7] = v1.w;
+        if (vec && i + E - 1 < idx_lim) {
+#pragma unroll
+            for (int c = 0; c < E; c += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(p + i + c);
+                r[c] = v.x; r[c + 1] = v.y; r[c + 2] = v.z; r[c + 3] = v.w;
+            }
             if (!kin) {
 #pragma unroll
-                for (int c = 0; c < 8; c++) r[c] = 0.f;
+                for (int c = 0; c < E; c++) r[c] = 0.f;
             }
         } else {
 #pragma unroll
-            for (int c = 0; c < 8; c++) r[c] = (kin && i + c < idx_lim) ? p[i + c] : 0.f;
+            for (int c = 0; c < E; c++) r[c] = (kin && i + c < idx_lim) ? p[i + c] : 0.f;
         }
     } else {
-        const int i = i0 + tid / 4, k = k0 + 8 * (tid % 4);
+        const int i = i0 + tid / (BK / E), k = k0 + E * (tid % (BK / E));
         const bool iin = i < idx_lim;
         const float *p = P + (long)min(i, idx_lim - 1) * ld;
-        if (vec && k + 7 < kend) {
-            const float4 v0 = *reinterpret_cast<const float4 *>(p + k);
-            const float4 v1 = *reinterpret_cast<const float4 *>(p + k + 4);
-            r[0] = v0.x; r[1] = v0.y; r[2] = v0.z; r[3] = v0.w;
-            r[4] = v1.x; r[5] = v1.y; r[6] = v1.z; r[7] = v1.w;
+        if (vec && k + E - 1 < kend) {
+#pragma unroll
+            for (int c = 0; c < E; c += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(p + k + c);
+                r[c] = v.x; r[c + 1] = v.y; r[c + 2] = v.z; r[c + 3] = v.w;
+            }
             if (!iin) {
 #pragma unroll
-                for (int c = 0; c < 8; c++) r[c] = 0.f;
+                for (int c = 0; c < E; c++) r[c] = 0.f;
             }
         } else {
 #pragma unroll
-            for (int c = 0; c < 8; c++) r[c] = (iin && k + c < kend) ? p[k + c] : 0.f;
+            for (int c = 0; c < E; c++) r[c] = (iin && k + c < kend) ? p[k + c] : 0.f;
         }
     }
 }
 
-template <bool KMAJOR>
-__device__ __forceinline__ void store_tile(float (*S)[LDP], int tid, const float (&r)[8]) {
+template <bool KMAJOR, int R>
+__device__ __forceinline__ void store_tile(float (*S)[R + 4], int tid, const float (&r)[R * BK / 256]) {
+    constexpr int E = R * BK / 256;
     if (KMAJOR) {
-        const int k = tid / 8, i = 8 * (tid % 8);
+        const int k = tid / 8, i = E * (tid % 8);
 #pragma unroll
-        for (int c = 0; c < 8; c++) S[k][i + c] = r[c];
+        for (int c = 0; c < E; c++) S[k][i + c] = r[c];
     } else {
-        const int i = tid / 4, k = 8 * (tid % 4);
+        const int i = tid / (BK / E), k = E * (tid % (BK / E));
 #pragma unroll
-        for (int c = 0; c < 8; c++) S[k + c][i] = r[c];
+        for (int c = 0; c < E; c++) S[k + c][i] = r[c];
     }
 }
 
-template <bool AT, bool BT>
+template <bool AT, bool BT, int TM, int TN>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
-    __shared__ float As[2][BK][LDP];
-    __shared__ float Bs[2][BK][LDP];
+    constexpr int FM = TM / 32, FN = TN / 32;          // 16x16 MFMA blocks per wave
+    constexpr int EA = TM * BK / 256, EB = TN * BK / 256;
+    __shared__ float As[2][BK][TM + 4];
+    __shared__ float Bs[2][BK][TN + 4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int li = lane & 15, lk = lane >> 4;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
     const int kb = blockIdx.z * g.k_per_split;
     const int kend = min(g.K, kb + g.k_per_split);
+    const int nk = kb < kend ? (kend - kb + BK - 1) / BK : 0;
 
-    floatx4 acc[2][2];
+    floatx4 acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < FN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    float ra[8], rb[8];
-    if (kb < kend) {
-        load_tile<AT>(g.A, g.lda, g.M, m0, kb, kend, g.a_vec, tid, ra);
-        load_tile<!BT>(g.B, g.ldb, g.N, n0, kb, kend, g.b_vec, tid, rb);
-        store_tile<AT>(As[0], tid, ra);
-        store_tile<!BT>(Bs[0], tid, rb);
-    }
-    __syncthreads();
-    int buf = 0;
-    for (int k0 = kb; k0 < kend; k0 += BK) {
-        const bool more = k0 + BK < kend;
-        if (more) {                                  // next tile -> registers
-            load_tile<AT>(g.A, g.lda, g.M, m0, k0 + BK, kend, g.a_vec, tid, ra);
-            load_tile<!BT>(g.B, g.ldb, g.N, n0, k0 + BK, kend, g.b_vec, tid, rb);
-        }
+    float ra0[EA], rb0[EB], ra1[EA], rb1[EB];
+    auto load = [&](int s, float (&ra)[EA], float (&rb)[EB]) {
+        load_tile<AT, TM>(g.A, g.lda, g.M, m0, kb + s * BK, kend, g.a_vec, tid, ra);
+        load_tile<!BT, TN>(g.B, g.ldb, g.N, n0, kb + s * BK, kend, g.b_vec, tid, rb);
+    };
+    auto store = [&](int s, const float (&ra)[EA], const float (&rb)[EB]) {
+        store_tile<AT, TM>(As[s & 1], tid, ra);
+        store_tile<!BT, TN>(Bs[s & 1], tid, rb);
+    };
+    auto compute = [&](int s) {
+        const int buf = s & 1;
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 4) {
-            const float a0 = As[buf][kk + lk][wm * 32 + li];
-            const float a1 = As[buf][kk + lk][wm * 32 + 16 + li];
-            const float b0 = Bs[buf][kk + lk][wn * 32 + li];
-            const float b1 = Bs[buf][kk + lk][wn * 32 + 16 + li];
-            acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[1][1], 0, 0, 0);
+            float a[FM], b[FN];
+#pragma unroll
+            for (int i = 0; i < FM; i++) a[i] = As[buf][kk + lk][wm * (TM / 2) + i * 16 + li];
+#pragma unroll
+            for (int j = 0; j < FN; j++) b[j] = Bs[buf][kk + lk][wn * (TN / 2) + j * 16 + li];
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
         }
-        if (more) {
-            store_tile<AT>(As[buf ^ 1], tid, ra);
-            store_tile<!BT>(Bs[buf ^ 1], tid, rb);
-        }
+    };
+    // One K step: tile s is in LDS, tile s+1 in registers `cur`; tile s+2
+    // goes into registers `nxt` (free: their tile went to LDS last step).
+    auto step = [&](int s, float (&cra)[EA], float (&crb)[EB], float (&nra)[EA], float (&nrb)[EB]) {
+        if (s + 2 < nk) load(s + 2, nra, nrb);
+        compute(s);
+        if (s + 1 < nk) store(s + 1, cra, crb);
         __syncthreads();
-        buf ^= 1;
+    };
+
+    if (nk > 0) {
+        load(0, ra0, rb0);
+        store(0, ra0, rb0);
+    }
+    if (nk > 1) load(1, ra1, rb1);
+    __syncthreads();
+    // register slots alternate: tile s+1 sits in slot (s+1)&1
+    for (int s = 0; s < nk; s += 2) {
+        step(s, ra1, rb1, ra0, rb0);
+        if (s + 1 < nk) step(s + 1, ra0, rb0, ra1, rb1);
     }
 
     // C[4*(l/16)+r][l%16] of each 16x16 block
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < FM; i++) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int n = n0 + wn * 32 + j * 16 + li;
+        for (int j = 0; j < FN; j++) {
+            const int n = n0 + wn * (TN / 2) + j * 16 + li;
             if (n >= g.N) continue;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = m0 + wm * 32 + i * 16 + 4 * lk + r;
+                const int m = m0 + wm * (TM / 2) + i * 16 + 4 * lk + r;
                 if (m >= g.M) continue;
                 const float v = acc[i][j][r];
                 if (g.partial) {
                     g.partial[((long)blockIdx.z * g.M + m) * g.N + n] = v;
                 } else {
-                    float *c = g.C + (long)m * g.ldc + n;
-                    *c = g.accumulate ? *c + v : v;
+                    const long o = (long)m * g.ldc + n;
+                    g.C[o] = g.accumulate ? g.Cin[o] + v : v;
                 }
             }
         }
     }
 }
 
-// C (+)= sum_z partial[z], z ascending.
-__global__ __launch_bounds__(256) void k_splitk_reduce(const float *partial, int splits, float *C, long ldc,
-                                                       int M, int N, int accumulate) {
+// C = (Cin +) sum_z partial[z], z ascending.
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float *partial, int splits, float *C, const float *Cin,
+                                                       long ldc, int M, int N, int accumulate) {
     const long idx = (long)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (long)M * N) return;
     const int m = (int)(idx / N), n = (int)(idx % N);
     float s = 0.0f;
     for (int z = 0; z < splits; z++) s += partial[(long)z * M * N + idx];
-    float *c = C + (long)m * ldc + n;
-    *c = accumulate ? *c + s : s;
+    const long o = (long)m * ldc + n;
+    C[o] = accumulate ? Cin[o] + s : s;
 }
 
 inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
@@ -190,7 +213,7 @@ inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 // Launch op(A).op(B) with shapes validated; `ws` (optional) is a split-K
 // workspace of ws_floats floats.
 int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc, int M, int N,
-                int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s) {
+                int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s, const float *Cin) {
     if (M <= 0 || N <= 0 || K <= 0) return set_error(PTMI_ERR_ARG, "gemm: M=%d N=%d K=%d", M, N, K);
     if (!A || !B || !C) return set_error(PTMI_ERR_ARG, "gemm: null operand");
     if (op < 0 || op > 2) return set_error(PTMI_ERR_ARG, "gemm: op %d", op);
@@ -201,31 +224,43 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
     GemmArgs g;
     g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc;
     g.M = M; g.N = N; g.K = K; g.accumulate = accumulate;
+    g.Cin = Cin ? Cin : C;
     g.a_vec = al16(A) && lda % 4 == 0;
     g.b_vec = al16(B) && ldb % 4 == 0;
-    const int gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM;
+    // Kernel choice, measured on MI355X for the training shapes (graph-
+    // replayed launches): 32x32 tiles win everywhere except long K (>= 4096:
+    // 64x64 with K split over >= 512 blocks) and large NT outputs (>= 4M
+    // elements: 64x64).  Every small GEMM is bound by the latency of its K
+    // steps, so K is split when a 32x32 grid is small and K long: about six
+    // K steps per split (K=768: 4 splits, 9.3 vs 14.6 us; K=1536: 8 splits).
+    const bool big = K >= 4096 || (op == 2 && (long)M * N >= (4L << 20));
+    const int TM = big ? 64 : 32, TN = TM;
+    const int gx = (N + TN - 1) / TN, gy = (M + TM - 1) / TM;
     const long blocks = (long)gx * gy;
-    // Split K when the tile grid leaves CUs idle: aim for >= 1024 blocks (four
-    // per CU, so one block's load latency hides behind another's MFMAs),
-    // keeping at least two K steps per split.
+    const int nk = (K + BK - 1) / BK;
     int splits = 1;
-    if (blocks < 1024 && K >= 4 * BK) {
-        splits = (int)std::min<long>((1024 + blocks - 1) / blocks, K / (2 * BK));
-        while (splits > 1 && (size_t)splits * M * N > ws_floats) splits--;
-    }
+    if (big && K >= 4096 && blocks < 512) splits = (int)std::min<long>((1024 + blocks - 1) / blocks, nk / 8);
+    else if (!big && blocks < 128 && nk > 9) splits = std::min(8, nk / 6);
+    while (splits > 1 && (size_t)splits * M * N > ws_floats) splits--;
     g.k_per_split = ((K + splits - 1) / splits + BK - 1) / BK * BK;
     splits = (K + g.k_per_split - 1) / g.k_per_split;
     g.partial = splits > 1 ? ws : nullptr;
     if (gy > 65535) return set_error(PTMI_ERR_ARG, "gemm: M too large");
     dim3 grid(gx, gy, splits);
-    if (op == 0) hipLaunchKernelGGL((k_gemm<false, false>), grid, dim3(256), 0, s, g);
-    else if (op == 1) hipLaunchKernelGGL((k_gemm<true, false>), grid, dim3(256), 0, s, g);
-    else hipLaunchKernelGGL((k_gemm<false, true>), grid, dim3(256), 0, s, g);
+    if (big) {
+        if (op == 0) hipLaunchKernelGGL((k_gemm<false, false, 64, 64>), grid, dim3(256), 0, s, g);
+        else if (op == 1) hipLaunchKernelGGL((k_gemm<true, false, 64, 64>), grid, dim3(256), 0, s, g);
+        else hipLaunchKernelGGL((k_gemm<false, true, 64, 64>), grid, dim3(256), 0, s, g);
+    } else {
+        if (op == 0) hipLaunchKernelGGL((k_gemm<false, false, 32, 32>), grid, dim3(256), 0, s, g);
+        else if (op == 1) hipLaunchKernelGGL((k_gemm<true, false, 32, 32>), grid, dim3(256), 0, s, g);
+        else hipLaunchKernelGGL((k_gemm<false, true, 32, 32>), grid, dim3(256), 0, s, g);
+    }
     PTMI_HIP(hipGetLastError());
     if (splits > 1) {
         const long n = (long)M * N;
-        hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ws, splits, C, ldc,
-                           M, N, accumulate);
+        hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ws, splits, C, g.Cin,
+                           ldc, M, N, accumulate);
         PTMI_HIP(hipGetLastError());
     }
     return PTMI_OK;

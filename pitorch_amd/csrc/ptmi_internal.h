@@ -248,8 +248,10 @@ int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0 = nullptr, hipEve
 
 // C[M,N] (+)= op(A).op(B) on the matrix cores; op 0 NN, 1 TN (A stored
 // [K][M]), 2 NT (B stored [N][K]).  ws: split-K workspace (may be null).
+// With accumulate, Cin (same leading dimension as C; null = C itself) is
+// the addend: C = Cin + op(A).op(B).
 int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc, int M, int N,
-                int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s);
+                int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s, const float *Cin = nullptr);
 
 // ── library state ───────────────────────────────────────────────────────
 struct Config {

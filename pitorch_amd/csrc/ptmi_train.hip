@@ -32,6 +32,12 @@ struct TrainState {
     float *d_res, *d_xb, *d_sh, *d_h13, *d_aout, *d_q, *d_k, *d_v, *d_qkv, *ds, *row_inv, *row_loss, *loss;
     float *ws;
     size_t ws_floats = 0;
+    float *lr;                  // device copy of the step's learning rate
+    // The step for one T, captured once (PTMI_TRAIN_EAGER=1: plain launches).
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int graph_T = 0;
+    bool eager = false;
 };
 
 namespace {
@@ -438,10 +444,18 @@ __global__ __launch_bounds__(256) void k_embed_bwd(const int *tok, const float *
     }
 }
 
-// sgd_step (pt_train.c:870-873) over the whole device weight buffer.
-__global__ void k_sgd(float *w, const float *g, float lr, long n) {
+// sgd_step (pt_train.c:870-873) over the whole device weight buffer; the
+// learning rate is read from device memory so a captured step serves any lr.
+__global__ void k_sgd(float *w, const float *g, const float *lr, long n) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) w[i] -= lr * g[i];
+    if (i < n) w[i] -= *lr * g[i];
+}
+
+// Zero fill (pt_zero_grads, pt_train.c:425-427), a kernel rather than a
+// memset node so the step can be captured.
+__global__ void k_fill0(float *p, long n) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.0f;
 }
 
 inline unsigned blocks_for(long n, int b) { return (unsigned)((n + b - 1) / b); }
@@ -473,11 +487,11 @@ int train_create(ptmi_model *m) {
         T * H, T * D, T * V,                                   // forward
         m->res->mem_floats,                                    // grads
         T * D, T * D, T * H, T * 2 * H, T * D, T * D, T * KV, T * KV, T * QS, NH * T * T, T, T, 64,
-        ts->ws_floats, T};
+        ts->ws_floats, T, 1};
     float **dst[] = {&ts->res, &ts->res_att, &ts->xb_att, &ts->qkv, &ts->att, &ts->att_out, &ts->xb_ffn, &ts->h13,
                      &ts->sh, &ts->x_final, &ts->logits, &ts->gmem, &ts->d_res, &ts->d_xb, &ts->d_sh, &ts->d_h13,
                      &ts->d_aout, &ts->d_q, &ts->d_k, &ts->d_v, &ts->d_qkv, &ts->ds, &ts->row_inv, &ts->row_loss,
-                     &ts->loss, &ts->ws, (float **)&ts->tok};
+                     &ts->loss, &ts->ws, (float **)&ts->tok, &ts->lr};
     const int nbuf = (int)(sizeof(sizes) / sizeof(sizes[0]));
     size_t total = 0;
     for (int i = 0; i < nbuf; i++) total += align_up(sizes[i], 64);
@@ -488,12 +502,16 @@ int train_create(ptmi_model *m) {
     e = hipMemsetAsync(ts->mem, 0, total * sizeof(float), lib_stream());
     if (e == hipSuccess) e = hipStreamSynchronize(lib_stream());
     if (e != hipSuccess) { (void)hipFree(ts->mem); delete ts; return hip_check(e, "zero training state"); }
+    const char *eager = getenv("PTMI_TRAIN_EAGER");
+    ts->eager = eager && eager[0] == '1';
     m->train = ts;
     return PTMI_OK;
 }
 
 void train_destroy(ptmi_model *m) {
     if (!m->train) return;
+    if (m->train->exec) (void)hipGraphExecDestroy(m->train->exec);
+    if (m->train->graph) (void)hipGraphDestroy(m->train->graph);
     (void)hipFree(m->train->mem);
     delete m->train;
     m->train = nullptr;
@@ -502,8 +520,12 @@ void train_destroy(ptmi_model *m) {
 namespace {
 
 int gemm(hipStream_t s, TrainState *ts, int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc,
-         int M, int N, int K, int acc) {
-    return launch_gemm(op, A, lda, B, ldb, C, ldc, M, N, K, acc, ts->ws, ts->ws_floats, s);
+         int M, int N, int K, int acc, const float *Cin = nullptr) {
+    return launch_gemm(op, A, lda, B, ldb, C, ldc, M, N, K, acc, ts->ws, ts->ws_floats, s, Cin);
+}
+
+void fill0(hipStream_t s, float *p, long n) {
+    hipLaunchKernelGGL(k_fill0, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n);
 }
 
 int rmsnorm_bwd(hipStream_t s, TrainState *ts, float *d_x, const float *d_o, const float *x, const float *w,
@@ -514,7 +536,9 @@ int rmsnorm_bwd(hipStream_t s, TrainState *ts, float *d_x, const float *d_o, con
     return PTMI_OK;
 }
 
-int enqueue_train(ptmi_model *m, int T, float lr, hipStream_t s) {
+// The whole step on stream s; T fixed, tokens and lr read from device
+// memory (ts->tok, ts->lr), so it can be captured once per T.
+int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     TrainState *ts = m->train;
     const Resident *r = m->res;
     const Config &c = m->c;
@@ -531,7 +555,7 @@ int enqueue_train(ptmi_model *m, int T, float lr, hipStream_t s) {
     auto attn_bwd_rows = hd4 <= 8 ? k_attn_bwd_rows<8> : hd4 <= 16 ? k_attn_bwd_rows<16> : k_attn_bwd_rows<32>;
     auto attn_bwd_cols = hd4 <= 8 ? k_attn_bwd_cols<8> : hd4 <= 16 ? k_attn_bwd_cols<16> : k_attn_bwd_cols<32>;
 
-    PTMI_HIP(hipMemsetAsync(ts->gmem, 0, r->mem_floats * sizeof(float), s));        // pt_zero_grads
+    fill0(s, ts->gmem, (long)r->mem_floats);                                        // pt_zero_grads
     // ── forward ──
     hipLaunchKernelGGL(k_embed_rows, dim3(T), dim3(256), 0, s, ts->tok, r->emb, ts->res, D);
     for (int l = 0; l < L; l++) {
@@ -543,13 +567,12 @@ int enqueue_train(ptmi_model *m, int T, float lr, hipStream_t s) {
         hipLaunchKernelGGL(k_rope_rows, dim3(blocks_for((long)T * D / 2, 256)), dim3(256), 0, s, qkv, T, D, QS, hd);
         hipLaunchKernelGGL(attn_fwd, dim3(T, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ao, T, D, QS, KV, hd, kv_mul,
                            scale);
-        PTMI_HIP(hipMemcpyAsync(rmid, rin, TD * sizeof(float), hipMemcpyDeviceToDevice, s));
-        if ((st = gemm(s, ts, 2, ao, D, r->wo + (long)l * D * D, D, rmid, D, T, D, D, 1))) return st;
+        // residual: rmid = rin + att_out . Wo^T
+        if ((st = gemm(s, ts, 2, ao, D, r->wo + (long)l * D * D, D, rmid, D, T, D, D, 1, rin))) return st;
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, rmid, r->rms_ffn + (long)l * D, xf, D);
         if ((st = gemm(s, ts, 2, xf, D, r->w13 + (long)l * 2 * H * D, D, h13, 2 * H, T, 2 * H, D, 0))) return st;
         hipLaunchKernelGGL(k_swiglu_fwd, dim3(blocks_for((long)T * H, 256)), dim3(256), 0, s, h13, ts->sh, (long)T * H, H);
-        PTMI_HIP(hipMemcpyAsync(rout, rmid, TD * sizeof(float), hipMemcpyDeviceToDevice, s));
-        if ((st = gemm(s, ts, 2, ts->sh, H, r->w2 + (long)l * D * H, H, rout, D, T, D, H, 1))) return st;
+        if ((st = gemm(s, ts, 2, ts->sh, H, r->w2 + (long)l * D * H, H, rout, D, T, D, H, 1, rmid))) return st;
     }
     hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, ts->res + L * TD, r->rms_final, ts->x_final, D);
     if ((st = gemm(s, ts, 2, ts->x_final, D, r->wcls, D, ts->logits, V, T, V, D, 0))) return st;
@@ -559,7 +582,7 @@ int enqueue_train(ptmi_model *m, int T, float lr, hipStream_t s) {
     PTMI_HIP(hipGetLastError());
 
     // ── backward ── (ts->logits now holds d_logits)
-    PTMI_HIP(hipMemsetAsync(ts->d_res, 0, TD * sizeof(float), s));
+    fill0(s, ts->d_res, TD);
     if ((st = gemm(s, ts, 0, ts->logits, V, r->wcls, D, ts->d_xb, D, R, D, V, 0))) return st;
     if ((st = rmsnorm_bwd(s, ts, ts->d_res, ts->d_xb, ts->res + L * TD, r->rms_final, G(r->rms_final), R, D))) return st;
     if ((st = gemm(s, ts, 1, ts->logits, V, ts->x_final, D, G(r->wcls), D, V, D, R, 1))) return st;
@@ -598,7 +621,7 @@ int enqueue_train(ptmi_model *m, int T, float lr, hipStream_t s) {
     }
     hipLaunchKernelGGL(k_embed_bwd, dim3(R), dim3(256), (size_t)R * sizeof(int), s, ts->tok, ts->d_res, G(r->emb), R, D);
     // ── SGD ──
-    hipLaunchKernelGGL(k_sgd, dim3(blocks_for((long)r->mem_floats, 256)), dim3(256), 0, s, r->mem, ts->gmem, lr,
+    hipLaunchKernelGGL(k_sgd, dim3(blocks_for((long)r->mem_floats, 256)), dim3(256), 0, s, r->mem, ts->gmem, ts->lr,
                        (long)r->mem_floats);
     PTMI_HIP(hipGetLastError());
     return PTMI_OK;
@@ -619,9 +642,34 @@ int ptmi_model_train_step(ptmi_model_t *m, const int *tokens, int T, float lr, f
     for (int i = 0; i < T; i++)
         if (tokens[i] < 0 || tokens[i] >= m->c.vocab) return set_error(PTMI_ERR_ARG, "tokens[%d]=%d out of range", i, tokens[i]);
     hipStream_t s = lib_stream();
-    PTMI_HIP(hipMemcpyAsync(m->train->tok, tokens, (size_t)T * sizeof(int), hipMemcpyHostToDevice, s));
-    int st = enqueue_train(m, T, lr, s);
-    if (st) return st;
+    TrainState *ts = m->train;
+    PTMI_HIP(hipMemcpyAsync(ts->tok, tokens, (size_t)T * sizeof(int), hipMemcpyHostToDevice, s));
+    PTMI_HIP(hipMemcpyAsync(ts->lr, &lr, sizeof(float), hipMemcpyHostToDevice, s));
+    int st;
+    if (ts->eager) {
+        if ((st = enqueue_train(m, T, s))) return st;
+    } else {
+        if (ts->graph_T != T) {                    // capture the step for this T
+            if (ts->exec) (void)hipGraphExecDestroy(ts->exec);
+            if (ts->graph) (void)hipGraphDestroy(ts->graph);
+            ts->exec = nullptr;
+            ts->graph = nullptr;
+            ts->graph_T = 0;
+            PTMI_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            st = enqueue_train(m, T, s);
+            hipGraph_t graph = nullptr;
+            const hipError_t e = hipStreamEndCapture(s, &graph);
+            if (st) { if (graph) (void)hipGraphDestroy(graph); return st; }
+            if (e != hipSuccess) return hip_check(e, "hipStreamEndCapture(train step)");
+            hipGraphExec_t exec = nullptr;
+            const hipError_t e2 = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            if (e2 != hipSuccess) { (void)hipGraphDestroy(graph); return hip_check(e2, "hipGraphInstantiate(train step)"); }
+            ts->graph = graph;
+            ts->exec = exec;
+            ts->graph_T = T;
+        }
+        PTMI_HIP(hipGraphLaunch(ts->exec, s));
+    }
     float l = 0.0f;
     PTMI_HIP(hipMemcpyAsync(&l, m->train->loss, sizeof(float), hipMemcpyDeviceToHost, s));
     PTMI_HIP(hipStreamSynchronize(s));

@@ -66,7 +66,11 @@ def test_backward_input_batched_exact(out_dim, in_dim):
     assert np.array_equal(dX, ref)
 
 
-@pytest.mark.parametrize("M,K,N", [(255, 288, 288), (255, 32000, 288), (300, 77, 130), (1, 5, 3)])
+# Kernel paths: 32x32 tiles (255x288x288, 300x77x130, 1x5x3, 1000x301x900),
+# 32x32 with split K (100x3001x70), 64x64 with split K (K = 32000); the
+# 64x64 NT path for large outputs runs in the 15M training-step tests.
+@pytest.mark.parametrize("M,K,N", [(255, 288, 288), (255, 32000, 288), (300, 77, 130), (1, 5, 3), (100, 3001, 70),
+                                   (1000, 301, 900)])
 def test_sgemm_rect_random_bounded(M, K, N):
     rng = np.random.default_rng(M + K + N)
     A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
