@@ -20,6 +20,26 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_stories110M_hbm_traffic.md")
+
+
+def committed_traffic(role, workload_tag):
+    """HBM bytes per launch of decode kernel `role`, measured by the two
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes whose summary is committed in
+    TRAFFIC_PROFILE (rows `| traffic | <tag> | <role> | ... | <bytes> |`),
+    or None when that file holds no row for this role and workload."""
+    try:
+        lines = open(TRAFFIC_PROFILE).read().splitlines()
+    except OSError:
+        return None
+    for ln in lines:
+        cells = [c.strip() for c in ln.strip().strip("|").split("|")]
+        if len(cells) >= 4 and cells[0] == "traffic" and cells[1] == workload_tag and cells[2] == role:
+            try:
+                return int(cells[-1])
+            except ValueError:
+                return None
+    return None
 
 
 def matvec_bytes(d, n):
@@ -220,6 +240,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=1024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-train", action="store_true", help="skip the training-GEMM leg")
+    ap.add_argument("--only-train", action="store_true",
+                    help="run only the training leg and print its JSON (for counter profiles), not the bench line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -229,6 +251,10 @@ def main():
     import numpy as np
 
     import pitorch_amd as pa
+
+    if args.only_train:
+        print(json.dumps(bench_train(pa)), flush=True)
+        return
 
     name = args.config
     cfg = pa.STORIES[name]
@@ -299,6 +325,10 @@ def main():
               flush=True)
     blob = pa.synth_model(cfg, pa.SEED_MODEL[name])
     cpu = None if args.no_cpu else cpu_baseline(blob, prompt)
+    # measured HBM bytes per launch of the dominant kernel (fetch + write,
+    # counter-calibrated); only for the workload the committed passes ran
+    default_run = args.steps == 1024 and args.profile_steps == 1024 and args.warmup == 32
+    traffic = committed_traffic(dominant, name) if default_run else None
 
     line = {
         "metric": "decode tok/s + matvec HBM GB/s (% peak), stories110M-shape fp32, 1 GPU",
@@ -318,7 +348,7 @@ def main():
                    "batch": 1},
         "roofline": {"bound": "hbm", "kernel": f"decode[{dominant}]", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_launch": dom["bytes_per_launch"], "avg_us": dom["avg_us"]},
+                     "traffic": traffic, "bytes_per_launch": dom["bytes_per_launch"], "avg_us": dom["avg_us"]},
         "step_roofline": {"bytes_per_token": int(step_bytes), "achieved_GBps": round(step_gbs, 1),
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4), "kernel_ms_per_token": round(kernel_ms, 4)},
         "matvec_sweep": sweep,
