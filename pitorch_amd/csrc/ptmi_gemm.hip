@@ -28,6 +28,7 @@ namespace {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int BK = 32;
+constexpr int kRing64 = 2, kRing32 = 2;   // K tiles in flight per block tile size
 
 struct GemmArgs {
     const float *A; long lda;
@@ -46,14 +47,14 @@ struct GemmArgs {
 // predicated scalars at ragged edges).  KMAJOR: the operand is stored with
 // k as the row index (A^T for TN, B for NN/TN); otherwise k is the
 // contiguous index.
-//   KMAJOR:  thread -> (k = tid/8,         idx = E*(tid%8) + c)
+//   KMAJOR:  thread -> (k = tid/(R/E),     idx = E*(tid%(R/E)) + c)
 //   !KMAJOR: thread -> (idx = tid/(32/E),  k = E*(tid%(32/E)) + c)
 template <bool KMAJOR, int R>
 __device__ __forceinline__ void load_tile(const float *P, long ld, int idx_lim, int i0, int k0, int kend, bool vec,
                                           int tid, float (&r)[R * BK / 256]) {
     constexpr int E = R * BK / 256;
     if (KMAJOR) {
-        const int k = k0 + tid / 8, i = i0 + E * (tid % 8);
+        const int k = k0 + tid / (R / E), i = i0 + E * (tid % (R / E));
         const bool kin = k < kend;
         const float *p = P + (long)min(k, kend - 1) * ld;
         if (vec && i + E - 1 < idx_lim) {
@@ -95,7 +96,7 @@ template <bool KMAJOR, int R>
 __device__ __forceinline__ void store_tile(float (*S)[R + 4], int tid, const float (&r)[R * BK / 256]) {
     constexpr int E = R * BK / 256;
     if (KMAJOR) {
-        const int k = tid / 8, i = E * (tid % 8);
+        const int k = tid / (R / E), i = E * (tid % (R / E));
 #pragma unroll
         for (int c = 0; c < E; c++) S[k][i + c] = r[c];
     } else {
@@ -105,7 +106,7 @@ __device__ __forceinline__ void store_tile(float (*S)[R + 4], int tid, const flo
     }
 }
 
-template <bool AT, bool BT, int TM, int TN>
+template <bool AT, bool BT, int TM, int TN, int P>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     constexpr int FM = TM / 32, FN = TN / 32;          // 16x16 MFMA blocks per wave
     constexpr int EA = TM * BK / 256, EB = TN * BK / 256;
@@ -125,14 +126,16 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    float ra0[EA], rb0[EB], ra1[EA], rb1[EB];
-    auto load = [&](int s, float (&ra)[EA], float (&rb)[EB]) {
-        load_tile<AT, TM>(g.A, g.lda, g.M, m0, kb + s * BK, kend, g.a_vec, tid, ra);
-        load_tile<!BT, TN>(g.B, g.ldb, g.N, n0, kb + s * BK, kend, g.b_vec, tid, rb);
+    // P K tiles in flight in a register ring (tile t in slot t % P); the
+    // loop is unrolled by P so every slot index is a compile-time constant.
+    float ra[P][EA], rb[P][EB];
+    auto load = [&](int s, float (&xa)[EA], float (&xb)[EB]) {
+        load_tile<AT, TM>(g.A, g.lda, g.M, m0, kb + s * BK, kend, g.a_vec, tid, xa);
+        load_tile<!BT, TN>(g.B, g.ldb, g.N, n0, kb + s * BK, kend, g.b_vec, tid, xb);
     };
-    auto store = [&](int s, const float (&ra)[EA], const float (&rb)[EB]) {
-        store_tile<AT, TM>(As[s & 1], tid, ra);
-        store_tile<!BT, TN>(Bs[s & 1], tid, rb);
+    auto store = [&](int s, const float (&xa)[EA], const float (&xb)[EB]) {
+        store_tile<AT, TM>(As[s & 1], tid, xa);
+        store_tile<!BT, TN>(Bs[s & 1], tid, xb);
     };
     auto compute = [&](int s) {
         const int buf = s & 1;
@@ -150,25 +153,25 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
         }
     };
-    // One K step: tile s is in LDS, tile s+1 in registers `cur`; tile s+2
-    // goes into registers `nxt` (free: their tile went to LDS last step).
-    auto step = [&](int s, float (&cra)[EA], float (&crb)[EB], float (&nra)[EA], float (&nrb)[EB]) {
-        if (s + 2 < nk) load(s + 2, nra, nrb);
-        compute(s);
-        if (s + 1 < nk) store(s + 1, cra, crb);
-        __syncthreads();
-    };
 
-    if (nk > 0) {
-        load(0, ra0, rb0);
-        store(0, ra0, rb0);
-    }
-    if (nk > 1) load(1, ra1, rb1);
+#pragma unroll
+    for (int t = 0; t < P; t++)
+        if (t < nk) load(t, ra[t], rb[t]);
+    if (nk > 0) store(0, ra[0], rb[0]);
     __syncthreads();
-    // register slots alternate: tile s+1 sits in slot (s+1)&1
-    for (int s = 0; s < nk; s += 2) {
-        step(s, ra1, rb1, ra0, rb0);
-        if (s + 1 < nk) step(s + 1, ra0, rb0, ra1, rb1);
+    // Step s: tile s is in LDS; its register slot (s % P) is free, so tile
+    // s+P is fetched into it; tile s+1 goes to the other LDS buffer.
+    for (int s0 = 0; s0 < nk; s0 += P) {
+#pragma unroll
+        for (int u = 0; u < P; u++) {
+            const int s = s0 + u;
+            if (s < nk) {
+                if (s + P < nk) load(s + P, ra[u], rb[u]);
+                compute(s);
+                if (s + 1 < nk) store(s + 1, ra[(u + 1) % P], rb[(u + 1) % P]);
+                __syncthreads();
+            }
+        }
     }
 
     // C[4*(l/16)+r][l%16] of each 16x16 block
@@ -248,13 +251,13 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
     if (gy > 65535) return set_error(PTMI_ERR_ARG, "gemm: M too large");
     dim3 grid(gx, gy, splits);
     if (big) {
-        if (op == 0) hipLaunchKernelGGL((k_gemm<false, false, 64, 64>), grid, dim3(256), 0, s, g);
-        else if (op == 1) hipLaunchKernelGGL((k_gemm<true, false, 64, 64>), grid, dim3(256), 0, s, g);
-        else hipLaunchKernelGGL((k_gemm<false, true, 64, 64>), grid, dim3(256), 0, s, g);
+        if (op == 0) hipLaunchKernelGGL((k_gemm<false, false, 64, 64, kRing64>), grid, dim3(256), 0, s, g);
+        else if (op == 1) hipLaunchKernelGGL((k_gemm<true, false, 64, 64, kRing64>), grid, dim3(256), 0, s, g);
+        else hipLaunchKernelGGL((k_gemm<false, true, 64, 64, kRing64>), grid, dim3(256), 0, s, g);
     } else {
-        if (op == 0) hipLaunchKernelGGL((k_gemm<false, false, 32, 32>), grid, dim3(256), 0, s, g);
-        else if (op == 1) hipLaunchKernelGGL((k_gemm<true, false, 32, 32>), grid, dim3(256), 0, s, g);
-        else hipLaunchKernelGGL((k_gemm<false, true, 32, 32>), grid, dim3(256), 0, s, g);
+        if (op == 0) hipLaunchKernelGGL((k_gemm<false, false, 32, 32, kRing32>), grid, dim3(256), 0, s, g);
+        else if (op == 1) hipLaunchKernelGGL((k_gemm<true, false, 32, 32, kRing32>), grid, dim3(256), 0, s, g);
+        else hipLaunchKernelGGL((k_gemm<false, true, 32, 32, kRing32>), grid, dim3(256), 0, s, g);
     }
     PTMI_HIP(hipGetLastError());
     if (splits > 1) {
