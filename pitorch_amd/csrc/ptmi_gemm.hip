@@ -42,6 +42,13 @@ struct GemmArgs {
     bool a_vec, b_vec;     // 16-byte aligned rows: float4 global loads
 };
 
+// One GEMM of a grouped launch: its arguments and its range of tiles.
+struct GemmGroupDesc {
+    GemmArgs g;
+    int tiles_n;           // tiles along N
+    int tile0;             // first block of this GEMM in the grouped grid
+};
+
 // One operand tile (R rows of the M or N side x 32 k) per K step; each of
 // the 256 threads moves E = R*32/256 floats (8 or 4) as float4s (or
 // predicated scalars at ragged edges).  KMAJOR: the operand is stored with
@@ -106,8 +113,9 @@ __device__ __forceinline__ void store_tile(float (*S)[R + 4], int tid, const flo
     }
 }
 
+// One TMxTN output tile of g at (m0, n0) over K range split z.
 template <bool AT, bool BT, int TM, int TN, int P>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int z) {
     constexpr int FM = TM / 32, FN = TN / 32;          // 16x16 MFMA blocks per wave
     constexpr int EA = TM * BK / 256, EB = TN * BK / 256;
     __shared__ float As[2][BK][TM + 4];
@@ -115,8 +123,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int li = lane & 15, lk = lane >> 4;
-    const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
-    const int kb = blockIdx.z * g.k_per_split;
+    const int kb = z * g.k_per_split;
     const int kend = min(g.K, kb + g.k_per_split);
     const int nk = kb < kend ? (kend - kb + BK - 1) / BK : 0;
 
@@ -187,7 +194,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
                 if (m >= g.M) continue;
                 const float v = acc[i][j][r];
                 if (g.partial) {
-                    g.partial[((long)blockIdx.z * g.M + m) * g.N + n] = v;
+                    g.partial[((long)z * g.M + m) * g.N + n] = v;
                 } else {
                     const long o = (long)m * g.ldc + n;
                     g.C[o] = g.accumulate ? g.Cin[o] + v : v;
@@ -195,6 +202,23 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
             }
         }
     }
+}
+
+template <bool AT, bool BT, int TM, int TN, int P>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
+    gemm_tile<AT, BT, TM, TN, P>(g, blockIdx.y * TM, blockIdx.x * TN, blockIdx.z);
+}
+
+// Grouped TN GEMMs (32x32 tiles, whole K): block b runs tile
+// b - d.tile0 of the descriptor d whose tile range holds b.
+template <int TM, int TN>
+__global__ __launch_bounds__(256) void k_gemm_tn_group(const GemmGroupDesc *d, int n) {
+    const int b = blockIdx.x;
+    int i = 0;
+    while (i + 1 < n && d[i + 1].tile0 <= b) i++;
+    const GemmGroupDesc &e = d[i];
+    const int t = b - e.tile0;
+    gemm_tile<true, false, TM, TN, kRing32>(e.g, (t / e.tiles_n) * TM, (t % e.tiles_n) * TN, 0);
 }
 
 // C = (Cin +) sum_z partial[z], z ascending.
@@ -266,6 +290,37 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
                            ldc, M, N, accumulate);
         PTMI_HIP(hipGetLastError());
     }
+    return PTMI_OK;
+}
+
+size_t gemm_group_desc_bytes(int n) { return sizeof(GemmGroupDesc) * (size_t)n; }
+
+int gemm_tn_group_prepare(const TnGemm *list, int n, void *host_desc, int *tiles_total) {
+    GemmGroupDesc *d = static_cast<GemmGroupDesc *>(host_desc);
+    int t = 0;
+    for (int i = 0; i < n; i++) {
+        const TnGemm &e = list[i];
+        if (e.M <= 0 || e.N <= 0 || e.K <= 0 || !e.A || !e.B || !e.C || e.lda < e.M || e.ldb < e.N || e.ldc < e.N)
+            return set_error(PTMI_ERR_ARG, "grouped gemm %d: bad shape", i);
+        GemmArgs &g = d[i].g;
+        g = GemmArgs{};
+        g.A = e.A; g.lda = e.lda; g.B = e.B; g.ldb = e.ldb; g.C = e.C; g.ldc = e.ldc; g.Cin = e.C;
+        g.M = e.M; g.N = e.N; g.K = e.K; g.accumulate = 1; g.partial = nullptr; g.k_per_split = e.K;
+        g.a_vec = al16(e.A) && e.lda % 4 == 0;
+        g.b_vec = al16(e.B) && e.ldb % 4 == 0;
+        d[i].tiles_n = (e.N + 31) / 32;
+        d[i].tile0 = t;
+        t += d[i].tiles_n * ((e.M + 31) / 32);
+    }
+    *tiles_total = t;
+    return PTMI_OK;
+}
+
+int launch_gemm_tn_group(const void *dev_desc, int n, int tiles_total, hipStream_t s) {
+    if (n <= 0 || tiles_total <= 0) return PTMI_OK;
+    hipLaunchKernelGGL((k_gemm_tn_group<32, 32>), dim3((unsigned)tiles_total), dim3(256), 0, s,
+                       static_cast<const GemmGroupDesc *>(dev_desc), n);
+    PTMI_HIP(hipGetLastError());
     return PTMI_OK;
 }
 

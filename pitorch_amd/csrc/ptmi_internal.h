@@ -253,6 +253,19 @@ int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0 = nullptr, hipEve
 int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc, int M, int N,
                 int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s, const float *Cin = nullptr);
 
+// Grouped C[M,N] += A^T.B GEMMs (TN; A stored [K][M]), one launch of 32x32
+// tiles over all of them.  prepare fills host_desc (gemm_group_desc_bytes(n)
+// bytes); the caller copies it to device memory for the launch.
+struct TnGemm {
+    const float *A; long lda;
+    const float *B; long ldb;
+    float *C; long ldc;
+    int M, N, K;
+};
+size_t gemm_group_desc_bytes(int n);
+int gemm_tn_group_prepare(const TnGemm *list, int n, void *host_desc, int *tiles_total);
+int launch_gemm_tn_group(const void *dev_desc, int n, int tiles_total, hipStream_t s);
+
 // ── library state ───────────────────────────────────────────────────────
 struct Config {
     int dim, hidden, n_layers, n_heads, n_kv_heads, vocab, seq_len;

@@ -20,6 +20,7 @@
 #include <cmath>
 #include <cstring>
 #include <new>
+#include <vector>
 
 namespace ptmi {
 
@@ -29,7 +30,15 @@ struct TrainState {
     int *tok = nullptr;
     float *res, *res_att, *xb_att, *qkv, *att, *att_out, *xb_ffn, *h13, *sh, *x_final, *logits;
     float *gmem;
-    float *d_res, *d_xb, *d_sh, *d_h13, *d_aout, *d_q, *d_k, *d_v, *d_qkv, *ds, *row_inv, *row_loss, *loss;
+    // Backward buffers.  What the deferred weight-gradient launches read is
+    // written once per step: d_res and d_xb by version (one per RMSNorm
+    // backward, 2L+1, plus d_res's zero start), d_h13, sh and d_qkv per
+    // layer, the RMSNorm inverse norms per norm.
+    float *d_res, *d_xb, *d_sh, *d_h13, *shb, *d_aout, *d_q, *d_k, *d_v, *d_qkv, *ds, *row_inv, *row_loss, *loss;
+    // Descriptor tables of the two grouped launches (device; built per T).
+    void *dw_desc;
+    float *nd_desc;
+    int desc_T = 0, dw_tiles = 0, n_dw = 0;
     float *ws;
     size_t ws_floats = 0;
     float *lr;                  // device copy of the step's learning rate
@@ -288,9 +297,10 @@ __global__ __launch_bounds__(256) void k_loss_reduce(const float *row_loss, int 
 
 // ── backward kernels ─────────────────────────────────────────────────────
 
-// rmsnorm_backward (pt_backward_ops.c:4-30), the d_x half, per row.
-__global__ __launch_bounds__(256) void k_rmsnorm_bwd_rows(float *d_x, const float *d_o, const float *x, const float *w,
-                                                          float *inv_out, int D) {
+// rmsnorm_backward (pt_backward_ops.c:4-30), the d_x half, per row:
+// d_out = d_in + (the reference's in-place d_x += term).
+__global__ __launch_bounds__(256) void k_rmsnorm_bwd_rows(float *d_out, const float *d_in, const float *d_o,
+                                                          const float *x, const float *w, float *inv_out, int D) {
     __shared__ float red[4];
     const long r = (long)blockIdx.x * D;
     float ss = 0.0f, dot = 0.0f;
@@ -305,27 +315,32 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd_rows(float *d_x, const floa
     const float inv = 1.0f / d_sqrtf(ss);
     const float cd = inv * inv * inv / (float)D * dot;
     if (threadIdx.x == 0) inv_out[blockIdx.x] = inv;
-    for (int i = threadIdx.x; i < D; i += 256) d_x[r + i] += inv * d_o[r + i] * w[i] - cd * x[r + i];
+    for (int i = threadIdx.x; i < D; i += 256) d_out[r + i] = d_in[r + i] + (inv * d_o[r + i] * w[i] - cd * x[r + i]);
 }
 
-// The d_w half: d_w[i] += sum_t d_o[t][i]*x[t][i]*inv[t]; 64 columns per
-// block, 16 interleaved row slices summed in LDS.
-__global__ __launch_bounds__(1024) void k_rmsnorm_bwd_dw(float *d_w, const float *d_o, const float *x,
-                                                         const float *inv, int R, int D) {
+// The d_w half of every RMSNorm of the step in one launch: for norm
+// j = blockIdx.x / cb, d_w[i] += sum_t d_o[t][i]*x[t][i]*inv[t]; 64 columns
+// per block, 16 interleaved row slices summed in LDS.
+struct NormDw {
+    float *d_w;
+    const float *d_o, *x, *inv;
+};
+__global__ __launch_bounds__(1024) void k_rmsnorm_bwd_dw(const NormDw *nd, int cb, int R, int D) {
     __shared__ float part[16][64];
+    const NormDw e = nd[blockIdx.x / cb];
     const int c = threadIdx.x & 63, sl = threadIdx.x >> 6;
-    const int i = blockIdx.x * 64 + c;
+    const int i = (blockIdx.x % cb) * 64 + c;
     float acc = 0.0f;
     if (i < D) {
 #pragma unroll 4
-        for (int t = sl; t < R; t += 16) acc += d_o[(long)t * D + i] * x[(long)t * D + i] * inv[t];
+        for (int t = sl; t < R; t += 16) acc += e.d_o[(long)t * D + i] * e.x[(long)t * D + i] * e.inv[t];
     }
     part[sl][c] = acc;
     __syncthreads();
     if (sl == 0 && i < D) {
-        float g = d_w[i];
+        float g = e.d_w[i];
         for (int k = 0; k < 16; k++) g += part[k][c];
-        d_w[i] = g;
+        e.d_w[i] = g;
     }
 }
 
@@ -486,12 +501,14 @@ int train_create(ptmi_model *m) {
         (L + 1) * T * D, L * T * D, L * T * D, L * T * QS, L * NH * T * T, L * T * D, L * T * D, L * T * 2 * H,
         T * H, T * D, T * V,                                   // forward
         m->res->mem_floats,                                    // grads
-        T * D, T * D, T * H, T * 2 * H, T * D, T * D, T * KV, T * KV, T * QS, NH * T * T, T, T, 64,
-        ts->ws_floats, T, 1};
+        (2 * L + 2) * T * D, (2 * L + 1) * T * D, T * H, L * T * 2 * H, L * T * H, T * D, T * D, T * KV, T * KV,
+        L * T * QS, NH * T * T, (2 * L + 1) * T, T, 64, ts->ws_floats, T, 1,
+        (gemm_group_desc_bytes(4 * (int)L + 1) + 3) / 4, (sizeof(NormDw) * (2 * L + 1) + 3) / 4};
+    float *dw_desc = nullptr;
     float **dst[] = {&ts->res, &ts->res_att, &ts->xb_att, &ts->qkv, &ts->att, &ts->att_out, &ts->xb_ffn, &ts->h13,
                      &ts->sh, &ts->x_final, &ts->logits, &ts->gmem, &ts->d_res, &ts->d_xb, &ts->d_sh, &ts->d_h13,
-                     &ts->d_aout, &ts->d_q, &ts->d_k, &ts->d_v, &ts->d_qkv, &ts->ds, &ts->row_inv, &ts->row_loss,
-                     &ts->loss, &ts->ws, (float **)&ts->tok, &ts->lr};
+                     &ts->shb, &ts->d_aout, &ts->d_q, &ts->d_k, &ts->d_v, &ts->d_qkv, &ts->ds, &ts->row_inv,
+                     &ts->row_loss, &ts->loss, &ts->ws, (float **)&ts->tok, &ts->lr, &dw_desc, &ts->nd_desc};
     const int nbuf = (int)(sizeof(sizes) / sizeof(sizes[0]));
     size_t total = 0;
     for (int i = 0; i < nbuf; i++) total += align_up(sizes[i], 64);
@@ -499,6 +516,7 @@ int train_create(ptmi_model *m) {
     if (e != hipSuccess) { delete ts; return hip_check(e, "hipMalloc(training state)"); }
     size_t o = 0;
     for (int i = 0; i < nbuf; i++) { *dst[i] = ts->mem + o; o += align_up(sizes[i], 64); }
+    ts->dw_desc = dw_desc;
     e = hipMemsetAsync(ts->mem, 0, total * sizeof(float), lib_stream());
     if (e == hipSuccess) e = hipStreamSynchronize(lib_stream());
     if (e != hipSuccess) { (void)hipFree(ts->mem); delete ts; return hip_check(e, "zero training state"); }
@@ -528,11 +546,50 @@ void fill0(hipStream_t s, float *p, long n) {
     hipLaunchKernelGGL(k_fill0, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n);
 }
 
-int rmsnorm_bwd(hipStream_t s, TrainState *ts, float *d_x, const float *d_o, const float *x, const float *w,
-                float *d_w, int R, int D) {
-    hipLaunchKernelGGL(k_rmsnorm_bwd_rows, dim3(R), dim3(256), 0, s, d_x, d_o, x, w, ts->row_inv, D);
-    hipLaunchKernelGGL(k_rmsnorm_bwd_dw, dim3(blocks_for(D, 64)), dim3(1024), 0, s, d_w, d_o, x, ts->row_inv, R, D);
-    PTMI_HIP(hipGetLastError());
+// Descriptor tables of the grouped weight-gradient launches for this T:
+// per layer dW2 += d_res^T sh, dW13 += d_h13^T x_ffn, dWo += d_res^T att_out,
+// dWqkv += d_qkv^T x_att, plus the classifier's dWcls += d_logits^T x_final;
+// and the 2L+1 RMSNorm dW reductions, in the d_res version order the dX
+// chain produces (final norm, then per layer from the last: ffn, att).
+int train_descriptors(ptmi_model *m, int T) {
+    TrainState *ts = m->train;
+    if (ts->desc_T == T) return PTMI_OK;
+    const Resident *r = m->res;
+    const Config &c = m->c;
+    const int D = c.dim, H = c.hidden, L = c.n_layers, V = c.vocab, KV = c.kv_dim, QS = D + 2 * KV, R = T - 1;
+    const long TD = (long)T * D;
+    auto G = [&](const float *p) { return ts->gmem + (p - r->mem); };
+    auto dres = [&](int k) { return ts->d_res + (long)k * TD; };
+    auto dxb = [&](int k) { return ts->d_xb + (long)k * TD; };
+    std::vector<TnGemm> g;
+    std::vector<NormDw> nd;
+    g.push_back({ts->logits, V, ts->x_final, D, G(r->wcls), D, V, D, R});
+    nd.push_back({G(r->rms_final), dxb(0), ts->res + L * TD, ts->row_inv});
+    int v = 1;
+    for (int l = L - 1; l >= 0; l--) {
+        const float *xa = ts->xb_att + l * TD, *xf = ts->xb_ffn + l * TD, *ao = ts->att_out + l * TD;
+        const float *rin = ts->res + l * TD, *rmid = ts->res_att + l * TD;
+        const float *w2 = r->w2 + (long)l * D * H, *w13 = r->w13 + (long)l * 2 * H * D;
+        const float *wo = r->wo + (long)l * D * D, *wqkv = r->wqkv + (long)l * QS * D;
+        const float *dh13 = ts->d_h13 + (long)l * T * 2 * H, *shb = ts->shb + (long)l * T * H;
+        const float *dqkv = ts->d_qkv + (long)l * T * QS;
+        g.push_back({dres(v), D, shb, H, G(w2), H, D, H, R});                  // FFN reads d_res[v]
+        g.push_back({dh13, 2 * H, xf, D, G(w13), D, 2 * H, D, R});
+        nd.push_back({G(r->rms_ffn + (long)l * D), dxb(v), rmid, ts->row_inv + (long)v * T});
+        v++;
+        g.push_back({dres(v), D, ao, D, G(wo), D, D, D, R});                   // Wo reads d_res[v+1]
+        g.push_back({dqkv, QS, xa, D, G(wqkv), D, QS, D, R});
+        nd.push_back({G(r->rms_att + (long)l * D), dxb(v), rin, ts->row_inv + (long)v * T});
+        v++;
+    }
+    std::vector<char> host(gemm_group_desc_bytes((int)g.size()));
+    int tiles = 0, st;
+    if ((st = gemm_tn_group_prepare(g.data(), (int)g.size(), host.data(), &tiles))) return st;
+    PTMI_HIP(hipMemcpy(ts->dw_desc, host.data(), host.size(), hipMemcpyHostToDevice));
+    PTMI_HIP(hipMemcpy(ts->nd_desc, nd.data(), nd.size() * sizeof(NormDw), hipMemcpyHostToDevice));
+    ts->n_dw = (int)g.size();
+    ts->dw_tiles = tiles;
+    ts->desc_T = T;
     return PTMI_OK;
 }
 
@@ -582,44 +639,60 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     PTMI_HIP(hipGetLastError());
 
     // ── backward ── (ts->logits now holds d_logits)
-    fill0(s, ts->d_res, TD);
-    if ((st = gemm(s, ts, 0, ts->logits, V, r->wcls, D, ts->d_xb, D, R, D, V, 0))) return st;
-    if ((st = rmsnorm_bwd(s, ts, ts->d_res, ts->d_xb, ts->res + L * TD, r->rms_final, G(r->rms_final), R, D))) return st;
-    if ((st = gemm(s, ts, 1, ts->logits, V, ts->x_final, D, G(r->wcls), D, V, D, R, 1))) return st;
+    // The dX chain runs here; the weight gradients (25 TN GEMMs and 2L+1
+    // RMSNorm dW reductions) only read buffers written once per step, so
+    // they run afterwards as two grouped launches (descriptor tables built
+    // by train_descriptors for this T).
+    auto dres = [&](int k) { return ts->d_res + (long)k * TD; };
+    auto dxb = [&](int k) { return ts->d_xb + (long)k * TD; };
+    int v = 0;                                            // d_res version
+    auto norm_bwd = [&](const float *x, const float *w) {
+        // d_res[v+1] = d_res[v] + rmsnorm_backward(d_xb[v]); inverse norms kept per norm
+        hipLaunchKernelGGL(k_rmsnorm_bwd_rows, dim3(R), dim3(256), 0, s, dres(v + 1), dres(v), dxb(v), x, w,
+                           ts->row_inv + (long)v * T, D);
+        v++;
+    };
+    fill0(s, dres(0), (long)R * D);
+    if ((st = gemm(s, ts, 0, ts->logits, V, r->wcls, D, dxb(0), D, R, D, V, 0))) return st;
+    norm_bwd(ts->res + L * TD, r->rms_final);
     for (int l = L - 1; l >= 0; l--) {
         const float *rin = ts->res + l * TD, *rmid = ts->res_att + l * TD;
-        const float *xa = ts->xb_att + l * TD, *qkv = ts->qkv + (long)l * T * QS, *att = ts->att + (long)l * NH * T * T;
-        const float *ao = ts->att_out + l * TD, *xf = ts->xb_ffn + l * TD, *h13 = ts->h13 + (long)l * T * 2 * H;
+        const float *qkv = ts->qkv + (long)l * T * QS, *att = ts->att + (long)l * NH * T * T;
+        const float *h13 = ts->h13 + (long)l * T * 2 * H;
         const float *w2 = r->w2 + (long)l * D * H, *w13 = r->w13 + (long)l * 2 * H * D;
         const float *wo = r->wo + (long)l * D * D, *wqkv = r->wqkv + (long)l * QS * D;
+        float *dh13 = ts->d_h13 + (long)l * T * 2 * H, *shb = ts->shb + (long)l * T * H;
+        float *dqkv = ts->d_qkv + (long)l * T * QS;
         // FFN
-        if ((st = gemm(s, ts, 0, ts->d_res, D, w2, H, ts->d_sh, H, R, H, D, 0))) return st;
-        hipLaunchKernelGGL(k_swiglu_bwd, dim3(blocks_for((long)R * H, 256)), dim3(256), 0, s, h13, ts->d_sh, ts->d_h13,
-                           ts->sh, (long)R * H, H);
-        if ((st = gemm(s, ts, 1, ts->d_res, D, ts->sh, H, G(w2), H, D, H, R, 1))) return st;
-        if ((st = gemm(s, ts, 0, ts->d_h13, 2 * H, w13, D, ts->d_xb, D, R, D, 2 * H, 0))) return st;
-        if ((st = gemm(s, ts, 1, ts->d_h13, 2 * H, xf, D, G(w13), D, 2 * H, D, R, 1))) return st;
-        if ((st = rmsnorm_bwd(s, ts, ts->d_res, ts->d_xb, rmid, r->rms_ffn + (long)l * D,
-                              G(r->rms_ffn + (long)l * D), R, D))) return st;
+        if ((st = gemm(s, ts, 0, dres(v), D, w2, H, ts->d_sh, H, R, H, D, 0))) return st;
+        hipLaunchKernelGGL(k_swiglu_bwd, dim3(blocks_for((long)R * H, 256)), dim3(256), 0, s, h13, ts->d_sh, dh13,
+                           shb, (long)R * H, H);
+        if ((st = gemm(s, ts, 0, dh13, 2 * H, w13, D, dxb(v), D, R, D, 2 * H, 0))) return st;
+        norm_bwd(rmid, r->rms_ffn + (long)l * D);
         // Wo
-        if ((st = gemm(s, ts, 0, ts->d_res, D, wo, D, ts->d_aout, D, R, D, D, 0))) return st;
-        if ((st = gemm(s, ts, 1, ts->d_res, D, ao, D, G(wo), D, D, D, R, 1))) return st;
+        if ((st = gemm(s, ts, 0, dres(v), D, wo, D, ts->d_aout, D, R, D, D, 0))) return st;
         // attention
         hipLaunchKernelGGL(attn_bwd_rows, dim3(R, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ts->d_aout, ts->ds, ts->d_q,
                            T, D, QS, KV, hd, kv_mul, scale);
         hipLaunchKernelGGL(attn_bwd_cols, dim3(R, NH), dim3(kAttnThreads), 2 * att_lds, s, qkv, att, ts->ds, ts->d_aout,
-                           ts->d_k, ts->d_v,
-                           T, R, D, QS, KV, hd, kv_mul);
+                           ts->d_k, ts->d_v, T, R, D, QS, KV, hd, kv_mul);
         hipLaunchKernelGGL(k_rope_bwd_pack, dim3(blocks_for((long)R * D / 2, 256)), dim3(256), 0, s, ts->d_q, ts->d_k,
-                           ts->d_v, ts->d_qkv, R, D, KV, QS, hd);
+                           ts->d_v, dqkv, R, D, KV, QS, hd);
         PTMI_HIP(hipGetLastError());
         // QKV
-        if ((st = gemm(s, ts, 0, ts->d_qkv, QS, wqkv, D, ts->d_xb, D, R, D, QS, 0))) return st;
-        if ((st = gemm(s, ts, 1, ts->d_qkv, QS, xa, D, G(wqkv), D, QS, D, R, 1))) return st;
-        if ((st = rmsnorm_bwd(s, ts, ts->d_res, ts->d_xb, rin, r->rms_att + (long)l * D,
-                              G(r->rms_att + (long)l * D), R, D))) return st;
+        if ((st = gemm(s, ts, 0, dqkv, QS, wqkv, D, dxb(v), D, R, D, QS, 0))) return st;
+        norm_bwd(rin, r->rms_att + (long)l * D);
     }
-    hipLaunchKernelGGL(k_embed_bwd, dim3(R), dim3(256), (size_t)R * sizeof(int), s, ts->tok, ts->d_res, G(r->emb), R, D);
+    PTMI_HIP(hipGetLastError());
+    // weight gradients: every TN GEMM in one launch, every RMSNorm dW in one
+    if ((st = launch_gemm_tn_group(ts->dw_desc, ts->n_dw, ts->dw_tiles, s))) return st;
+    {
+        const int cb = (D + 63) / 64;
+        hipLaunchKernelGGL(k_rmsnorm_bwd_dw, dim3((unsigned)((2 * L + 1) * cb)), dim3(1024), 0, s,
+                           reinterpret_cast<const NormDw *>(ts->nd_desc), cb, R, D);
+        PTMI_HIP(hipGetLastError());
+    }
+    hipLaunchKernelGGL(k_embed_bwd, dim3(R), dim3(256), (size_t)R * sizeof(int), s, ts->tok, dres(v), G(r->emb), R, D);
     // ── SGD ──
     hipLaunchKernelGGL(k_sgd, dim3(blocks_for((long)r->mem_floats, 256)), dim3(256), 0, s, r->mem, ts->gmem, ts->lr,
                        (long)r->mem_floats);
@@ -645,7 +718,8 @@ int ptmi_model_train_step(ptmi_model_t *m, const int *tokens, int T, float lr, f
     TrainState *ts = m->train;
     PTMI_HIP(hipMemcpyAsync(ts->tok, tokens, (size_t)T * sizeof(int), hipMemcpyHostToDevice, s));
     PTMI_HIP(hipMemcpyAsync(ts->lr, &lr, sizeof(float), hipMemcpyHostToDevice, s));
-    int st;
+    int st = train_descriptors(m, T);
+    if (st) return st;
     if (ts->eager) {
         if ((st = enqueue_train(m, T, s))) return st;
     } else {
