@@ -36,10 +36,11 @@ def tensor_slices(cfg):
     return out, o
 
 
-# head_dim 16 / 32 / 32 / 80 (8-, 8-, 8- and 32-lane attention rows); vocab
-# 1501 exercises the loss kernel's scalar tail (vocab % 4 != 0).
+# head_dim 16 / 32 / 32 / 80 / 128 (8-, 8-, 8-, 32- and 32-lane attention
+# rows); vocab 1501 exercises the loss kernel's scalar tail (vocab % 4 != 0).
 @pytest.mark.parametrize("cfg,T", [((64, 160, 2, 4, 4, 512, 32), 16), ((96, 256, 1, 3, 3, 1000, 64), 64),
-                                   ((64, 128, 2, 2, 2, 300, 8), 2), ((160, 256, 1, 2, 2, 1501, 24), 24)])
+                                   ((64, 128, 2, 2, 2, 300, 8), 2), ((160, 256, 1, 2, 2, 1501, 24), 24),
+                                   ((128, 256, 1, 1, 1, 1300, 160), 144)])
 def test_one_step_matches_oracle(cfg, T):
     blob = pa.synth_model(cfg, 11, 0.05)
     tokens = pa.seed_tokens(5, T, cfg[5])
