@@ -78,9 +78,11 @@ SWEEP = [(288, 288), (768, 288), (288, 768), (32000, 288), (2048, 768), (768, 20
 
 def matvec_sweep(pa, footprint_mb=1536, reps_max=2048):
     """Config 2: standalone y = W x at each shape, W rotated through a
-    footprint well above the 256 MB MALL so every launch reads HBM; HIP
-    events around the whole batch of launches on the library stream."""
-    from pitorch_amd._hip import DeviceArray, Event
+    footprint well above the 256 MB MALL so every launch reads HBM.  The
+    launches are captured back to back in a hipGraph on the library stream
+    and timed with HIP events around its replay, so host launch cost is not
+    in the figure."""
+    from pitorch_amd._hip import DeviceArray, Event, Graph
     L = pa.load_ptmi()
     stream = L.ptmi_stream()
     big = DeviceArray(footprint_mb * (1 << 20) // 4)
@@ -91,17 +93,62 @@ def matvec_sweep(pa, footprint_mb=1536, reps_max=2048):
         stride = (d * n + 63) // 64 * 64
         copies = max(1, min(big.n // stride, reps_max))
         pa._ffi.check(L.ptmi_matvec_dev(big.ptr, n, x.ptr, y.ptr, d, n, None))
+        pa._ffi.check(L.ptmi_sync())
+
+        def enqueue():
+            for i in range(copies):
+                pa._ffi.check(L.ptmi_matvec_dev(big.ptr + 4 * i * stride, n, x.ptr, y.ptr, d, n, stream))
+
+        g = Graph(stream, enqueue)
+        g.launch()
         e0, e1 = Event(), Event()
         e0.record(stream)
-        for i in range(copies):
-            pa._ffi.check(L.ptmi_matvec_dev(big.ptr + 4 * i * stride, n, x.ptr, y.ptr, d, n, None))
+        g.launch()
         e1.record(stream)
         us = e0.elapsed_ms(e1) * 1e3 / copies
+        g.free()
         gbs = matvec_bytes(d, n) / (us * 1e-6) / 1e9
         out.append({"d": d, "n": n, "us": round(us, 2), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
     for a in (big, x, y):
         a.free()
     return out
+
+
+def cpu_extra():
+    """The reference's own host code (oracle/_ref, -O2 -ffp-contract=off,
+    1 thread) on the other measured paths: its smatvec_cpu at every sweep
+    shape (~0.2 s each) and one pt_train_step of the 15M training
+    configuration (T=256, same blob and ids; ~10 s)."""
+    import ctypes
+
+    import numpy as np
+
+    import pitorch_amd as pa
+    from tests._oracle import P, ref
+    R = ref()
+    if R is None:
+        return None
+    sweep = []
+    for d, n in SWEEP:
+        W = pa.seed_uniform(4, d * n)
+        xx = pa.seed_uniform(5, n)
+        yy = np.zeros(d, np.float32)
+        k, t0 = 0, time.perf_counter()
+        while k < 2 or time.perf_counter() - t0 < 0.2:
+            R.smatvec_cpu(P(W), P(xx), P(yy), d, n)
+            k += 1
+        us = (time.perf_counter() - t0) * 1e6 / k
+        sweep.append({"d": d, "n": n, "us": round(us, 1), "GBps": round(matvec_bytes(d, n) / (us * 1e-6) / 1e9, 2)})
+    cfg = pa.STORIES["stories15M"]
+    blob = pa.synth_model(cfg, pa.SEED_MODEL["stories15M"])
+    tok = pa.seed_tokens(pa.SEED_TRAIN, 256, cfg[5]).astype(np.int32)
+    ctx = R.ref_ctx_new(P(blob), 256)
+    t0 = time.perf_counter()
+    R.ref_train_step(ctx, tok.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), 256, 1e-3)
+    train_s = time.perf_counter() - t0
+    R.ref_ctx_free(ctx)
+    return {"cores": 1, "kind": "reference", "matvec_sweep": sweep,
+            "train_step": {"workload": "stories15M, T=256, lr=1e-3, 1 step", "s_per_step": round(train_s, 2)}}
 
 
 def cpu_model():
@@ -325,6 +372,8 @@ def main():
               flush=True)
     blob = pa.synth_model(cfg, pa.SEED_MODEL[name])
     cpu = None if args.no_cpu else cpu_baseline(blob, prompt)
+    del blob
+    cpu_more = None if args.no_cpu else cpu_extra()
     # measured HBM bytes per launch of the dominant kernel (fetch + write,
     # counter-calibrated); only for the workload the committed passes ran
     default_run = args.steps == 1024 and args.profile_steps == 1024 and args.warmup == 32
@@ -353,6 +402,7 @@ def main():
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4), "kernel_ms_per_token": round(kernel_ms, 4)},
         "matvec_sweep": sweep,
         "cpu_baseline": cpu,
+        "cpu_extra": cpu_more,
         "breakdown": breakdown,
         "train": train,
     }
