@@ -59,6 +59,10 @@ __global__ __launch_bounds__(kAttnWaves * 64) void k_attn_chunk(AttnParams a) {
     __shared__ float red[kAttnWaves][kMaxHeadDim];
     __shared__ float wred[kAttnWaves];
 
+    // The position (a scalar load) goes out first; the compute path's
+    // arguments are fetched in the same batch as the prefetch test.
+    const int n = a.ctl->pos + 1;
+    kernarg_batch(a.q, a.kc, a.vc, a.part_o, a.part_ml, a.head_dim, a.kv_dim, a.kv_mul, a.chunk, a.scale);
     if ((int)blockIdx.x >= a.n_heads * a.n_chunks) {
         run_prefetch(a.pf);
         return;
@@ -71,7 +75,6 @@ __global__ __launch_bounds__(kAttnWaves * 64) void k_attn_chunk(AttnParams a) {
     const int sub_c = has ? sub : 0;
     // q does not depend on the position: its load overlaps the pos fetch.
     float4 q4 = reinterpret_cast<const float4 *>(a.q + h * hd)[sub_c];
-    const int n = a.ctl->pos + 1;
     const int t0 = c * a.chunk;
     if (t0 >= n) return;                               // uniform per block
     const int t1 = min(t0 + a.chunk, n);

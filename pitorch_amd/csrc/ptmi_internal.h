@@ -144,6 +144,19 @@ __device__ __forceinline__ float group_max(float v) {
     return v;
 }
 
+// Makes the kernel-argument loads of `v...` complete here, in one batch.
+// Without it the compiler fetches kernel arguments lazily, per branch, and
+// a kernel that first tests one argument (a prefetch-block split) pays two
+// serial scalar round trips before its first vector load.
+template <typename T>
+__device__ __forceinline__ void kernarg_pin(T v) {
+    asm volatile("" ::"s"(v));
+}
+template <typename... T>
+__device__ __forceinline__ void kernarg_batch(T... v) {
+    (kernarg_pin(v), ...);
+}
+
 // ── matvec launch description ───────────────────────────────────────────
 enum Prologue { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_EMBED_RMSNORM = 2, PRO_ATTN_COMBINE = 3 };
 constexpr int kMaxCombineDim = 4096;   // PRO_ATTN_COMBINE: x staged in LDS
@@ -168,10 +181,12 @@ struct PrefetchDesc {
 // Rows of one matvec per XCD stripe and per wave (shared by the launcher
 // and by producers that prefetch for it).
 // lpr lanes per row, it float4 of x per lane, rows_per_wave rows per wave
-// in one (two_pass = 0) or two interleaved passes of 64/lpr rows, wpb
-// waves per block, blocks_per_xcd blocks on each XCD's stripe of rows.
+// taken np passes of 64/lpr rows at a time (np = 1 or 2), wpb waves per
+// block, blocks_per_xcd blocks on each XCD's stripe of rows (linear = 0) or
+// 8*blocks_per_xcd blocks over the rows in order (linear = 1).
 struct MatvecGeom {
-    int lpr, it, exact, step, stripe, rows_per_wave, blocks_per_xcd, wpb, two_pass;
+    int lpr, it, np, step, stripe, rows_per_wave, blocks_per_xcd, wpb;
+    int linear;            // 1: wave w takes rows [w*rows_per_wave, ...) of the whole matrix
 };
 bool matvec_geometry(int rows, int n, int pro, int epi, MatvecGeom *g);
 
@@ -203,13 +218,14 @@ struct MatvecParams {
     const float *att_ml;   // [heads][chunks][2] (chunk max, chunk sum)
     int att_chunks, att_chunk, att_heads;
     int rows_per_wave;     // filled by the launcher
-    int stripe, blocks_per_xcd, two_pass;
+    int stripe, blocks_per_xcd, linear;
     PrefetchDesc pf;       // optional L2 prefetch for the next stage
 };
 
 // Prefetch blocks' body (any kernel): loads its share of stripe
 // (blockIdx.x % 8) of the consumer weights and discards it.
 __device__ __forceinline__ void run_prefetch(const PrefetchDesc &pf) {
+    kernarg_batch(pf.base, pf.row_floats, pf.rows, pf.stripe, pf.blocks, pf.first_block, pf.sink, (int)blockDim.x);
     const int q = (int)blockIdx.x - pf.first_block;
     const int xcd = (int)(blockIdx.x & 7), rank = q >> 3, per_xcd = pf.blocks >> 3;
     const long r0 = (long)xcd * pf.stripe;

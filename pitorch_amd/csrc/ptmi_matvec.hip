@@ -25,6 +25,13 @@ namespace {
 
 constexpr int kWaves = 4;          // waves per workgroup
 constexpr int kMaxRowsPerWave = 64;
+constexpr int kBigRows = 16384;    // matrices with at least this many rows ...
+constexpr int kBigWaves = 8192;    // ... run about this many single-iteration waves
+
+// v if keep, else 0 (branch-free per-lane select)
+__device__ __forceinline__ float4 sel4(bool keep, float4 v) {
+    return make_float4(keep ? v.x : 0.0f, keep ? v.y : 0.0f, keep ? v.z : 0.0f, keep ? v.w : 0.0f);
+}
 
 __device__ __forceinline__ float dot4(float4 w, float4 x, float acc) {
     acc = fmaf(w.x, x.x, acc);
@@ -77,11 +84,11 @@ __device__ __forceinline__ void run_epilogue(const MatvecParams &p, const float 
     }
 }
 
-// Register-resident-x kernel: LPR lanes per row, IT float4 chunks per lane.
-// EXACT: n/4 == LPR*IT, so no chunk is out of range.  Otherwise chunk
-// addresses are clamped into the row and the loaded value replaced by 0,
-// which keeps every load unconditional (no per-load branches).
-template <int LPR, int IT, bool EXACT, int PRO, int EPI>
+// Register-resident-x kernel: LPR lanes per row, IT float4 chunks per lane,
+// NP passes of 64/LPR rows loaded together.  IT = ceil(n/4 / LPR), so only
+// the last chunk can run past the row: its address is clamped into the row
+// and its value replaced by 0, which keeps every load unconditional.
+template <int LPR, int IT, int NP, int PRO, int EPI>
 __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
     constexpr int RPP = 64 / LPR;                  // rows per pass
     constexpr bool kNorm = PRO == PRO_RMSNORM || PRO == PRO_EMBED_RMSNORM;
@@ -92,78 +99,80 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
     const int slot = lane / LPR;
     const int sub = lane % LPR;
     const int n4 = p.n >> 2;
+    // The decode position: a scalar load issued before anything else (it
+    // stays a scalar load only ahead of the asm statements below).
+    int pos = 0;
+    if constexpr (EPI == EPI_QKV_ROPE || PRO == PRO_ATTN_COMBINE) pos = *p.pos;
+    // The compute path's launch parameters are fetched in the same batch
+    // as the prefetch test below; otherwise every wave pays a second
+    // kernel-argument round trip after the branch.
+    kernarg_batch(p.W, p.x, p.ld, p.rows, p.n, p.stripe, p.rows_per_wave, p.linear, (int)blockDim.x);
+    if constexpr (kNorm) kernarg_batch(p.norm_w);
+    if constexpr (EPI == EPI_RESIDUAL) kernarg_batch(p.y);
+    if constexpr (PRO == PRO_EMBED_RMSNORM) kernarg_batch(p.token);
+    if constexpr (PRO == PRO_ATTN_COMBINE) kernarg_batch(p.att_o, p.att_ml, p.att_chunks, p.att_heads);
     // Blocks past the compute grid prefetch the next stage's weights.
     if ((int)blockIdx.x >= 8 * p.blocks_per_xcd) {
         run_prefetch(p.pf);
         return;
     }
-    // XCD-striped rows: block b (on XCD b%8) works inside stripe b%8.
-    const long s0 = (long)(blockIdx.x & 7) * p.stripe;
-    const long s1 = s0 + p.stripe < (long)p.rows ? s0 + p.stripe : (long)p.rows;
+    // XCD-striped rows: block b (on XCD b%8) works inside stripe b%8; or
+    // rows in block order over the whole matrix.
     const int wpb = blockDim.x >> 6;
-    const long row0l = s0 + ((long)(blockIdx.x >> 3) * wpb + wave) * p.rows_per_wave;
+    const bool lin = p.linear != 0;                    // uniform
+    const long s0 = lin ? 0L : (long)(blockIdx.x & 7) * p.stripe;
+    const long s1 = lin ? (long)p.rows : (s0 + p.stripe < (long)p.rows ? s0 + p.stripe : (long)p.rows);
+    const long row0l = s0 + ((long)(lin ? blockIdx.x : blockIdx.x >> 3) * wpb + wave) * p.rows_per_wave;
     const bool active = row0l < s1;
     const int row0 = active ? (int)row0l : 0;
     const int nrows = active ? (int)min((long)p.rows_per_wave, s1 - row0l) : 0;
 
-    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    // ---- main loop: one or two passes (RPP rows each) per iteration ----
+    // Weight loads of the NP passes starting at row `base` of the wave.
     // Rows past the end re-read the wave's last row; their sums are dropped.
-    const bool two = p.two_pass != 0;              // uniform
-    const int iter_rows = two ? 2 * RPP : RPP;
-    float4 la[IT], lb[IT];
-    auto load_pair = [&](int base) {
-        const int ra = min(base + slot, nrows - 1), rb = min(base + RPP + slot, nrows - 1);
-        const float4 *wa = reinterpret_cast<const float4 *>(p.W + (long)(row0 + ra) * p.ld);
-        const float4 *wb = reinterpret_cast<const float4 *>(p.W + (long)(row0 + rb) * p.ld);
+    constexpr int kIterRows = NP * RPP;
+    float4 wv[NP][IT];
+    auto load_rows = [&](int base) {
 #pragma unroll
-        for (int it = 0; it < IT; it++) {
-            const int c = sub + it * LPR;
-            const int cc = EXACT ? c : min(c, n4 - 1);
-            la[it] = wa[cc];
-            if (!EXACT && c >= n4) la[it] = zero4;
-        }
-        if (two) {
+        for (int q = 0; q < NP; q++) {
+            const int r = max(0, min(base + q * RPP + slot, nrows - 1));   // idle waves read row 0
+            const float4 *w = reinterpret_cast<const float4 *>(p.W + (long)(row0 + r) * p.ld);
 #pragma unroll
             for (int it = 0; it < IT; it++) {
                 const int c = sub + it * LPR;
-                const int cc = EXACT ? c : min(c, n4 - 1);
-                lb[it] = wb[cc];
-                if (!EXACT && c >= n4) lb[it] = zero4;
+                wv[q][it] = w[it < IT - 1 ? c : min(c, n4 - 1)];
             }
         }
     };
-    // The first pair's weight loads go out before the prologue, so the x
-    // fetch and RMSNorm arithmetic overlap the weight latency.
-    if (nrows > 0) load_pair(0);
-    // The residual this wave's epilogue adds to (its rows only).
-    float res = 0.0f;
-    if constexpr (EPI == EPI_RESIDUAL) {
-        if (lane < nrows) res = p.y[row0 + lane];
-    }
+    // This lane's x chunks (and RMSNorm weights).
+    float4 xr[IT], nw[IT];
+    auto load_x = [&](const float *src) {
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int c = sub + it * LPR;
+            const int cc = it < IT - 1 ? c : min(c, n4 - 1);
+            xr[it] = reinterpret_cast<const float4 *>(src)[cc];
+            if constexpr (kNorm) nw[it] = reinterpret_cast<const float4 *>(p.norm_w)[cc];
+        }
+    };
 
-    // ---- prologue: this lane's x chunks (and RMSNorm weights) -> registers.
-    // Every load the prologue and epilogue need is issued here, together,
-    // so they cost one memory round trip overlapping the weight fetch.
-    const float *xs = p.x;
-    if constexpr (PRO == PRO_EMBED_RMSNORM) xs = p.x + (long)(*p.token) * p.n;
-    int pos = 0;
-    if constexpr (EPI == EPI_QKV_ROPE || PRO == PRO_ATTN_COMBINE) pos = *p.pos;
+    // ---- issue order.  Loads return in issue order, so a loaded value is
+    // usable only once every load issued before it has returned.  The
+    // prologue's few loads go out first and the weight stream right behind
+    // them: the prologue arithmetic then waits for its own round trip while
+    // the weights are in flight.  The embedding row's address needs the
+    // token id, so that prologue issues its x loads after the weights.  A
+    // plain y = Wx has no prologue arithmetic; there the weights go first
+    // (measured faster on the large classifier-shaped matrices).
+    constexpr bool kXFirst = !(PRO == PRO_NONE && EPI == EPI_STORE);
+    // PRO_ATTN_COMBINE inputs: every allocated chunk's partial sums and
+    // statistics; chunks past the active ones are dropped later by selects.
+    constexpr int kFastI = 6;                            // n <= 6 * threads in one round trip
+    float ov[kFastI][kMaxAttnChunks], mv[kMaxAttnChunks], lv[kMaxAttnChunks];
+    const int nthr = blockDim.x;
+    const int hd = PRO == PRO_ATTN_COMBINE ? p.n / p.att_heads : 1;
+    const int nch = p.att_chunks;
+    const bool fast = p.n <= kFastI * nthr;              // uniform
     if constexpr (PRO == PRO_ATTN_COMBINE) {
-        // x[i] = sum_c w[h][c] o_c[i], w[h][c] = e^(m_c - M) / sum_c' l_c' e^(m_c' - M)
-        // over the active chunks of head h = i/hd, once per workgroup into
-        // LDS.  The chunk statistics and partial sums of every allocated
-        // chunk are loaded together with the position (one memory round
-        // trip); chunks past the active ones are dropped by selects, so
-        // whatever they hold never reaches the result.
-        __shared__ float xcomb[kMaxCombineDim];
-        __shared__ float wts[kMaxCombineHeads][kMaxAttnChunks];
-        const int hd = p.n / p.att_heads;
-        const int nch = p.att_chunks;
-        constexpr int kFastI = 6;                        // n <= 6 * threads in one round trip
-        const int nthr = blockDim.x;
-        const bool fast = p.n <= kFastI * nthr;          // uniform
-        float ov[kFastI][kMaxAttnChunks];
         if (fast) {
 #pragma unroll
             for (int k = 0; k < kFastI; k++) {
@@ -175,7 +184,6 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
                 for (int c = 0; c < kMaxAttnChunks; c++) ov[k][c] = o[(long)min(c, nch - 1) * hd];
             }
         }
-        float mv[kMaxAttnChunks], lv[kMaxAttnChunks];
         const int h_ml = min((int)threadIdx.x, p.att_heads - 1);
         const float *ml = p.att_ml + 2L * h_ml * nch;
 #pragma unroll
@@ -184,6 +192,26 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
             mv[c] = ml[2 * cc];
             lv[c] = ml[2 * cc + 1];
         }
+    } else if constexpr (kXFirst) {
+        load_x(p.x);
+    }
+    __builtin_amdgcn_sched_barrier(0);            // keep the issue order above
+    load_rows(0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PRO == PRO_EMBED_RMSNORM) load_x(p.x + (long)(*p.token) * p.n);
+    if constexpr (PRO == PRO_NONE && !kXFirst) load_x(p.x);
+    // The residual this wave's epilogue adds to (its rows only).
+    float res = 0.0f;
+    if constexpr (EPI == EPI_RESIDUAL) {
+        if (lane < nrows) res = p.y[row0 + lane];
+    }
+
+    // ---- prologue arithmetic
+    if constexpr (PRO == PRO_ATTN_COMBINE) {
+        // x[i] = sum_c w[h][c] o_c[i], w[h][c] = e^(m_c - M) / sum_c' l_c' e^(m_c' - M)
+        // over the active chunks of head h = i/hd, once per workgroup into LDS.
+        __shared__ float xcomb[kMaxCombineDim];
+        __shared__ float wts[kMaxCombineHeads][kMaxAttnChunks];
         const int active = pos / p.att_chunk + 1;
         if ((int)threadIdx.x < p.att_heads) {
             float M = mv[0];
@@ -227,17 +255,12 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
             }
         }
         __syncthreads();
-        xs = xcomb;
+        load_x(xcomb);
     }
-    float4 xr[IT], nw[IT];
-#pragma unroll
-    for (int it = 0; it < IT; it++) {
-        const int c = sub + it * LPR;
-        const int cc = EXACT ? c : min(c, n4 - 1);
-        xr[it] = reinterpret_cast<const float4 *>(xs)[cc];
-        if constexpr (kNorm) nw[it] = reinterpret_cast<const float4 *>(p.norm_w)[cc];
-        if (!EXACT && c >= n4) xr[it] = zero4;
-    }
+    // The last chunk past the row contributes 0 (x and w both zeroed, so
+    // a non-finite weight read through the clamped address cannot leak in).
+    const bool tail_in = sub + (IT - 1) * LPR < n4;
+    xr[IT - 1] = sel4(tail_in, xr[IT - 1]);
     if (PRO == PRO_EMBED_RMSNORM && blockIdx.x == 0 && wave == 0 && slot == 0) {
 #pragma unroll
         for (int it = 0; it < IT; it++) {
@@ -261,20 +284,17 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
         }
     }
 
-    for (int base = 0; base < nrows; base += iter_rows) {
-        if (base > 0) load_pair(base);
-        const int ra = base + slot, rb = base + RPP + slot;
-        float acc_a = 0.0f;
+    for (int base = 0; base < nrows; base += kIterRows) {
+        if (base > 0) load_rows(base);
 #pragma unroll
-        for (int it = 0; it < IT; it++) acc_a = dot4(la[it], xr[it], acc_a);
-        acc_a = group_sum<LPR>(acc_a);
-        if (sub == 0 && ra < nrows) ybuf[wave][ra] = acc_a;
-        if (two) {
-            float acc_b = 0.0f;
+        for (int q = 0; q < NP; q++) {
+            float acc = 0.0f;
 #pragma unroll
-            for (int it = 0; it < IT; it++) acc_b = dot4(lb[it], xr[it], acc_b);
-            acc_b = group_sum<LPR>(acc_b);
-            if (sub == 0 && rb < nrows) ybuf[wave][rb] = acc_b;
+            for (int it = 0; it < IT; it++)
+                acc = dot4(it < IT - 1 ? wv[q][it] : sel4(tail_in, wv[q][it]), xr[it], acc);
+            acc = group_sum<LPR>(acc);
+            const int r = base + q * RPP + slot;
+            if (sub == 0 && r < nrows) ybuf[wave][r] = acc;
         }
     }
     __syncthreads();
@@ -330,18 +350,18 @@ __global__ __launch_bounds__(256) void k_matvec_scalar(MatvecParams p) {
 
 using KernelFn = void (*)(MatvecParams);
 
-template <int LPR, bool EXACT, int PRO, int EPI>
+template <int LPR, int NP, int PRO, int EPI>
 KernelFn pick_it(int it) {
     switch (it) {
-    case 1: return k_matvec<LPR, 1, EXACT, PRO, EPI>;
-    case 2: return k_matvec<LPR, 2, EXACT, PRO, EPI>;
-    case 3: return k_matvec<LPR, 3, EXACT, PRO, EPI>;
-    case 4: return k_matvec<LPR, 4, EXACT, PRO, EPI>;
-    case 5: return k_matvec<LPR, 5, EXACT, PRO, EPI>;
-    case 6: return k_matvec<LPR, 6, EXACT, PRO, EPI>;
-    case 7: return k_matvec<LPR, 7, EXACT, PRO, EPI>;
-    case 8: return k_matvec<LPR, 8, EXACT, PRO, EPI>;
-    case 9: return k_matvec<LPR, 9, EXACT, PRO, EPI>;
+    case 1: return k_matvec<LPR, 1, NP, PRO, EPI>;
+    case 2: return k_matvec<LPR, 2, NP, PRO, EPI>;
+    case 3: return k_matvec<LPR, 3, NP, PRO, EPI>;
+    case 4: return k_matvec<LPR, 4, NP, PRO, EPI>;
+    case 5: return k_matvec<LPR, 5, NP, PRO, EPI>;
+    case 6: return k_matvec<LPR, 6, NP, PRO, EPI>;
+    case 7: return k_matvec<LPR, 7, NP, PRO, EPI>;
+    case 8: return k_matvec<LPR, 8, NP, PRO, EPI>;
+    case 9: return k_matvec<LPR, 9, NP, PRO, EPI>;
     default: return nullptr;
     }
 }
@@ -349,22 +369,22 @@ KernelFn pick_it(int it) {
 // Only the (prologue, epilogue) pairs the library launches are built:
 // plain y=Wx, QKV (+embed on layer 0), residual (Wo, w2), SwiGLU (w1|w3),
 // classifier (RMSNorm prologue, plain store).
-template <int LPR, bool EXACT>
+template <int LPR, int NP>
 KernelFn pick_role(int it, int pro, int epi) {
-    if (pro == PRO_NONE && epi == EPI_STORE) return pick_it<LPR, EXACT, PRO_NONE, EPI_STORE>(it);
-    if (pro == PRO_NONE && epi == EPI_RESIDUAL) return pick_it<LPR, EXACT, PRO_NONE, EPI_RESIDUAL>(it);
-    if (pro == PRO_RMSNORM && epi == EPI_STORE) return pick_it<LPR, EXACT, PRO_RMSNORM, EPI_STORE>(it);
-    if (pro == PRO_RMSNORM && epi == EPI_SWIGLU) return pick_it<LPR, EXACT, PRO_RMSNORM, EPI_SWIGLU>(it);
-    if (pro == PRO_RMSNORM && epi == EPI_QKV_ROPE) return pick_it<LPR, EXACT, PRO_RMSNORM, EPI_QKV_ROPE>(it);
+    if (pro == PRO_NONE && epi == EPI_STORE) return pick_it<LPR, NP, PRO_NONE, EPI_STORE>(it);
+    if (pro == PRO_NONE && epi == EPI_RESIDUAL) return pick_it<LPR, NP, PRO_NONE, EPI_RESIDUAL>(it);
+    if (pro == PRO_RMSNORM && epi == EPI_STORE) return pick_it<LPR, NP, PRO_RMSNORM, EPI_STORE>(it);
+    if (pro == PRO_RMSNORM && epi == EPI_SWIGLU) return pick_it<LPR, NP, PRO_RMSNORM, EPI_SWIGLU>(it);
+    if (pro == PRO_RMSNORM && epi == EPI_QKV_ROPE) return pick_it<LPR, NP, PRO_RMSNORM, EPI_QKV_ROPE>(it);
     if (pro == PRO_EMBED_RMSNORM && epi == EPI_QKV_ROPE)
-        return pick_it<LPR, EXACT, PRO_EMBED_RMSNORM, EPI_QKV_ROPE>(it);
-    if (pro == PRO_ATTN_COMBINE && epi == EPI_RESIDUAL) return pick_it<LPR, EXACT, PRO_ATTN_COMBINE, EPI_RESIDUAL>(it);
+        return pick_it<LPR, NP, PRO_EMBED_RMSNORM, EPI_QKV_ROPE>(it);
+    if (pro == PRO_ATTN_COMBINE && epi == EPI_RESIDUAL) return pick_it<LPR, NP, PRO_ATTN_COMBINE, EPI_RESIDUAL>(it);
     return nullptr;
 }
 
 template <int LPR>
-KernelFn pick(int it, bool exact, int pro, int epi) {
-    return exact ? pick_role<LPR, true>(it, pro, epi) : pick_role<LPR, false>(it, pro, epi);
+KernelFn pick(int it, int np, int pro, int epi) {
+    return np == 2 ? pick_role<LPR, 2>(it, pro, epi) : pick_role<LPR, 1>(it, pro, epi);
 }
 
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
@@ -376,6 +396,10 @@ inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 // that each XCD runs ~256 waves (8 per CU) when the matrix is big enough.
 // Kernel geometry, chosen from measurements on MI355X (graph-replayed
 // launches, weights in HBM or MALL):
+//  * >= 16384 rows (the classifier), any prologue: many short waves in row
+//    order (32000x768: 18.1 vs 19.1 us; 32000x512: 13.1 vs 15.8 us).  A
+//    wave that walks several row groups one after another leaves the tail
+//    of the launch to a few late waves.
 //  * With a prologue (RMSNorm, embedding, attention combine), whose cost is
 //    paid per wave or per workgroup: the fewest lanes per row that keep a
 //    lane's x slice within 9 float4, two row passes per iteration, ~256
@@ -393,7 +417,40 @@ bool matvec_geometry(int rows, int n, int pro, int epi, MatvecGeom *g) {
     const int per = (rows + 7) / 8;
     int lpr = lpr_min, rpw, wpb;
     bool two;
-    if (pro != PRO_NONE) {
+    int linear = 0;
+    if (rows >= kBigRows) {
+        // Large matrices (the classifier): one iteration per wave, each
+        // wave's few rows loaded at once, ~8192 waves of 4, rows in block
+        // order.  Lanes per row: the widest power of two that keeps >= 3/4
+        // of the lanes' chunks inside the row; then, while there are too
+        // many waves, halve it (x slice <= 6 float4), or take two passes,
+        // or more rows per wave.
+        lpr = 64;
+        while (lpr > lpr_min && 4 * n4 < 3 * lpr * ((n4 + lpr - 1) / lpr)) lpr /= 2;
+        int it = (n4 + lpr - 1) / lpr;
+        int rpp = 64 / lpr;
+        two = gran > rpp;
+        rpw = two ? 2 * rpp : rpp;
+        while ((rows + rpw - 1) / rpw > kBigWaves) {
+            if (!two && lpr / 2 >= lpr_min && 2 * it <= 6) {
+                lpr /= 2;
+                it = (n4 + lpr - 1) / lpr;
+                rpp = 64 / lpr;
+                rpw = std::max(rpp, gran);
+                two = rpw > rpp;
+            } else if (!two) {
+                two = true;
+                rpw = 2 * rpp;
+            } else if (rpw < kMaxRowsPerWave) {
+                rpw *= 2;
+            } else {
+                break;
+            }
+        }
+        g->stripe = (per + gran - 1) / gran * gran;
+        wpb = kWaves;
+        linear = 1;
+    } else if (pro != PRO_NONE) {
         const int step = 2 * (64 / lpr);
         g->stripe = (per + step - 1) / step * step;
         rpw = (g->stripe + 255) / 256;
@@ -415,13 +472,18 @@ bool matvec_geometry(int rows, int n, int pro, int epi, MatvecGeom *g) {
     }
     g->lpr = lpr;
     g->it = (n4 + lpr - 1) / lpr;
-    g->exact = n4 == lpr * g->it;
+    g->np = two ? 2 : 1;
     g->step = gran;
     g->rows_per_wave = rpw;
-    g->two_pass = two;
+    g->linear = linear;
     g->wpb = wpb;
-    const int waves = (g->stripe + rpw - 1) / rpw;
-    g->blocks_per_xcd = (waves + wpb - 1) / wpb;
+    if (g->linear) {
+        const long blocks = ((long)(rows + rpw - 1) / rpw + wpb - 1) / wpb;
+        g->blocks_per_xcd = (int)((blocks + 7) / 8);
+    } else {
+        const int waves = (g->stripe + rpw - 1) / rpw;
+        g->blocks_per_xcd = (waves + wpb - 1) / wpb;
+    }
     return true;
 }
 
@@ -482,16 +544,16 @@ int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     MatvecGeom geo;
     if (vec_ok && matvec_geometry(p.rows, p.n, p.pro, p.epi, &geo)) {
         switch (geo.lpr) {
-        case 8: fn = pick<8>(geo.it, geo.exact, p.pro, p.epi); break;
-        case 16: fn = pick<16>(geo.it, geo.exact, p.pro, p.epi); break;
-        case 32: fn = pick<32>(geo.it, geo.exact, p.pro, p.epi); break;
-        default: fn = pick<64>(geo.it, geo.exact, p.pro, p.epi); break;
+        case 8: fn = pick<8>(geo.it, geo.np, p.pro, p.epi); break;
+        case 16: fn = pick<16>(geo.it, geo.np, p.pro, p.epi); break;
+        case 32: fn = pick<32>(geo.it, geo.np, p.pro, p.epi); break;
+        default: fn = pick<64>(geo.it, geo.np, p.pro, p.epi); break;
         }
         if (!fn) return set_error(PTMI_ERR_ARG, "matvec: unsupported prologue/epilogue pair %d/%d", p.pro, p.epi);
         p.stripe = geo.stripe;
         p.rows_per_wave = geo.rows_per_wave;
         p.blocks_per_xcd = geo.blocks_per_xcd;
-        p.two_pass = geo.two_pass;
+        p.linear = geo.linear;
         const int compute_blocks = 8 * geo.blocks_per_xcd;
         if (p.pf.blocks && p.pf.first_block != compute_blocks)
             return set_error(PTMI_ERR_ARG, "matvec: prefetch descriptor built for another grid");
