@@ -99,8 +99,8 @@ __device__ __forceinline__ void load_tile(const float *P, long ld, int idx_lim, 
     }
 }
 
-template <bool KMAJOR, int R>
-__device__ __forceinline__ void store_tile(float (*S)[R + 4], int tid, const float (&r)[R * BK / 256]) {
+template <bool KMAJOR, int R, int PD>
+__device__ __forceinline__ void store_tile(float (*S)[R + PD], int tid, const float (&r)[R * BK / 256]) {
     constexpr int E = R * BK / 256;
     if (KMAJOR) {
         const int k = tid / (R / E), i = E * (tid % (R / E));
@@ -114,12 +114,16 @@ __device__ __forceinline__ void store_tile(float (*S)[R + 4], int tid, const flo
 }
 
 // One TMxTN output tile of g at (m0, n0) over K range split z.
+// LDS rows are padded so that a row's start moves by 16 banks from the
+// previous row for 64-wide tiles (the two k rows one half-wave reads
+// for the MFMA operands then fall on disjoint banks).
 template <bool AT, bool BT, int TM, int TN, int P>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int z) {
     constexpr int FM = TM / 32, FN = TN / 32;          // 16x16 MFMA blocks per wave
     constexpr int EA = TM * BK / 256, EB = TN * BK / 256;
-    __shared__ float As[2][BK][TM + 4];
-    __shared__ float Bs[2][BK][TN + 4];
+    constexpr int PA = TM == 64 ? 16 : 4, PB = TN == 64 ? 16 : 4;
+    __shared__ float As[2][BK][TM + PA];
+    __shared__ float Bs[2][BK][TN + PB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int li = lane & 15, lk = lane >> 4;
@@ -141,8 +145,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
         load_tile<!BT, TN>(g.B, g.ldb, g.N, n0, kb + s * BK, kend, g.b_vec, tid, xb);
     };
     auto store = [&](int s, const float (&xa)[EA], const float (&xb)[EB]) {
-        store_tile<AT, TM>(As[s & 1], tid, xa);
-        store_tile<!BT, TN>(Bs[s & 1], tid, xb);
+        store_tile<AT, TM, PA>(As[s & 1], tid, xa);
+        store_tile<!BT, TN, PB>(Bs[s & 1], tid, xb);
     };
     auto compute = [&](int s) {
         const int buf = s & 1;
