@@ -39,7 +39,6 @@ struct GemmArgs {
     int accumulate;
     float *partial;        // split-K workspace [splits][M][N] or null
     int k_per_split;
-    bool a_vec, b_vec;     // 16-byte aligned rows: float4 global loads
 };
 
 // One GEMM of a grouped launch: its arguments and its range of tiles.
@@ -49,52 +48,57 @@ struct GemmGroupDesc {
     int tile0;             // first block of this GEMM in the grouped grid
 };
 
+// Read by loads whose element lies outside the operand (ragged edges and
+// the K tail), so every load is unconditional and needs no select after it.
+__device__ __align__(16) float g_gemm_zero[16] = {};
+
 // One operand tile (R rows of the M or N side x 32 k) per K step; each of
-// the 256 threads moves E = R*32/256 floats (8 or 4) as float4s (or
-// predicated scalars at ragged edges).  KMAJOR: the operand is stored with
-// k as the row index (A^T for TN, B for NN/TN); otherwise k is the
-// contiguous index.
+// the 256 threads moves E = R*32/256 floats (8 or 4).  KMAJOR: the operand
+// is stored with k as the row index (A^T for TN, B for NN/TN); otherwise k
+// is the contiguous index.
 //   KMAJOR:  thread -> (k = tid/(R/E),     idx = E*(tid%(R/E)) + c)
 //   !KMAJOR: thread -> (idx = tid/(32/E),  k = E*(tid%(32/E)) + c)
-template <bool KMAJOR, int R>
-__device__ __forceinline__ void load_tile(const float *P, long ld, int idx_lim, int i0, int k0, int kend, bool vec,
-                                          int tid, float (&r)[R * BK / 256]) {
+// VEC: 16-byte float4 loads; the launcher guarantees aligned rows and a
+// contiguous extent (idx_lim for KMAJOR, K otherwise) that is a multiple of
+// 4, so a float4 is either wholly inside the operand or wholly outside.
+// Elements outside read g_gemm_zero: only the address is selected, before
+// the load, so the loads of a tile stay in flight together (a select on the
+// loaded value, or a branch, makes the compiler wait for every load issued
+// so far).
+template <bool KMAJOR, int R, bool VEC>
+__device__ __forceinline__ void load_tile(const float *P, long ld, int idx_lim, int i0, int k0, int kend, int tid,
+                                          float (&r)[R * BK / 256]) {
     constexpr int E = R * BK / 256;
+    const float *zero = g_gemm_zero;
     if (KMAJOR) {
         const int k = k0 + tid / (R / E), i = i0 + E * (tid % (R / E));
         const bool kin = k < kend;
-        const float *p = P + (long)min(k, kend - 1) * ld;
-        if (vec && i + E - 1 < idx_lim) {
+        const float *row = P + (long)(kin ? k : 0) * ld;
+        if constexpr (VEC) {
 #pragma unroll
             for (int c = 0; c < E; c += 4) {
-                const float4 v = *reinterpret_cast<const float4 *>(p + i + c);
+                const bool in = kin && i + c < idx_lim;
+                const float4 v = *reinterpret_cast<const float4 *>(in ? row + i + c : zero + c);
                 r[c] = v.x; r[c + 1] = v.y; r[c + 2] = v.z; r[c + 3] = v.w;
-            }
-            if (!kin) {
-#pragma unroll
-                for (int c = 0; c < E; c++) r[c] = 0.f;
             }
         } else {
 #pragma unroll
-            for (int c = 0; c < E; c++) r[c] = (kin && i + c < idx_lim) ? p[i + c] : 0.f;
+            for (int c = 0; c < E; c++) r[c] = *((kin && i + c < idx_lim) ? row + i + c : zero + c);
         }
     } else {
         const int i = i0 + tid / (BK / E), k = k0 + E * (tid % (BK / E));
         const bool iin = i < idx_lim;
-        const float *p = P + (long)min(i, idx_lim - 1) * ld;
-        if (vec && k + E - 1 < kend) {
+        const float *row = P + (long)(iin ? i : 0) * ld;
+        if constexpr (VEC) {
 #pragma unroll
             for (int c = 0; c < E; c += 4) {
-                const float4 v = *reinterpret_cast<const float4 *>(p + k + c);
+                const bool in = iin && k + c < kend;
+                const float4 v = *reinterpret_cast<const float4 *>(in ? row + k + c : zero + c);
                 r[c] = v.x; r[c + 1] = v.y; r[c + 2] = v.z; r[c + 3] = v.w;
-            }
-            if (!iin) {
-#pragma unroll
-                for (int c = 0; c < E; c++) r[c] = 0.f;
             }
         } else {
 #pragma unroll
-            for (int c = 0; c < E; c++) r[c] = (iin && k + c < kend) ? p[k + c] : 0.f;
+            for (int c = 0; c < E; c++) r[c] = *((iin && k + c < kend) ? row + k + c : zero + c);
         }
     }
 }
@@ -117,7 +121,7 @@ __device__ __forceinline__ void store_tile(float (*S)[R + PD], int tid, const fl
 // LDS rows are padded so that a row's start moves by 16 banks from the
 // previous row for 64-wide tiles (the two k rows one half-wave reads
 // for the MFMA operands then fall on disjoint banks).
-template <bool AT, bool BT, int TM, int TN, int P>
+template <bool AT, bool BT, int TM, int TN, int P, bool VEC>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int z) {
     constexpr int FM = TM / 32, FN = TN / 32;          // 16x16 MFMA blocks per wave
     constexpr int EA = TM * BK / 256, EB = TN * BK / 256;
@@ -141,8 +145,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
     // loop is unrolled by P so every slot index is a compile-time constant.
     float ra[P][EA], rb[P][EB];
     auto load = [&](int s, float (&xa)[EA], float (&xb)[EB]) {
-        load_tile<AT, TM>(g.A, g.lda, g.M, m0, kb + s * BK, kend, g.a_vec, tid, xa);
-        load_tile<!BT, TN>(g.B, g.ldb, g.N, n0, kb + s * BK, kend, g.b_vec, tid, xb);
+        load_tile<AT, TM, VEC>(g.A, g.lda, g.M, m0, kb + s * BK, kend, tid, xa);
+        load_tile<!BT, TN, VEC>(g.B, g.ldb, g.N, n0, kb + s * BK, kend, tid, xb);
     };
     auto store = [&](int s, const float (&xa)[EA], const float (&xb)[EB]) {
         store_tile<AT, TM, PA>(As[s & 1], tid, xa);
@@ -166,22 +170,32 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
     };
 
 #pragma unroll
-    for (int t = 0; t < P; t++)
-        if (t < nk) load(t, ra[t], rb[t]);
-    if (nk > 0) store(0, ra[0], rb[0]);
+    // Loads are unconditional (tiles past the K range read zeros): a load
+    // under a branch leaves the compiler unsure how many loads are in flight,
+    // and it then waits for all of them, which empties the ring.
+    for (int t = 0; t < P; t++) load(t, ra[t], rb[t]);
+    store(0, ra[0], rb[0]);
     __syncthreads();
     // Step s: tile s is in LDS; its register slot (s % P) is free, so tile
-    // s+P is fetched into it; tile s+1 goes to the other LDS buffer.
-    for (int s0 = 0; s0 < nk; s0 += P) {
+    // s+P is fetched into it; tile s+1 goes to the other LDS buffer.  Full
+    // groups of P steps run without branches; the last nk % P steps follow.
+    int s0 = 0;
+    for (; s0 + P <= nk; s0 += P) {
 #pragma unroll
         for (int u = 0; u < P; u++) {
-            const int s = s0 + u;
-            if (s < nk) {
-                if (s + P < nk) load(s + P, ra[u], rb[u]);
-                compute(s);
-                if (s + 1 < nk) store(s + 1, ra[(u + 1) % P], rb[(u + 1) % P]);
-                __syncthreads();
-            }
+            load(s0 + u + P, ra[u], rb[u]);
+            __builtin_amdgcn_sched_barrier(0);              // issue the loads before the MFMAs
+            compute(s0 + u);
+            store(s0 + u + 1, ra[(u + 1) % P], rb[(u + 1) % P]);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int u = 0; u + 1 < P; u++) {
+        if (s0 + u < nk) {                                  // uniform
+            compute(s0 + u);
+            store(s0 + u + 1, ra[(u + 1) % P], rb[(u + 1) % P]);
+            __syncthreads();
         }
     }
 
@@ -208,21 +222,21 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
     }
 }
 
-template <bool AT, bool BT, int TM, int TN, int P>
+template <bool AT, bool BT, int TM, int TN, int P, bool VEC>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
-    gemm_tile<AT, BT, TM, TN, P>(g, blockIdx.y * TM, blockIdx.x * TN, blockIdx.z);
+    gemm_tile<AT, BT, TM, TN, P, VEC>(g, blockIdx.y * TM, blockIdx.x * TN, blockIdx.z);
 }
 
 // Grouped TN GEMMs (32x32 tiles, whole K): block b runs tile
 // b - d.tile0 of the descriptor d whose tile range holds b.
-template <int TM, int TN>
+template <int TM, int TN, bool VEC>
 __global__ __launch_bounds__(256) void k_gemm_tn_group(const GemmGroupDesc *d, int n) {
     const int b = blockIdx.x;
     int i = 0;
     while (i + 1 < n && d[i + 1].tile0 <= b) i++;
     const GemmGroupDesc &e = d[i];
     const int t = b - e.tile0;
-    gemm_tile<true, false, TM, TN, kRing32>(e.g, (t / e.tiles_n) * TM, (t % e.tiles_n) * TN, 0);
+    gemm_tile<true, false, TM, TN, kRing32, VEC>(e.g, (t / e.tiles_n) * TM, (t % e.tiles_n) * TN, 0);
 }
 
 // C = (Cin +) sum_z partial[z], z ascending.
@@ -231,8 +245,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *partial, int
     const long idx = (long)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (long)M * N) return;
     const int m = (int)(idx / N), n = (int)(idx % N);
-    float s = 0.0f;
-    for (int z = 0; z < splits; z++) s += partial[(long)z * M * N + idx];
+    const float s = sum_splits(partial, splits, (long)M * N, idx);
     const long o = (long)m * ldc + n;
     C[o] = accumulate ? Cin[o] + s : s;
 }
@@ -244,7 +257,8 @@ inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 // Launch op(A).op(B) with shapes validated; `ws` (optional) is a split-K
 // workspace of ws_floats floats.
 int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc, int M, int N,
-                int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s, const float *Cin) {
+                int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s, const float *Cin, SplitK *defer) {
+    if (defer) *defer = SplitK{nullptr, 0, 0};
     if (M <= 0 || N <= 0 || K <= 0) return set_error(PTMI_ERR_ARG, "gemm: M=%d N=%d K=%d", M, N, K);
     if (!A || !B || !C) return set_error(PTMI_ERR_ARG, "gemm: null operand");
     if (op < 0 || op > 2) return set_error(PTMI_ERR_ARG, "gemm: op %d", op);
@@ -256,8 +270,10 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
     g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc;
     g.M = M; g.N = N; g.K = K; g.accumulate = accumulate;
     g.Cin = Cin ? Cin : C;
-    g.a_vec = al16(A) && lda % 4 == 0;
-    g.b_vec = al16(B) && ldb % 4 == 0;
+    // float4 loads when both operands have aligned rows and a contiguous
+    // extent that is a multiple of 4 (M for A^T, K for A; K for B^T, N for B)
+    const bool vec = al16(A) && lda % 4 == 0 && (AT ? M : K) % 4 == 0 && al16(B) && ldb % 4 == 0 &&
+                     (BT ? K : N) % 4 == 0;
     // Kernel choice, measured on MI355X for the training shapes (graph-
     // replayed launches): 32x32 tiles win everywhere except long K (>= 4096:
     // 64x64 with K split over >= 512 blocks) and large NT outputs (>= 4M
@@ -278,17 +294,21 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
     g.partial = splits > 1 ? ws : nullptr;
     if (gy > 65535) return set_error(PTMI_ERR_ARG, "gemm: M too large");
     dim3 grid(gx, gy, splits);
-    if (big) {
-        if (op == 0) hipLaunchKernelGGL((k_gemm<false, false, 64, 64, kRing64>), grid, dim3(256), 0, s, g);
-        else if (op == 1) hipLaunchKernelGGL((k_gemm<true, false, 64, 64, kRing64>), grid, dim3(256), 0, s, g);
-        else hipLaunchKernelGGL((k_gemm<false, true, 64, 64, kRing64>), grid, dim3(256), 0, s, g);
-    } else {
-        if (op == 0) hipLaunchKernelGGL((k_gemm<false, false, 32, 32, kRing32>), grid, dim3(256), 0, s, g);
-        else if (op == 1) hipLaunchKernelGGL((k_gemm<true, false, 32, 32, kRing32>), grid, dim3(256), 0, s, g);
-        else hipLaunchKernelGGL((k_gemm<false, true, 32, 32, kRing32>), grid, dim3(256), 0, s, g);
-    }
+    using KFn = void (*)(GemmArgs);
+    static const KFn kernels[2][2][3] = {
+        {{k_gemm<false, false, 32, 32, kRing32, false>, k_gemm<true, false, 32, 32, kRing32, false>,
+          k_gemm<false, true, 32, 32, kRing32, false>},
+         {k_gemm<false, false, 32, 32, kRing32, true>, k_gemm<true, false, 32, 32, kRing32, true>,
+          k_gemm<false, true, 32, 32, kRing32, true>}},
+        {{k_gemm<false, false, 64, 64, kRing64, false>, k_gemm<true, false, 64, 64, kRing64, false>,
+          k_gemm<false, true, 64, 64, kRing64, false>},
+         {k_gemm<false, false, 64, 64, kRing64, true>, k_gemm<true, false, 64, 64, kRing64, true>,
+          k_gemm<false, true, 64, 64, kRing64, true>}}};
+    hipLaunchKernelGGL(kernels[big][vec][op], grid, dim3(256), 0, s, g);
     PTMI_HIP(hipGetLastError());
-    if (splits > 1) {
+    if (splits > 1 && defer) {
+        *defer = SplitK{ws, splits, (long)M * N};
+    } else if (splits > 1) {
         const long n = (long)M * N;
         hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ws, splits, C, g.Cin,
                            ldc, M, N, accumulate);
@@ -299,9 +319,9 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
 
 size_t gemm_group_desc_bytes(int n) { return sizeof(GemmGroupDesc) * (size_t)n; }
 
-int gemm_tn_group_prepare(const TnGemm *list, int n, void *host_desc, int *tiles_total) {
+int gemm_tn_group_prepare(const TnGemm *list, int n, void *host_desc, int *tiles_total, int *vec_out) {
     GemmGroupDesc *d = static_cast<GemmGroupDesc *>(host_desc);
-    int t = 0;
+    int t = 0, vec = 1;
     for (int i = 0; i < n; i++) {
         const TnGemm &e = list[i];
         if (e.M <= 0 || e.N <= 0 || e.K <= 0 || !e.A || !e.B || !e.C || e.lda < e.M || e.ldb < e.N || e.ldc < e.N)
@@ -309,21 +329,21 @@ int gemm_tn_group_prepare(const TnGemm *list, int n, void *host_desc, int *tiles
         GemmArgs &g = d[i].g;
         g = GemmArgs{};
         g.A = e.A; g.lda = e.lda; g.B = e.B; g.ldb = e.ldb; g.C = e.C; g.ldc = e.ldc; g.Cin = e.C;
-        g.M = e.M; g.N = e.N; g.K = e.K; g.accumulate = 1; g.partial = nullptr; g.k_per_split = e.K;
-        g.a_vec = al16(e.A) && e.lda % 4 == 0;
-        g.b_vec = al16(e.B) && e.ldb % 4 == 0;
+        g.M = e.M; g.N = e.N; g.K = e.K; g.accumulate = 0; g.partial = nullptr; g.k_per_split = e.K;
+        if (!(al16(e.A) && e.lda % 4 == 0 && e.M % 4 == 0 && al16(e.B) && e.ldb % 4 == 0 && e.N % 4 == 0)) vec = 0;
         d[i].tiles_n = (e.N + 31) / 32;
         d[i].tile0 = t;
         t += d[i].tiles_n * ((e.M + 31) / 32);
     }
     *tiles_total = t;
+    *vec_out = vec;
     return PTMI_OK;
 }
 
-int launch_gemm_tn_group(const void *dev_desc, int n, int tiles_total, hipStream_t s) {
+int launch_gemm_tn_group(const void *dev_desc, int n, int tiles_total, int vec, hipStream_t s) {
     if (n <= 0 || tiles_total <= 0) return PTMI_OK;
-    hipLaunchKernelGGL((k_gemm_tn_group<32, 32>), dim3((unsigned)tiles_total), dim3(256), 0, s,
-                       static_cast<const GemmGroupDesc *>(dev_desc), n);
+    void (*fn)(const GemmGroupDesc *, int) = vec ? k_gemm_tn_group<32, 32, true> : k_gemm_tn_group<32, 32, false>;
+    hipLaunchKernelGGL(fn, dim3((unsigned)tiles_total), dim3(256), 0, s, static_cast<const GemmGroupDesc *>(dev_desc), n);
     PTMI_HIP(hipGetLastError());
     return PTMI_OK;
 }

@@ -262,15 +262,41 @@ inline void launch_k(F f, dim3 g, dim3 b, size_t shmem, hipStream_t s, hipEvent_
 // Launch y = epilogue(W . prologue(x)); validates shapes, picks a kernel.
 int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 
+// Split-K partial sums left in the workspace for the next kernel to add up
+// (dense [splits][M][N]; C = (Cin +) sum over z ascending of parts[z]).
+struct SplitK {
+    const float *parts;
+    int splits;            // 0: C was written by the GEMM itself
+    long stride;           // M*N
+};
+
+// sum_z parts[z*stride + idx] for z = 0..splits-1 in ascending order (the
+// split-K reduction).  Loads go out eight at a time before any is added,
+// so a reduction costs about splits/8 memory round trips, not splits.
+__device__ __forceinline__ float sum_splits(const float *parts, int splits, long stride, long idx) {
+    float v = 0.0f;
+    for (int z0 = 0; z0 < splits; z0 += 8) {
+        float pv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) pv[u] = parts[(long)min(z0 + u, splits - 1) * stride + idx];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v = z0 + u < splits ? v + pv[u] : v;
+    }
+    return v;
+}
+
 // C[M,N] (+)= op(A).op(B) on the matrix cores; op 0 NN, 1 TN (A stored
 // [K][M]), 2 NT (B stored [N][K]).  ws: split-K workspace (may be null).
 // With accumulate, Cin (same leading dimension as C; null = C itself) is
-// the addend: C = Cin + op(A).op(B).
+// the addend: C = Cin + op(A).op(B).  With `defer`, a split-K GEMM skips its
+// reduction launch and leaves the partials to the caller (defer->splits > 0;
+// C is then not written); otherwise defer->splits = 0.
 int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc, int M, int N,
-                int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s, const float *Cin = nullptr);
+                int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s, const float *Cin = nullptr,
+                SplitK *defer = nullptr);
 
-// Grouped C[M,N] += A^T.B GEMMs (TN; A stored [K][M]), one launch of 32x32
-// tiles over all of them.  prepare fills host_desc (gemm_group_desc_bytes(n)
+// Grouped C[M,N] = A^T.B GEMMs (TN; A stored [K][M]; C written, not
+// accumulated), one launch of 32x32 tiles over all of them.  prepare fills host_desc (gemm_group_desc_bytes(n)
 // bytes); the caller copies it to device memory for the launch.
 struct TnGemm {
     const float *A; long lda;
@@ -279,8 +305,8 @@ struct TnGemm {
     int M, N, K;
 };
 size_t gemm_group_desc_bytes(int n);
-int gemm_tn_group_prepare(const TnGemm *list, int n, void *host_desc, int *tiles_total);
-int launch_gemm_tn_group(const void *dev_desc, int n, int tiles_total, hipStream_t s);
+int gemm_tn_group_prepare(const TnGemm *list, int n, void *host_desc, int *tiles_total, int *vec);
+int launch_gemm_tn_group(const void *dev_desc, int n, int tiles_total, int vec, hipStream_t s);
 
 // ── library state ───────────────────────────────────────────────────────
 struct Config {

@@ -38,7 +38,7 @@ struct TrainState {
     // Descriptor tables of the two grouped launches (device; built per T).
     void *dw_desc;
     float *nd_desc;
-    int desc_T = 0, dw_tiles = 0, n_dw = 0;
+    int desc_T = 0, dw_tiles = 0, n_dw = 0, dw_vec = 0;
     float *ws;
     size_t ws_floats = 0;
     float *lr;                  // device copy of the step's learning rate
@@ -90,14 +90,26 @@ __global__ void k_embed_rows(const int *tok, const float *emb, float *out, int D
 }
 
 // rmsnorm (pt_ops.c:5-12) per row.
-__global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *in, const float *w, float *out, int D) {
+// With pk.splits > 0 the row x is first completed from split-K partial sums
+// of the GEMM that produced it, x = (cin +) sum_z pk.parts[z] (the split-K
+// reduction, z ascending), and stored; each thread re-reads only the
+// elements it stored.
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(float *in, const float *w, float *out, int D, SplitK pk,
+                                                      const float *cin) {
     __shared__ float red[4];
-    const float *x = in + (long)blockIdx.x * D;
+    const long r = (long)blockIdx.x * D;
+    float *x = in + r;
+    if (pk.splits > 0) {                                         // uniform
+        for (int i = threadIdx.x; i < D; i += 256) {
+            const float v = sum_splits(pk.parts, pk.splits, pk.stride, r + i);
+            x[i] = cin ? cin[r + i] + v : v;
+        }
+    }
     float ss = 0.0f;
     for (int i = threadIdx.x; i < D; i += 256) ss += x[i] * x[i];
     ss = block_sum<4>(ss, red);
     const float inv = 1.0f / d_sqrtf(ss / D + 1e-5f);
-    for (int i = threadIdx.x; i < D; i += 256) out[(long)blockIdx.x * D + i] = x[i] * inv * w[i];
+    for (int i = threadIdx.x; i < D; i += 256) out[r + i] = x[i] * inv * w[i];
 }
 
 // rope (pt_ops.c:33-49) on the q and k columns of each position's qkv row.
@@ -299,10 +311,16 @@ __global__ __launch_bounds__(256) void k_loss_reduce(const float *row_loss, int 
 
 // rmsnorm_backward (pt_backward_ops.c:4-30), the d_x half, per row:
 // d_out = d_in + (the reference's in-place d_x += term).
-__global__ __launch_bounds__(256) void k_rmsnorm_bwd_rows(float *d_out, const float *d_in, const float *d_o,
-                                                          const float *x, const float *w, float *inv_out, int D) {
+// With pk.splits > 0, d_o is first completed from the split-K partial sums
+// of the GEMM that produced it (z ascending) and stored.
+__global__ __launch_bounds__(256) void k_rmsnorm_bwd_rows(float *d_out, const float *d_in, float *d_o,
+                                                          const float *x, const float *w, float *inv_out, int D,
+                                                          SplitK pk) {
     __shared__ float red[4];
     const long r = (long)blockIdx.x * D;
+    if (pk.splits > 0) {                                         // uniform
+        for (int i = threadIdx.x; i < D; i += 256) d_o[r + i] = sum_splits(pk.parts, pk.splits, pk.stride, r + i);
+    }
     float ss = 0.0f, dot = 0.0f;
     for (int i = threadIdx.x; i < D; i += 256) {
         const float xi = x[r + i];
@@ -315,12 +333,17 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd_rows(float *d_out, const fl
     const float inv = 1.0f / d_sqrtf(ss);
     const float cd = inv * inv * inv / (float)D * dot;
     if (threadIdx.x == 0) inv_out[blockIdx.x] = inv;
-    for (int i = threadIdx.x; i < D; i += 256) d_out[r + i] = d_in[r + i] + (inv * d_o[r + i] * w[i] - cd * x[r + i]);
+    // d_in == nullptr: the incoming residual gradient is zero (0 + v == v)
+    for (int i = threadIdx.x; i < D; i += 256) {
+        const float v = inv * d_o[r + i] * w[i] - cd * x[r + i];
+        d_out[r + i] = d_in ? d_in[r + i] + v : v;
+    }
 }
 
 // The d_w half of every RMSNorm of the step in one launch: for norm
-// j = blockIdx.x / cb, d_w[i] += sum_t d_o[t][i]*x[t][i]*inv[t]; 64 columns
-// per block, 16 interleaved row slices summed in LDS.
+// j = blockIdx.x / cb, d_w[i] = sum_t d_o[t][i]*x[t][i]*inv[t] (written: each
+// norm weight is used once per step); 64 columns per block, 16 interleaved
+// row slices summed in LDS.
 struct NormDw {
     float *d_w;
     const float *d_o, *x, *inv;
@@ -338,7 +361,7 @@ __global__ __launch_bounds__(1024) void k_rmsnorm_bwd_dw(const NormDw *nd, int c
     part[sl][c] = acc;
     __syncthreads();
     if (sl == 0 && i < D) {
-        float g = e.d_w[i];
+        float g = 0.0f;
         for (int k = 0; k < 16; k++) g += part[k][c];
         e.d_w[i] = g;
     }
@@ -538,8 +561,8 @@ void train_destroy(ptmi_model *m) {
 namespace {
 
 int gemm(hipStream_t s, TrainState *ts, int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc,
-         int M, int N, int K, int acc, const float *Cin = nullptr) {
-    return launch_gemm(op, A, lda, B, ldb, C, ldc, M, N, K, acc, ts->ws, ts->ws_floats, s, Cin);
+         int M, int N, int K, int acc, const float *Cin = nullptr, SplitK *defer = nullptr) {
+    return launch_gemm(op, A, lda, B, ldb, C, ldc, M, N, K, acc, ts->ws, ts->ws_floats, s, Cin, defer);
 }
 
 void fill0(hipStream_t s, float *p, long n) {
@@ -583,12 +606,13 @@ int train_descriptors(ptmi_model *m, int T) {
         v++;
     }
     std::vector<char> host(gemm_group_desc_bytes((int)g.size()));
-    int tiles = 0, st;
-    if ((st = gemm_tn_group_prepare(g.data(), (int)g.size(), host.data(), &tiles))) return st;
+    int tiles = 0, vec = 0, st;
+    if ((st = gemm_tn_group_prepare(g.data(), (int)g.size(), host.data(), &tiles, &vec))) return st;
     PTMI_HIP(hipMemcpy(ts->dw_desc, host.data(), host.size(), hipMemcpyHostToDevice));
     PTMI_HIP(hipMemcpy(ts->nd_desc, nd.data(), nd.size() * sizeof(NormDw), hipMemcpyHostToDevice));
     ts->n_dw = (int)g.size();
     ts->dw_tiles = tiles;
+    ts->dw_vec = vec;
     ts->desc_T = T;
     return PTMI_OK;
 }
@@ -612,26 +636,42 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     auto attn_bwd_rows = hd4 <= 8 ? k_attn_bwd_rows<8> : hd4 <= 16 ? k_attn_bwd_rows<16> : k_attn_bwd_rows<32>;
     auto attn_bwd_cols = hd4 <= 8 ? k_attn_bwd_cols<8> : hd4 <= 16 ? k_attn_bwd_cols<16> : k_attn_bwd_cols<32>;
 
-    fill0(s, ts->gmem, (long)r->mem_floats);                                        // pt_zero_grads
+    // pt_zero_grads (pt_train.c:425-427) is implicit: every gradient below is
+    // written, not accumulated, by the one kernel that produces it (0 + v is
+    // v), and gradient words no kernel produces stay at their initial zero.
+    // The one accumulation is the embedding's: with the classifier tied to
+    // it, the classifier's dW (written first) is its starting value;
+    // untied, its rows are cleared here.
+    const bool tied = r->wcls == r->emb;
+    if (!tied) fill0(s, G(r->emb), (long)V * D);
     // ── forward ──
     hipLaunchKernelGGL(k_embed_rows, dim3(T), dim3(256), 0, s, ts->tok, r->emb, ts->res, D);
+    // A split-K w2 GEMM leaves its partial sums; the next RMSNorm completes
+    // the residual stream row (adding the GEMM's residual input) and stores it.
+    SplitK pend = {};
+    const float *pend_cin = nullptr;
+    const SplitK none = {};
     for (int l = 0; l < L; l++) {
         float *rin = ts->res + l * TD, *rmid = ts->res_att + l * TD, *rout = ts->res + (l + 1) * TD;
         float *xa = ts->xb_att + l * TD, *qkv = ts->qkv + (long)l * T * QS, *att = ts->att + (long)l * NH * T * T;
         float *ao = ts->att_out + l * TD, *xf = ts->xb_ffn + l * TD, *h13 = ts->h13 + (long)l * T * 2 * H;
-        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, rin, r->rms_att + (long)l * D, xa, D);
+        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, rin, r->rms_att + (long)l * D, xa, D, pend,
+                           pend_cin);
         if ((st = gemm(s, ts, 2, xa, D, r->wqkv + (long)l * QS * D, D, qkv, QS, T, QS, D, 0))) return st;
         hipLaunchKernelGGL(k_rope_rows, dim3(blocks_for((long)T * D / 2, 256)), dim3(256), 0, s, qkv, T, D, QS, hd);
         hipLaunchKernelGGL(attn_fwd, dim3(T, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ao, T, D, QS, KV, hd, kv_mul,
                            scale);
         // residual: rmid = rin + att_out . Wo^T
         if ((st = gemm(s, ts, 2, ao, D, r->wo + (long)l * D * D, D, rmid, D, T, D, D, 1, rin))) return st;
-        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, rmid, r->rms_ffn + (long)l * D, xf, D);
+        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, rmid, r->rms_ffn + (long)l * D, xf, D, none,
+                           nullptr);
         if ((st = gemm(s, ts, 2, xf, D, r->w13 + (long)l * 2 * H * D, D, h13, 2 * H, T, 2 * H, D, 0))) return st;
         hipLaunchKernelGGL(k_swiglu_fwd, dim3(blocks_for((long)T * H, 256)), dim3(256), 0, s, h13, ts->sh, (long)T * H, H);
-        if ((st = gemm(s, ts, 2, ts->sh, H, r->w2 + (long)l * D * H, H, rout, D, T, D, H, 1, rmid))) return st;
+        if ((st = gemm(s, ts, 2, ts->sh, H, r->w2 + (long)l * D * H, H, rout, D, T, D, H, 1, rmid, &pend))) return st;
+        pend_cin = rmid;
     }
-    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, ts->res + L * TD, r->rms_final, ts->x_final, D);
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, ts->res + L * TD, r->rms_final, ts->x_final, D, pend,
+                       pend_cin);
     if ((st = gemm(s, ts, 2, ts->x_final, D, r->wcls, D, ts->logits, V, T, V, D, 0))) return st;
     hipLaunchKernelGGL(k_loss_rows, dim3(T), dim3(kLossThreads), 0, s, ts->logits, ts->tok, T, V, 1.0f / (float)(T - 1),
                        ts->row_loss);
@@ -646,14 +686,15 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     auto dres = [&](int k) { return ts->d_res + (long)k * TD; };
     auto dxb = [&](int k) { return ts->d_xb + (long)k * TD; };
     int v = 0;                                            // d_res version
+    SplitK pk = {};                                       // split-K partials of d_xb[v], if deferred
     auto norm_bwd = [&](const float *x, const float *w) {
         // d_res[v+1] = d_res[v] + rmsnorm_backward(d_xb[v]); inverse norms kept per norm
-        hipLaunchKernelGGL(k_rmsnorm_bwd_rows, dim3(R), dim3(256), 0, s, dres(v + 1), dres(v), dxb(v), x, w,
-                           ts->row_inv + (long)v * T, D);
+        hipLaunchKernelGGL(k_rmsnorm_bwd_rows, dim3(R), dim3(256), 0, s, dres(v + 1), v ? dres(v) : nullptr, dxb(v),
+                           x, w, ts->row_inv + (long)v * T, D, pk);
+        pk = SplitK{};
         v++;
     };
-    fill0(s, dres(0), (long)R * D);
-    if ((st = gemm(s, ts, 0, ts->logits, V, r->wcls, D, dxb(0), D, R, D, V, 0))) return st;
+    if ((st = gemm(s, ts, 0, ts->logits, V, r->wcls, D, dxb(0), D, R, D, V, 0, nullptr, &pk))) return st;
     norm_bwd(ts->res + L * TD, r->rms_final);
     for (int l = L - 1; l >= 0; l--) {
         const float *rin = ts->res + l * TD, *rmid = ts->res_att + l * TD;
@@ -667,7 +708,7 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         if ((st = gemm(s, ts, 0, dres(v), D, w2, H, ts->d_sh, H, R, H, D, 0))) return st;
         hipLaunchKernelGGL(k_swiglu_bwd, dim3(blocks_for((long)R * H, 256)), dim3(256), 0, s, h13, ts->d_sh, dh13,
                            shb, (long)R * H, H);
-        if ((st = gemm(s, ts, 0, dh13, 2 * H, w13, D, dxb(v), D, R, D, 2 * H, 0))) return st;
+        if ((st = gemm(s, ts, 0, dh13, 2 * H, w13, D, dxb(v), D, R, D, 2 * H, 0, nullptr, &pk))) return st;
         norm_bwd(rmid, r->rms_ffn + (long)l * D);
         // Wo
         if ((st = gemm(s, ts, 0, dres(v), D, wo, D, ts->d_aout, D, R, D, D, 0))) return st;
@@ -680,12 +721,12 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
                            ts->d_v, dqkv, R, D, KV, QS, hd);
         PTMI_HIP(hipGetLastError());
         // QKV
-        if ((st = gemm(s, ts, 0, dqkv, QS, wqkv, D, dxb(v), D, R, D, QS, 0))) return st;
+        if ((st = gemm(s, ts, 0, dqkv, QS, wqkv, D, dxb(v), D, R, D, QS, 0, nullptr, &pk))) return st;
         norm_bwd(rin, r->rms_att + (long)l * D);
     }
     PTMI_HIP(hipGetLastError());
     // weight gradients: every TN GEMM in one launch, every RMSNorm dW in one
-    if ((st = launch_gemm_tn_group(ts->dw_desc, ts->n_dw, ts->dw_tiles, s))) return st;
+    if ((st = launch_gemm_tn_group(ts->dw_desc, ts->n_dw, ts->dw_tiles, ts->dw_vec, s))) return st;
     {
         const int cb = (D + 63) / 64;
         hipLaunchKernelGGL(k_rmsnorm_bwd_dw, dim3((unsigned)((2 * L + 1) * cb)), dim3(1024), 0, s,
