@@ -218,10 +218,11 @@ def bench_train(pa, reps=20):
     blob = pa.synth_model(cfg, pa.SEED_MODEL[name])
     tokens = pa.seed_tokens(pa.SEED_TRAIN, T, cfg[5])
     m = pa.Model(blob, max_T=T)
-    m.train_step(tokens, lr)
+    for _ in range(3):                       # capture the step's graph, reach steady clocks
+        m.train_step(tokens, lr)
     t0 = time.perf_counter()
-    losses = [m.train_step(tokens, lr) for _ in range(17)]
-    step_ms = (time.perf_counter() - t0) * 1e3 / 17
+    losses = [m.train_step(tokens, lr) for _ in range(18)]
+    step_ms = (time.perf_counter() - t0) * 1e3 / 18
     m.close()
     stream = L.ptmi_stream()
     shapes = train_gemm_shapes(cfg, T)
@@ -278,6 +279,26 @@ def calib_copy(pa, mb=256):
     b.free()
 
 
+def pmc_workload(pa, name, positions):
+    """Decode positions 0..positions-1 with the step's launches enqueued
+    directly (no graph), eight steps per synchronisation, then the copy that
+    calibrates FETCH_SIZE / WRITE_SIZE.  The input token of each chunk is
+    fixed: the bytes moved do not depend on it."""
+    os.environ["PTMI_DECODE_EAGER"] = "1"
+    cfg = pa.STORIES[name]
+    blob = pa.synth_model(cfg, pa.SEED_MODEL[name])
+    prompt = pa.seed_tokens(pa.SEED_PROMPT, pa.N_PROMPT, cfg[5])
+    m = pa.Model(blob)
+    L = pa.load_ptmi()
+    m.reset_kv()
+    for k in range(0, positions, 8):
+        m.decode_async(int(prompt[0]), min(8, positions - k))
+        pa._ffi.check(L.ptmi_sync())
+    m.close()
+    calib_copy(pa)
+    print(f"[bench] pmc workload: {positions} positions of {name}, then the calibration copy", file=sys.stderr)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -292,6 +313,10 @@ def main():
                          "kernel trace on this image: the profiler's host side faults)")
     ap.add_argument("--only-train", action="store_true",
                     help="run only the training leg and print its JSON (for counter profiles), not the bench line")
+    ap.add_argument("--pmc-workload", type=int, default=0, metavar="POSITIONS",
+                    help="counter-profile workload, no timing: POSITIONS decode steps of the --config model "
+                         "enqueued without graphs, 8 at a time (rocprofv3 --pmc faults on its host side with "
+                         "thousands of dispatches in flight), then the 256 MiB calibration copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -304,6 +329,9 @@ def main():
 
     if args.only_train:
         print(json.dumps(bench_train(pa)), flush=True)
+        return
+    if args.pmc_workload:
+        pmc_workload(pa, args.config, args.pmc_workload)
         return
 
     name = args.config
