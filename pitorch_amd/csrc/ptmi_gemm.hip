@@ -39,6 +39,7 @@ struct GemmArgs {
     int accumulate;
     float *partial;        // split-K workspace [splits][M][N] or null
     int k_per_split;
+    GemmEpi epi;           // fused element-wise epilogue (whole-K launches only)
 };
 
 // One GEMM of a grouped launch: its arguments and its range of tiles.
@@ -121,7 +122,7 @@ __device__ __forceinline__ void store_tile(float (*S)[R + PD], int tid, const fl
 // LDS rows are padded so that a row's start moves by 16 banks from the
 // previous row for 64-wide tiles (the two k rows one half-wave reads
 // for the MFMA operands then fall on disjoint banks).
-template <bool AT, bool BT, int TM, int TN, int P, bool VEC>
+template <bool AT, bool BT, int TM, int TN, int P, bool VEC, int EPI = GEMM_EPI_NONE>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int z) {
     constexpr int FM = TM / 32, FN = TN / 32;          // 16x16 MFMA blocks per wave
     constexpr int EA = TM * BK / 256, EB = TN * BK / 256;
@@ -199,18 +200,38 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
         }
     }
 
-    // C[4*(l/16)+r][l%16] of each 16x16 block
+    // C[4*(l/16)+r][l%16] of each 16x16 block; columns n and n^1 of a row sit
+    // in lanes l and l^1, which the fused epilogues pair with a DPP swap
+    // (every lane reaches it: bounds are checked after).
 #pragma unroll
     for (int i = 0; i < FM; i++) {
 #pragma unroll
         for (int j = 0; j < FN; j++) {
             const int n = n0 + wn * (TN / 2) + j * 16 + li;
-            if (n >= g.N) continue;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int m = m0 + wm * (TM / 2) + i * 16 + 4 * lk + r;
-                if (m >= g.M) continue;
-                const float v = acc[i][j][r];
+                float v = acc[i][j][r];
+                if constexpr (EPI == GEMM_EPI_ROPE) {
+                    // RoPE of the q and k columns at position m (pt_ops.c:33-49;
+                    // training forward pt_train.c:217)
+                    const float pv = dpp_xor1(v);
+                    if (n < 2 * g.epi.rope_dim) {
+                        const int ip = (n < g.epi.rope_dim ? n : n - g.epi.rope_dim) & ~1;
+                        float c, sn;
+                        d_rope_cs(ip, g.epi.head_dim, m, &c, &sn);
+                        v = (n & 1) ? pv * sn + v * c : v * c - pv * sn;
+                    }
+                } else if constexpr (EPI == GEMM_EPI_SWIGLU) {
+                    // columns (2i, 2i+1) = (h1, h3): out[m][i] = (h1*sigmoid(h1))*h3,
+                    // the training form of silu (pt_train.c:280-284)
+                    const float pv = dpp_xor1(v);
+                    if (!(n & 1) && n < g.N && m < g.M) {
+                        const float sig = 1.0f / (1.0f + d_expf(-v));
+                        g.epi.out[(long)m * g.epi.ld + (n >> 1)] = (v * sig) * pv;
+                    }
+                }
+                if (n >= g.N || m >= g.M) continue;
                 if (g.partial) {
                     g.partial[((long)z * g.M + m) * g.N + n] = v;
                 } else {
@@ -222,9 +243,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
     }
 }
 
-template <bool AT, bool BT, int TM, int TN, int P, bool VEC>
+template <bool AT, bool BT, int TM, int TN, int P, bool VEC, int EPI = GEMM_EPI_NONE>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
-    gemm_tile<AT, BT, TM, TN, P, VEC>(g, blockIdx.y * TM, blockIdx.x * TN, blockIdx.z);
+    gemm_tile<AT, BT, TM, TN, P, VEC, EPI>(g, blockIdx.y * TM, blockIdx.x * TN, blockIdx.z);
 }
 
 // Grouped TN GEMMs (32x32 tiles, whole K): block b runs tile
@@ -257,8 +278,13 @@ inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 // Launch op(A).op(B) with shapes validated; `ws` (optional) is a split-K
 // workspace of ws_floats floats.
 int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc, int M, int N,
-                int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s, const float *Cin, SplitK *defer) {
+                int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s, const float *Cin, SplitK *defer,
+                const GemmEpi *epi) {
     if (defer) *defer = SplitK{nullptr, 0, 0};
+    const int ek = epi ? epi->kind : GEMM_EPI_NONE;
+    if (ek != GEMM_EPI_NONE && (op != 2 || N % 2 || (ek == GEMM_EPI_SWIGLU && !epi->out) ||
+                                (ek == GEMM_EPI_ROPE && (epi->rope_dim % 2 || epi->head_dim <= 0))))
+        return set_error(PTMI_ERR_ARG, "gemm: fused epilogue %d needs an NT GEMM with even N", ek);
     if (M <= 0 || N <= 0 || K <= 0) return set_error(PTMI_ERR_ARG, "gemm: M=%d N=%d K=%d", M, N, K);
     if (!A || !B || !C) return set_error(PTMI_ERR_ARG, "gemm: null operand");
     if (op < 0 || op > 2) return set_error(PTMI_ERR_ARG, "gemm: op %d", op);
@@ -291,7 +317,9 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
     while (splits > 1 && (size_t)splits * M * N > ws_floats) splits--;
     g.k_per_split = ((K + splits - 1) / splits + BK - 1) / BK * BK;
     splits = (K + g.k_per_split - 1) / g.k_per_split;
+    if (ek != GEMM_EPI_NONE) splits = 1, g.k_per_split = K;      // the epilogue needs whole-K sums
     g.partial = splits > 1 ? ws : nullptr;
+    g.epi = epi ? *epi : GemmEpi{};
     if (gy > 65535) return set_error(PTMI_ERR_ARG, "gemm: M too large");
     dim3 grid(gx, gy, splits);
     using KFn = void (*)(GemmArgs);
@@ -304,7 +332,16 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
           k_gemm<false, true, 64, 64, kRing64, false>},
          {k_gemm<false, false, 64, 64, kRing64, true>, k_gemm<true, false, 64, 64, kRing64, true>,
           k_gemm<false, true, 64, 64, kRing64, true>}}};
-    hipLaunchKernelGGL(kernels[big][vec][op], grid, dim3(256), 0, s, g);
+    KFn fn = kernels[big][vec][op];
+    if (ek != GEMM_EPI_NONE) {                                    // NT only
+        static const KFn fused[2][2][2] = {
+            {{k_gemm<false, true, 32, 32, kRing32, false, GEMM_EPI_ROPE>, k_gemm<false, true, 32, 32, kRing32, true, GEMM_EPI_ROPE>},
+             {k_gemm<false, true, 64, 64, kRing64, false, GEMM_EPI_ROPE>, k_gemm<false, true, 64, 64, kRing64, true, GEMM_EPI_ROPE>}},
+            {{k_gemm<false, true, 32, 32, kRing32, false, GEMM_EPI_SWIGLU>, k_gemm<false, true, 32, 32, kRing32, true, GEMM_EPI_SWIGLU>},
+             {k_gemm<false, true, 64, 64, kRing64, false, GEMM_EPI_SWIGLU>, k_gemm<false, true, 64, 64, kRing64, true, GEMM_EPI_SWIGLU>}}};
+        fn = fused[ek == GEMM_EPI_SWIGLU][big][vec];
+    }
+    hipLaunchKernelGGL(fn, grid, dim3(256), 0, s, g);
     PTMI_HIP(hipGetLastError());
     if (splits > 1 && defer) {
         *defer = SplitK{ws, splits, (long)M * N};

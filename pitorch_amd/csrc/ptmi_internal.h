@@ -285,6 +285,19 @@ __device__ __forceinline__ float sum_splits(const float *parts, int splits, long
     return v;
 }
 
+// Element-wise epilogues fused into an NT GEMM (whole K, no split):
+//  GEMM_EPI_ROPE: RoPE at position m on columns [0, 2*rope_dim) (q then k),
+//    applied to C in place;
+//  GEMM_EPI_SWIGLU: C columns (2i, 2i+1) hold (h1, h3); also writes
+//    out[m*ld + i] = (h1*sigmoid(h1))*h3.
+enum { GEMM_EPI_NONE = 0, GEMM_EPI_ROPE = 1, GEMM_EPI_SWIGLU = 2 };
+struct GemmEpi {
+    int kind;
+    float *out;            // SWIGLU output
+    long ld;               // its row stride
+    int rope_dim, head_dim;
+};
+
 // C[M,N] (+)= op(A).op(B) on the matrix cores; op 0 NN, 1 TN (A stored
 // [K][M]), 2 NT (B stored [N][K]).  ws: split-K workspace (may be null).
 // With accumulate, Cin (same leading dimension as C; null = C itself) is
@@ -293,7 +306,7 @@ __device__ __forceinline__ float sum_splits(const float *parts, int splits, long
 // C is then not written); otherwise defer->splits = 0.
 int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc, int M, int N,
                 int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s, const float *Cin = nullptr,
-                SplitK *defer = nullptr);
+                SplitK *defer = nullptr, const GemmEpi *epi = nullptr);
 
 // Grouped C[M,N] = A^T.B GEMMs (TN; A stored [K][M]; C written, not
 // accumulated), one launch of 32x32 tiles over all of them.  prepare fills host_desc (gemm_group_desc_bytes(n)

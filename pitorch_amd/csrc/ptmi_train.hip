@@ -112,22 +112,6 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(float *in, const float *w,
     for (int i = threadIdx.x; i < D; i += 256) out[r + i] = x[i] * inv * w[i];
 }
 
-// rope (pt_ops.c:33-49) on the q and k columns of each position's qkv row.
-__global__ void k_rope_rows(float *qkv, int T, int D, int QS, int hd) {
-    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    const int pairs = D / 2;
-    if (idx >= (long)T * pairs) return;
-    const int t = (int)(idx / pairs), i = 2 * (int)(idx % pairs);
-    float c, s;
-    d_rope_cs(i, hd, t, &c, &s);
-    float *q = qkv + (long)t * QS + i, *k = q + D;
-    const float q0 = q[0], q1 = q[1], k0 = k[0], k1 = k[1];
-    q[0] = q0 * c - q1 * s;
-    q[1] = q0 * s + q1 * c;
-    k[0] = k0 * c - k1 * s;
-    k[1] = k0 * s + k1 * c;
-}
-
 // Attention blocks: 256 threads; G lanes (G*4 >= head_dim) hold one
 // position's head row as float4, so a wave covers 64/G positions per load
 // and the block 256/G.
@@ -231,16 +215,6 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_fwd(const float *qkv, flo
     __syncthreads();
     const float o = weighted_rows<G>(qkv + vo, QS, sc, hd4, n, part);
     if (tid < hd) att_out[(long)t * D + h * hd + tid] = o;
-}
-
-// silu(h1)*h3 in the training form (h1*sigmoid(h1))*h3, pt_train.c:280-284.
-__global__ void k_swiglu_fwd(const float *h13, float *sh, long n, int H) {
-    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= n) return;
-    const long t = idx / H, i = idx % H;
-    const float h1 = h13[t * 2 * H + 2 * i], h3 = h13[t * 2 * H + 2 * i + 1];
-    const float sig = 1.0f / (1.0f + d_expf(-h1));
-    sh[idx] = (h1 * sig) * h3;
 }
 
 // Cross-entropy row t < T-1 (pt_train.c:310-325) and, in place, its loss
@@ -561,8 +535,9 @@ void train_destroy(ptmi_model *m) {
 namespace {
 
 int gemm(hipStream_t s, TrainState *ts, int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc,
-         int M, int N, int K, int acc, const float *Cin = nullptr, SplitK *defer = nullptr) {
-    return launch_gemm(op, A, lda, B, ldb, C, ldc, M, N, K, acc, ts->ws, ts->ws_floats, s, Cin, defer);
+         int M, int N, int K, int acc, const float *Cin = nullptr, SplitK *defer = nullptr,
+         const GemmEpi *epi = nullptr) {
+    return launch_gemm(op, A, lda, B, ldb, C, ldc, M, N, K, acc, ts->ws, ts->ws_floats, s, Cin, defer, epi);
 }
 
 void fill0(hipStream_t s, float *p, long n) {
@@ -657,16 +632,21 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         float *ao = ts->att_out + l * TD, *xf = ts->xb_ffn + l * TD, *h13 = ts->h13 + (long)l * T * 2 * H;
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, rin, r->rms_att + (long)l * D, xa, D, pend,
                            pend_cin);
-        if ((st = gemm(s, ts, 2, xa, D, r->wqkv + (long)l * QS * D, D, qkv, QS, T, QS, D, 0))) return st;
-        hipLaunchKernelGGL(k_rope_rows, dim3(blocks_for((long)T * D / 2, 256)), dim3(256), 0, s, qkv, T, D, QS, hd);
+        // qkv = x . Wqkv^T with RoPE on the q and k columns in the GEMM's epilogue
+        const GemmEpi rope = {GEMM_EPI_ROPE, nullptr, 0, D, hd};
+        if ((st = gemm(s, ts, 2, xa, D, r->wqkv + (long)l * QS * D, D, qkv, QS, T, QS, D, 0, nullptr, nullptr, &rope)))
+            return st;
         hipLaunchKernelGGL(attn_fwd, dim3(T, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ao, T, D, QS, KV, hd, kv_mul,
                            scale);
         // residual: rmid = rin + att_out . Wo^T
         if ((st = gemm(s, ts, 2, ao, D, r->wo + (long)l * D * D, D, rmid, D, T, D, D, 1, rin))) return st;
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, rmid, r->rms_ffn + (long)l * D, xf, D, none,
                            nullptr);
-        if ((st = gemm(s, ts, 2, xf, D, r->w13 + (long)l * 2 * H * D, D, h13, 2 * H, T, 2 * H, D, 0))) return st;
-        hipLaunchKernelGGL(k_swiglu_fwd, dim3(blocks_for((long)T * H, 256)), dim3(256), 0, s, h13, ts->sh, (long)T * H, H);
+        // h13 = x . W13^T (rows interleaved w1/w3), sh = silu(h1)*h3 in the GEMM's epilogue
+        const GemmEpi swiglu = {GEMM_EPI_SWIGLU, ts->sh, H, 0, 0};
+        if ((st = gemm(s, ts, 2, xf, D, r->w13 + (long)l * 2 * H * D, D, h13, 2 * H, T, 2 * H, D, 0, nullptr, nullptr,
+                       &swiglu)))
+            return st;
         if ((st = gemm(s, ts, 2, ts->sh, H, r->w2 + (long)l * D * H, H, rout, D, T, D, H, 1, rmid, &pend))) return st;
         pend_cin = rmid;
     }
