@@ -231,6 +231,22 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
                         g.epi.out[(long)m * g.epi.ld + (n >> 1)] = (v * sig) * pv;
                     }
                 }
+                if constexpr (EPI == GEMM_EPI_SWIGLU_BWD) {
+                    // silu*gate backward (pt_train.c:696-721) into the interleaved
+                    // (d_h1, d_h3) columns, plus silu(h1)*h3 for dW2
+                    if (n < g.N && m < g.M) {
+                        const float *hp = g.epi.aux + (long)m * g.epi.aux_ld + 2 * n;
+                        const float h1 = hp[0], h3 = hp[1];
+                        const float sig = 1.0f / (1.0f + d_expf(-h1));
+                        const float silu_val = h1 * sig;
+                        g.epi.out2[(long)m * g.epi.ld2 + n] = silu_val * h3;
+                        const float d_silu = v * h3;
+                        float *dp = g.epi.out + (long)m * g.epi.ld + 2 * n;
+                        dp[1] = v * silu_val;
+                        dp[0] = d_silu * sig * (1.0f + h1 * (1.0f - sig));
+                    }
+                    continue;                                   // d_sh itself is not kept
+                }
                 if (n >= g.N || m >= g.M) continue;
                 if (g.partial) {
                     g.partial[((long)z * g.M + m) * g.N + n] = v;
@@ -282,9 +298,10 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
                 const GemmEpi *epi) {
     if (defer) *defer = SplitK{nullptr, 0, 0};
     const int ek = epi ? epi->kind : GEMM_EPI_NONE;
-    if (ek != GEMM_EPI_NONE && (op != 2 || N % 2 || (ek == GEMM_EPI_SWIGLU && !epi->out) ||
-                                (ek == GEMM_EPI_ROPE && (epi->rope_dim % 2 || epi->head_dim <= 0))))
-        return set_error(PTMI_ERR_ARG, "gemm: fused epilogue %d needs an NT GEMM with even N", ek);
+    if (ek == GEMM_EPI_SWIGLU_BWD ? (op != 0 || !epi->out || !epi->out2 || !epi->aux)
+                                  : ek != GEMM_EPI_NONE && (op != 2 || N % 2 || (ek == GEMM_EPI_SWIGLU && !epi->out) ||
+                                                            (ek == GEMM_EPI_ROPE && (epi->rope_dim % 2 || epi->head_dim <= 0))))
+        return set_error(PTMI_ERR_ARG, "gemm: fused epilogue %d does not fit this GEMM", ek);
     if (M <= 0 || N <= 0 || K <= 0) return set_error(PTMI_ERR_ARG, "gemm: M=%d N=%d K=%d", M, N, K);
     if (!A || !B || !C) return set_error(PTMI_ERR_ARG, "gemm: null operand");
     if (op < 0 || op > 2) return set_error(PTMI_ERR_ARG, "gemm: op %d", op);
@@ -333,13 +350,18 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
          {k_gemm<false, false, 64, 64, kRing64, true>, k_gemm<true, false, 64, 64, kRing64, true>,
           k_gemm<false, true, 64, 64, kRing64, true>}}};
     KFn fn = kernels[big][vec][op];
-    if (ek != GEMM_EPI_NONE) {                                    // NT only
+    if (ek != GEMM_EPI_NONE) {
         static const KFn fused[2][2][2] = {
             {{k_gemm<false, true, 32, 32, kRing32, false, GEMM_EPI_ROPE>, k_gemm<false, true, 32, 32, kRing32, true, GEMM_EPI_ROPE>},
              {k_gemm<false, true, 64, 64, kRing64, false, GEMM_EPI_ROPE>, k_gemm<false, true, 64, 64, kRing64, true, GEMM_EPI_ROPE>}},
             {{k_gemm<false, true, 32, 32, kRing32, false, GEMM_EPI_SWIGLU>, k_gemm<false, true, 32, 32, kRing32, true, GEMM_EPI_SWIGLU>},
              {k_gemm<false, true, 64, 64, kRing64, false, GEMM_EPI_SWIGLU>, k_gemm<false, true, 64, 64, kRing64, true, GEMM_EPI_SWIGLU>}}};
-        fn = fused[ek == GEMM_EPI_SWIGLU][big][vec];
+        static const KFn fused_nn[2][2] = {
+            {k_gemm<false, false, 32, 32, kRing32, false, GEMM_EPI_SWIGLU_BWD>,
+             k_gemm<false, false, 32, 32, kRing32, true, GEMM_EPI_SWIGLU_BWD>},
+            {k_gemm<false, false, 64, 64, kRing64, false, GEMM_EPI_SWIGLU_BWD>,
+             k_gemm<false, false, 64, 64, kRing64, true, GEMM_EPI_SWIGLU_BWD>}};
+        fn = ek == GEMM_EPI_SWIGLU_BWD ? fused_nn[big][vec] : fused[ek == GEMM_EPI_SWIGLU][big][vec];
     }
     hipLaunchKernelGGL(fn, grid, dim3(256), 0, s, g);
     PTMI_HIP(hipGetLastError());

@@ -290,12 +290,19 @@ __device__ __forceinline__ float sum_splits(const float *parts, int splits, long
 //    applied to C in place;
 //  GEMM_EPI_SWIGLU: C columns (2i, 2i+1) hold (h1, h3); also writes
 //    out[m*ld + i] = (h1*sigmoid(h1))*h3.
-enum { GEMM_EPI_NONE = 0, GEMM_EPI_ROPE = 1, GEMM_EPI_SWIGLU = 2 };
+//  GEMM_EPI_SWIGLU_BWD (NN GEMM): C[m][i] is d_sh; with (h1, h3) =
+//    aux[m*aux_ld + 2i + {0,1}] it writes d_h1, d_h3 to out[m*ld + 2i + {0,1}]
+//    and silu(h1)*h3 to out2[m*ld2 + i]; C itself is not stored.
+enum { GEMM_EPI_NONE = 0, GEMM_EPI_ROPE = 1, GEMM_EPI_SWIGLU = 2, GEMM_EPI_SWIGLU_BWD = 3 };
 struct GemmEpi {
     int kind;
-    float *out;            // SWIGLU output
+    float *out;            // SWIGLU / SWIGLU_BWD output
     long ld;               // its row stride
     int rope_dim, head_dim;
+    float *out2;           // SWIGLU_BWD: recomputed silu(h1)*h3
+    long ld2;
+    const float *aux;      // SWIGLU_BWD: the forward's (h1, h3) pairs
+    long aux_ld;
 };
 
 // C[M,N] (+)= op(A).op(B) on the matrix cores; op 0 NN, 1 TN (A stored

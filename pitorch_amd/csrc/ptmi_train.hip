@@ -341,22 +341,6 @@ __global__ __launch_bounds__(1024) void k_rmsnorm_bwd_dw(const NormDw *nd, int c
     }
 }
 
-// silu*gate backward (pt_train.c:696-721) into interleaved [d_hid | d_hid2]
-// columns matching the w1|w3 row interleave, plus sh for dW2.
-__global__ void k_swiglu_bwd(const float *h13, const float *d_sh, float *d_h13, float *sh, long n, int H) {
-    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= n) return;
-    const long t = idx / H, i = idx % H;
-    const float h1 = h13[t * 2 * H + 2 * i], h3 = h13[t * 2 * H + 2 * i + 1];
-    const float sig = 1.0f / (1.0f + d_expf(-h1));
-    const float silu_val = h1 * sig;
-    sh[idx] = silu_val * h3;
-    const float dh = d_sh[idx];
-    const float d_silu = dh * h3;
-    d_h13[t * 2 * H + 2 * i + 1] = dh * silu_val;
-    d_h13[t * 2 * H + 2 * i] = d_silu * sig * (1.0f + h1 * (1.0f - sig));
-}
-
 // Attention backward, row half (pt_train.c:780-811): for (t < R, head h):
 // d_att_s, the softmax backward dot, ds = d_pre*scale (kept for the column
 // half) and d_q[t] = sum_t2 ds[t2] k[t2].  Dynamic LDS: das[T].
@@ -685,9 +669,10 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         float *dh13 = ts->d_h13 + (long)l * T * 2 * H, *shb = ts->shb + (long)l * T * H;
         float *dqkv = ts->d_qkv + (long)l * T * QS;
         // FFN
-        if ((st = gemm(s, ts, 0, dres(v), D, w2, H, ts->d_sh, H, R, H, D, 0))) return st;
-        hipLaunchKernelGGL(k_swiglu_bwd, dim3(blocks_for((long)R * H, 256)), dim3(256), 0, s, h13, ts->d_sh, dh13,
-                           shb, (long)R * H, H);
+        // d_sh = d_res . W2, consumed in the GEMM's epilogue by the swiglu
+        // backward: d_h13 (interleaved d_h1, d_h3) and shb = silu(h1)*h3
+        GemmEpi sgb = {GEMM_EPI_SWIGLU_BWD, dh13, 2 * H, 0, 0, shb, H, h13, 2 * H};
+        if ((st = gemm(s, ts, 0, dres(v), D, w2, H, ts->d_sh, H, R, H, D, 0, nullptr, nullptr, &sgb))) return st;
         if ((st = gemm(s, ts, 0, dh13, 2 * H, w13, D, dxb(v), D, R, D, 2 * H, 0, nullptr, &pk))) return st;
         norm_bwd(rmid, r->rms_ffn + (long)l * D);
         // Wo
