@@ -519,7 +519,6 @@ int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     if (p.rows <= 0 || p.n <= 0) return set_error(PTMI_ERR_ARG, "matvec: rows=%d n=%d", p.rows, p.n);
     if (!p.W || !p.x || !p.y) return set_error(PTMI_ERR_ARG, "matvec: null pointer");
     if (p.ld < p.n) return set_error(PTMI_ERR_ARG, "matvec: ld=%ld < n=%d", p.ld, p.n);
-    const int n4 = p.n / 4;
     if (p.pro == PRO_ATTN_COMBINE &&
         (!p.att_o || !p.att_ml || !p.pos || p.att_heads <= 0 || p.att_heads > kMaxCombineHeads ||
          p.n % p.att_heads || p.n > kMaxCombineDim || p.att_chunk <= 0 || p.att_chunks <= 0 ||

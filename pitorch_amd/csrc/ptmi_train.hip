@@ -273,6 +273,63 @@ __global__ __launch_bounds__(kLossThreads) void k_loss_rows(float *lg_dl, const 
     }
 }
 
+// The same row loss and gradient with the row held in registers, for rows of
+// V % 4 == 0 and V <= 4 * NS * kLossThreads: one read and one write of the
+// logits and one exp per element.  The maximum comes first, then the sum of
+// e^(x - max) (the reference's loss order, pt_train.c:311-323), and the
+// gradient is formed from the kept exps.  Loads are unconditional (clamped
+// to the row) and out-of-row slots are dropped by selects.
+template <int NS>
+__global__ __launch_bounds__(kLossThreads) void k_loss_rows_reg(float *lg_dl, const int *tok, int T, int V,
+                                                                float inv_T1, float *row_loss) {
+    __shared__ float red[kLossThreads / 64];
+    const int t = blockIdx.x, tid = threadIdx.x, n4 = V / 4;
+    float4 *row4 = reinterpret_cast<float4 *>(lg_dl + (long)t * V);
+    if (t == T - 1) {
+        for (int v = tid; v < n4; v += kLossThreads) row4[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+        return;
+    }
+    const int target = tok[t + 1];
+    const float xt = lg_dl[(long)t * V + target];
+    float4 x[NS];
+#pragma unroll
+    for (int i = 0; i < NS; i++) x[i] = row4[min(tid + i * kLossThreads, n4 - 1)];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        const float mi = fmaxf(fmaxf(x[i].x, x[i].y), fmaxf(x[i].z, x[i].w));
+        m = tid + i * kLossThreads < n4 ? fmaxf(m, mi) : m;
+    }
+    const float mx = block_max<kLossThreads / 64>(m, red);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        x[i].x = d_expf(x[i].x - mx);
+        x[i].y = d_expf(x[i].y - mx);
+        x[i].z = d_expf(x[i].z - mx);
+        x[i].w = d_expf(x[i].w - mx);
+        const float si = x[i].x + x[i].y + x[i].z + x[i].w;
+        s = tid + i * kLossThreads < n4 ? s + si : s;
+    }
+    const float sum = block_sum<kLossThreads / 64>(s, red);
+    if (tid == 0) row_loss[t] = -(xt - mx - d_logf(sum));
+    const float scale = (1.0f / sum) * inv_T1;
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        const int v = tid + i * kLossThreads;
+        if (v < n4) {
+            float4 d;
+            d.x = x[i].x * scale;
+            d.y = x[i].y * scale;
+            d.z = x[i].z * scale;
+            d.w = x[i].w * scale;
+            const int b = 4 * v;
+            if (target >= b && target < b + 4) (&d.x)[target - b] -= inv_T1;
+            row4[v] = d;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void k_loss_reduce(const float *row_loss, int T, float *loss) {
     __shared__ float red[4];
     float l = 0.0f;
@@ -423,19 +480,30 @@ __global__ void k_rope_bwd_pack(const float *d_q, const float *d_k, const float 
 
 // embedding_backward (pt_backward_ops.c:90-95) in the reference's order:
 // the block of the first position holding a token accumulates, per column,
-// every position with that token in ascending t.  Dynamic LDS: tok[R].
+// every position with that token in ascending t.  One pass over tok marks
+// the block's positions in an LDS bit mask (any earlier one hands the token
+// to an earlier block); each column then walks the mask in ascending order.
+// Dynamic LDS: (R + 31) / 32 words.
 __global__ __launch_bounds__(256) void k_embed_bwd(const int *tok, const float *d_res, float *g_emb, int R, int D) {
-    extern __shared__ int stok[];
-    const int t = blockIdx.x;
-    for (int k = threadIdx.x; k < R; k += 256) stok[k] = tok[k];
+    extern __shared__ unsigned pmask[];
+    const int t = blockIdx.x, nw = (R + 31) / 32;
+    const int tk = tok[t];
+    for (int w = threadIdx.x; w < nw; w += 256) pmask[w] = 0u;
     __syncthreads();
-    const int tk = stok[t];
-    for (int k = 0; k < t; k++)
-        if (stok[k] == tk) return;                  // uniform: an earlier block owns this token
+    int earlier = 0;
+    for (int k = threadIdx.x; k < R; k += 256) {
+        if (tok[k] == tk) {
+            if (k < t) earlier = 1;
+            else atomicOr(&pmask[k >> 5], 1u << (k & 31));
+        }
+    }
+    if (__syncthreads_or(earlier)) return;          // uniform: an earlier block owns this token
     for (int j = threadIdx.x; j < D; j += 256) {
         float acc = g_emb[(long)tk * D + j];
-        for (int k = t; k < R; k++)
-            if (stok[k] == tk) acc += d_res[(long)k * D + j];
+        for (int w = 0; w < nw; w++) {
+            for (unsigned bits = pmask[w]; bits; bits &= bits - 1)
+                acc += d_res[(long)(32 * w + __builtin_ctz(bits)) * D + j];
+        }
         g_emb[(long)tk * D + j] = acc;
     }
 }
@@ -637,8 +705,18 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, ts->res + L * TD, r->rms_final, ts->x_final, D, pend,
                        pend_cin);
     if ((st = gemm(s, ts, 2, ts->x_final, D, r->wcls, D, ts->logits, V, T, V, D, 0))) return st;
-    hipLaunchKernelGGL(k_loss_rows, dim3(T), dim3(kLossThreads), 0, s, ts->logits, ts->tok, T, V, 1.0f / (float)(T - 1),
-                       ts->row_loss);
+    {
+        using LossFn = void (*)(float *, const int *, int, int, float, float *);
+        const int slots = (V / 4 + kLossThreads - 1) / kLossThreads;
+        const LossFn loss = V % 4 ? k_loss_rows
+                            : slots <= 1 ? k_loss_rows_reg<1>
+                            : slots <= 2 ? k_loss_rows_reg<2>
+                            : slots <= 4 ? k_loss_rows_reg<4>
+                            : slots <= 8 ? k_loss_rows_reg<8>
+                                         : k_loss_rows;
+        hipLaunchKernelGGL(loss, dim3(T), dim3(kLossThreads), 0, s, ts->logits, ts->tok, T, V, 1.0f / (float)(T - 1),
+                           ts->row_loss);
+    }
     hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, s, ts->row_loss, T, ts->loss);
     PTMI_HIP(hipGetLastError());
 
@@ -698,7 +776,7 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
                            reinterpret_cast<const NormDw *>(ts->nd_desc), cb, R, D);
         PTMI_HIP(hipGetLastError());
     }
-    hipLaunchKernelGGL(k_embed_bwd, dim3(R), dim3(256), (size_t)R * sizeof(int), s, ts->tok, dres(v), G(r->emb), R, D);
+    hipLaunchKernelGGL(k_embed_bwd, dim3(R), dim3(256), (size_t)(R + 31) / 32 * sizeof(unsigned), s, ts->tok, dres(v), G(r->emb), R, D);
     // ── SGD ──
     hipLaunchKernelGGL(k_sgd, dim3(blocks_for((long)r->mem_floats, 256)), dim3(256), 0, s, r->mem, ts->gmem, ts->lr,
                        (long)r->mem_floats);
