@@ -457,6 +457,383 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_cols(const float *qkv
     }
 }
 
+// ── attention on the matrix cores ────────────────────────────────────────
+// The same three attention kernels for head_dim = 16*HQ (HQ <= 8), with
+// n_kv_heads == n_heads (training requires it), on v_mfma_f32_16x16x4_f32.
+// One block of kMW waves per (16-row tile, head).  Lane l supplies
+// A[l%16][l/16] and B[l/16][l%16]; result register r of lane l is
+// C[4*(l/16)+r][l%16].  A and B may share any order of the contraction
+// index: over head_dim, lane group g = l/16 takes the quarter
+// [4*HQ*g, 4*HQ*(g+1)) as HQ float4s (step 4q+c uses component c of float4
+// q); over positions, step s of a 16-position block takes position 4g + s,
+// so a lane's four weights are one float4 in LDS.  Sums therefore run in a
+// different order from the reference's sequential loops.
+constexpr int kMW = 8, kMT = 64 * kMW;
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4v mfma4(float a, float b, f4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// sc[i][16*kb + j] = mul * (a[r0+i] . b[16*kb+j]) over head_dim for this
+// wave's key blocks kb = wave, wave + kMW, ... < nkb (LDS rows of `pitch`
+// floats).  Rows past a_rows / b_rows read the operand's last row; those
+// entries are never used.
+template <int HQ>
+__device__ __forceinline__ void attn_dots(const float *a, long lda, int r0, int a_rows, const float *b, long ldb,
+                                          int b_rows, int nkb, float mul, float *sc, int pitch) {
+    constexpr int U = HQ <= 3 ? 2 : 1;                 // key blocks in flight per wave
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
+    float4 av[HQ];
+    const float4 *ap = reinterpret_cast<const float4 *>(a + (long)min(r0 + li, a_rows - 1) * lda) + g * HQ;
+#pragma unroll
+    for (int q = 0; q < HQ; q++) av[q] = ap[q];
+    for (int kb0 = wave; kb0 < nkb; kb0 += U * kMW) {
+        float4 bv[U][HQ];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int key = min((kb0 + u * kMW) * 16 + li, b_rows - 1);
+            const float4 *bp = reinterpret_cast<const float4 *>(b + (long)key * ldb) + g * HQ;
+#pragma unroll
+            for (int q = 0; q < HQ; q++) bv[u][q] = bp[q];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int kb = kb0 + u * kMW;
+            f4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q = 0; q < HQ; q++) {
+                acc = mfma4(av[q].x, bv[u][q].x, acc);
+                acc = mfma4(av[q].y, bv[u][q].y, acc);
+                acc = mfma4(av[q].z, bv[u][q].z, acc);
+                acc = mfma4(av[q].w, bv[u][q].w, acc);
+            }
+            if (kb < nkb) {                                 // uniform
+#pragma unroll
+                for (int r = 0; r < 4; r++) sc[(4 * g + r) * pitch + kb * 16 + li] = acc[r] * mul;
+            }
+        }
+    }
+}
+
+// acc[cb] = this wave's share of sum_key sc[i][key] * v[key][16*cb + j]
+// over its key blocks (the weights in LDS rows of `pitch` floats).  load()
+// fetches the operand rows of the wave's first U key blocks and may be
+// issued before the weights are ready; run() fetches any further ones.
+template <int HQ>
+struct AttnWsum {
+    static constexpr int U = HQ <= 3 ? 2 : 1;
+    float vv[U][4][HQ];
+    __device__ __forceinline__ void load(const float *v, long ldv, int v_rows, int kb0) {
+        const int lane = threadIdx.x & 63, li = lane & 15, g = lane >> 4;
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const int key = min((kb0 + u * kMW) * 16 + 4 * g + s, v_rows - 1);
+#pragma unroll
+                for (int cb = 0; cb < HQ; cb++) vv[u][s][cb] = v[(long)key * ldv + cb * 16 + li];
+            }
+    }
+    __device__ __forceinline__ void run(const float *sc, int pitch, const float *v, long ldv, int v_rows, int nkb,
+                                        f4v (&acc)[HQ]) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
+#pragma unroll
+        for (int cb = 0; cb < HQ; cb++) acc[cb] = f4v{0.f, 0.f, 0.f, 0.f};
+        for (int kb0 = wave; kb0 < nkb; kb0 += U * kMW) {
+            if (kb0 != wave) load(v, ldv, v_rows, kb0);     // uniform
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int kb = kb0 + u * kMW;
+                if (kb < nkb) {                             // uniform
+                    const float4 w = *reinterpret_cast<const float4 *>(sc + li * pitch + kb * 16 + 4 * g);
+#pragma unroll
+                    for (int cb = 0; cb < HQ; cb++) {
+                        acc[cb] = mfma4(w.x, vv[u][0][cb], acc[cb]);
+                        acc[cb] = mfma4(w.y, vv[u][1][cb], acc[cb]);
+                        acc[cb] = mfma4(w.z, vv[u][2][cb], acc[cb]);
+                        acc[cb] = mfma4(w.w, vv[u][3][cb], acc[cb]);
+                    }
+                }
+            }
+        }
+    }
+};
+
+// A row's first kw (a multiple of 16) LDS entries, 4 consecutive per lane
+// in up to kAttnChunks chunks of 256 (T <= 1024): x[c] holds keys
+// 256c + 4*lane + (0..3); chunks at or past kw read as zeros.  Addresses
+// are clamped into the row so that every lane's read stays inside it.
+constexpr int kAttnChunks = 4;
+__device__ __forceinline__ void row_chunks(const float *row, int kw, float4 (&x)[kAttnChunks]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int c = 0; c < kAttnChunks; c++) {
+        x[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (256 * c < kw) x[c] = *reinterpret_cast<const float4 *>(row + min(256 * c + 4 * lane, kw - 4));
+    }
+}
+
+// Sum / max over the 64 lanes of a wave, returned to every lane: DPP within
+// each row of 16 lanes (quad xor 1, quad xor 2, half-row mirror, row
+// mirror), then the four row results read as scalars.  No LDS round trips.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
+// Sums the kMW waves' 16 x 16*HQ tiles in wave order through LDS `red`
+// (kMW*16*16*HQ floats) and hands each element to out(i, c, value).
+template <int HQ, typename F>
+__device__ __forceinline__ void attn_reduce(const f4v (&acc)[HQ], float *red, F &&out) {
+    constexpr int HD = 16 * HQ;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
+    __syncthreads();                                       // earlier readers of red are done
+#pragma unroll
+    for (int cb = 0; cb < HQ; cb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) red[(wave * 16 + 4 * g + r) * HD + cb * 16 + li] = acc[cb][r];
+    __syncthreads();
+    for (int e = threadIdx.x; e < 16 * HD; e += kMT) {
+        float v = red[e];
+#pragma unroll
+        for (int w = 1; w < kMW; w++) v += red[w * 16 * HD + e];
+        out(e / HD, e % HD, v);
+    }
+}
+
+// Causal attention forward (pt_train.c:224-255) for positions
+// [16*blockIdx.x, +16) of head blockIdx.y: scores into LDS, a softmax per
+// row (one wave per row; max, then e^(s - max) and its sum, then the 1/sum
+// scaling, as the reference), the probabilities to att (zeros past the
+// diagonal), then att_out = P.V.  Dynamic LDS: max(16*pitch, kMW*16*hd)
+// floats, pitch = 16*ceil(T/16) + 4.
+template <int HQ>
+__global__ __launch_bounds__(kMT) void k_attn_fwd_mfma(const float *qkv, float *att, float *att_out, int T, int D,
+                                                      int QS, float scale, int pitch) {
+    extern __shared__ float lds[];
+    constexpr int HD = 16 * HQ;
+    const int r0 = blockIdx.x * 16, h = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nkb = (min(r0 + 16, T) + 15) / 16, kw = nkb * 16;
+    const float *q = qkv + h * HD, *k = qkv + D + h * HD, *v = qkv + 2 * D + h * HD;
+    attn_dots<HQ>(q, QS, r0, T, k, QS, T, nkb, scale, lds, pitch);
+    AttnWsum<HQ> ws;
+    ws.load(v, QS, T, wave);                                // in flight during the softmax
+    __syncthreads();
+    // the wave's rows i = wave + w*kMW, in lockstep (rows past T compute
+    // unused values and store nothing)
+    constexpr int RW = 16 / kMW;
+    float4 x[RW][kAttnChunks];
+    float mx[RW], sum[RW];
+#pragma unroll
+    for (int w = 0; w < RW; w++) {
+        const int n = r0 + wave + w * kMW + 1;
+        row_chunks(lds + (wave + w * kMW) * pitch, kw, x[w]);
+        mx[w] = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; c++) {
+            const int j = 256 * c + 4 * lane;
+#pragma unroll
+            for (int e = 0; e < 4; e++) mx[w] = j + e < n ? fmaxf(mx[w], (&x[w][c].x)[e]) : mx[w];
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < RW; w++) mx[w] = wave_max(mx[w]);
+#pragma unroll
+    for (int w = 0; w < RW; w++) {
+        const int n = r0 + wave + w * kMW + 1;
+        sum[w] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; c++) {
+            if (256 * c < kw) {                             // uniform
+                const int j = 256 * c + 4 * lane;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float ex = j + e < n ? d_expf((&x[w][c].x)[e] - mx[w]) : 0.0f;
+                    (&x[w][c].x)[e] = ex;
+                    sum[w] += ex;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < RW; w++) sum[w] = wave_sum(sum[w]);
+#pragma unroll
+    for (int w = 0; w < RW; w++) {
+        const int i = wave + w * kMW, t = r0 + i;
+        if (t >= T) continue;                               // uniform
+        const float inv = 1.0f / sum[w];
+        float *row = lds + i * pitch, *arow = att + ((long)h * T + t) * T;
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; c++) {
+            const int j = 256 * c + 4 * lane;
+            const float4 a = make_float4(x[w][c].x * inv, x[w][c].y * inv, x[w][c].z * inv, x[w][c].w * inv);
+            if (j < kw) *reinterpret_cast<float4 *>(row + j) = a;
+            if ((T & 3) == 0) {
+                if (j < T) *reinterpret_cast<float4 *>(arow + j) = a;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (j + e < T) arow[j + e] = (&a.x)[e];
+            }
+        }
+    }
+    __syncthreads();
+    f4v acc[HQ];
+    ws.run(lds, pitch, v, QS, T, nkb, acc);
+    attn_reduce<HQ>(acc, lds, [&](int i, int c, float o) {
+        if (r0 + i < T) att_out[(long)(r0 + i) * D + h * HD + c] = o;
+    });
+}
+
+// Attention backward, row half (pt_train.c:780-811) for rows t < R in
+// [16*blockIdx.x, +16) of head blockIdx.y: d_att = d_aout.V^T into LDS, per
+// row the softmax backward dot and ds = att*(d_att - dot)*scale (kept for
+// the column half), then d_q = ds.K.  LDS as k_attn_fwd_mfma.
+template <int HQ>
+__global__ __launch_bounds__(kMT) void k_attn_bwd_rows_mfma(const float *qkv, const float *att, const float *d_aout,
+                                                           float *ds, float *d_q, int T, int R, int D, int QS,
+                                                           float scale, int pitch) {
+    extern __shared__ float lds[];
+    constexpr int HD = 16 * HQ, RW = 16 / kMW;             // rows per wave
+    const int r0 = blockIdx.x * 16, h = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nkb = (min(r0 + 16, R) + 15) / 16, kw = nkb * 16;
+    const float *k = qkv + D + h * HD, *v = qkv + 2 * D + h * HD;
+    // this wave's att rows (keys < n, clamped), fetched with the GEMM operands
+    float ar[RW][kAttnChunks][4];
+#pragma unroll
+    for (int w = 0; w < RW; w++) {
+        const int t = min(r0 + wave + w * kMW, R - 1);
+        const float *arow = att + ((long)h * T + t) * T;
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; c++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) ar[w][c][e] = 256 * c < kw ? arow[min(256 * c + 4 * lane + e, t)] : 0.0f;
+    }
+    attn_dots<HQ>(d_aout + h * HD, D, r0, R, v, QS, T, nkb, 1.0f, lds, pitch);
+    AttnWsum<HQ> ws;
+    ws.load(k, QS, T, wave);
+    __syncthreads();
+    // the wave's rows i = wave + w*kMW in lockstep, as in the forward
+    float4 x[RW][kAttnChunks];
+    float dot[RW];
+#pragma unroll
+    for (int w = 0; w < RW; w++) {
+        const int n = r0 + wave + w * kMW + 1;
+        row_chunks(lds + (wave + w * kMW) * pitch, kw, x[w]);
+        dot[w] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; c++) {
+            const int j = 256 * c + 4 * lane;
+#pragma unroll
+            for (int e = 0; e < 4; e++) dot[w] = j + e < n ? dot[w] + (&x[w][c].x)[e] * ar[w][c][e] : dot[w];
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < RW; w++) dot[w] = wave_sum(dot[w]);
+#pragma unroll
+    for (int w = 0; w < RW; w++) {
+        const int i = wave + w * kMW, t = r0 + i;
+        if (t >= R) continue;                               // uniform
+        const int n = t + 1;
+        float *row = lds + i * pitch, *dsrow = ds + ((long)h * T + t) * T;
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; c++) {
+            if (256 * c < kw) {                             // uniform
+                const int j = 256 * c + 4 * lane;
+                float4 d;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const bool in = j + e < n;
+                    (&d.x)[e] = in ? ar[w][c][e] * ((&x[w][c].x)[e] - dot[w]) * scale : 0.0f;
+                    if (in) dsrow[j + e] = (&d.x)[e];
+                }
+                if (j < kw) *reinterpret_cast<float4 *>(row + j) = d;
+            }
+        }
+    }
+    __syncthreads();
+    f4v acc[HQ];
+    ws.run(lds, pitch, k, QS, T, nkb, acc);
+    attn_reduce<HQ>(acc, lds, [&](int i, int c, float o) {
+        if (r0 + i < R) d_q[(long)(r0 + i) * D + h * HD + c] = o;
+    });
+}
+
+// Attention backward, column half, for keys t2 < R in [16*blockIdx.x, +16)
+// of head blockIdx.y: d_v[t2] = sum_{t2<=t<R} att[t][t2] d_aout[t] and
+// d_k[t2] = sum_{t2<=t<R} ds[t][t2] q[t].  ds holds only t2 <= t, so the
+// weights are selected (never multiplied) by that condition.  Dynamic LDS:
+// kMW*16*hd floats.
+template <int HQ>
+__global__ __launch_bounds__(kMT) void k_attn_bwd_cols_mfma(const float *qkv, const float *att, const float *ds,
+                                                           const float *d_aout, float *d_k, float *d_v, int T, int R,
+                                                           int D, int QS) {
+    extern __shared__ float lds[];
+    constexpr int HD = 16 * HQ, U = HQ <= 3 ? 2 : 1;
+    const int k0 = blockIdx.x * 16, h = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int li = lane & 15, g = lane >> 4, ntb = (R + 15) / 16;
+    const int key = min(k0 + li, T - 1);
+    const float *q = qkv + h * HD, *go = d_aout + h * HD;
+    const float *ah = att + (long)h * T * T + key, *dh = ds + (long)h * T * T + key;
+    f4v av[HQ], ak[HQ];
+#pragma unroll
+    for (int cb = 0; cb < HQ; cb++) av[cb] = ak[cb] = f4v{0.f, 0.f, 0.f, 0.f};
+    for (int tb0 = blockIdx.x + wave; tb0 < ntb; tb0 += U * kMW) {
+        float wa[U][4], wd[U][4], bo[U][4][HQ], bq[U][4][HQ];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const int t = min((tb0 + u * kMW) * 16 + 4 * g + s, R - 1);
+                wa[u][s] = ah[(long)t * T];
+                wd[u][s] = dh[(long)t * T];
+#pragma unroll
+                for (int cb = 0; cb < HQ; cb++) {
+                    bo[u][s][cb] = go[(long)t * D + cb * 16 + li];
+                    bq[u][s][cb] = q[(long)t * QS + cb * 16 + li];
+                }
+            }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const int t = (tb0 + u * kMW) * 16 + 4 * g + s;
+                const bool use = t < R && t >= k0 + li;
+                const float a1 = use ? wa[u][s] : 0.0f, a2 = use ? wd[u][s] : 0.0f;
+#pragma unroll
+                for (int cb = 0; cb < HQ; cb++) {
+                    av[cb] = mfma4(a1, bo[u][s][cb], av[cb]);
+                    ak[cb] = mfma4(a2, bq[u][s][cb], ak[cb]);
+                }
+            }
+    }
+    attn_reduce<HQ>(av, lds, [&](int i, int c, float o) {
+        if (k0 + i < R) d_v[(long)(k0 + i) * D + h * HD + c] = o;
+    });
+    attn_reduce<HQ>(ak, lds, [&](int i, int c, float o) {
+        if (k0 + i < R) d_k[(long)(k0 + i) * D + h * HD + c] = o;
+    });
+}
+
 // rope_backward (pt_backward_ops.c:52-69) of d_q, d_k, packed with d_v into
 // the fused [dq | dk | dv] row used by the QKV GEMMs.
 __global__ void k_rope_bwd_pack(const float *d_q, const float *d_k, const float *d_v, float *d_qkv, int R, int D,
@@ -662,6 +1039,27 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     auto attn_fwd = hd4 <= 8 ? k_attn_fwd<8> : hd4 <= 16 ? k_attn_fwd<16> : k_attn_fwd<32>;
     auto attn_bwd_rows = hd4 <= 8 ? k_attn_bwd_rows<8> : hd4 <= 16 ? k_attn_bwd_rows<16> : k_attn_bwd_rows<32>;
     auto attn_bwd_cols = hd4 <= 8 ? k_attn_bwd_cols<8> : hd4 <= 16 ? k_attn_bwd_cols<16> : k_attn_bwd_cols<32>;
+    // The matrix-core attention kernels when head_dim is a multiple of 16 (up
+    // to 128), a row fits the softmax's registers and the LDS fits in 64 KB;
+    // otherwise the per-position ones.
+    using MfFwd = void (*)(const float *, float *, float *, int, int, int, float, int);
+    using MfRows = void (*)(const float *, const float *, const float *, float *, float *, int, int, int, int, float,
+                            int);
+    using MfCols = void (*)(const float *, const float *, const float *, const float *, float *, float *, int, int, int,
+                            int);
+    static const MfFwd mf_fwd[8] = {k_attn_fwd_mfma<1>, k_attn_fwd_mfma<2>, k_attn_fwd_mfma<3>, k_attn_fwd_mfma<4>,
+                                    k_attn_fwd_mfma<5>, k_attn_fwd_mfma<6>, k_attn_fwd_mfma<7>, k_attn_fwd_mfma<8>};
+    static const MfRows mf_rows[8] = {k_attn_bwd_rows_mfma<1>, k_attn_bwd_rows_mfma<2>, k_attn_bwd_rows_mfma<3>,
+                                      k_attn_bwd_rows_mfma<4>, k_attn_bwd_rows_mfma<5>, k_attn_bwd_rows_mfma<6>,
+                                      k_attn_bwd_rows_mfma<7>, k_attn_bwd_rows_mfma<8>};
+    static const MfCols mf_cols[8] = {k_attn_bwd_cols_mfma<1>, k_attn_bwd_cols_mfma<2>, k_attn_bwd_cols_mfma<3>,
+                                      k_attn_bwd_cols_mfma<4>, k_attn_bwd_cols_mfma<5>, k_attn_bwd_cols_mfma<6>,
+                                      k_attn_bwd_cols_mfma<7>, k_attn_bwd_cols_mfma<8>};
+    const int HQ = hd / 16, pitch = (T + 15) / 16 * 16 + 4;
+    const size_t mf_lds = std::max<size_t>((size_t)16 * pitch, (size_t)kMW * 16 * hd) * sizeof(float);
+    const size_t mc_lds = (size_t)kMW * 16 * hd * sizeof(float);
+    const bool mfma_attn =
+        hd % 16 == 0 && HQ >= 1 && HQ <= 8 && KV == D && T <= 256 * kAttnChunks && mf_lds <= 65536;
 
     // pt_zero_grads (pt_train.c:425-427) is implicit: every gradient below is
     // written, not accumulated, by the one kernel that produces it (0 + v is
@@ -688,8 +1086,12 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         const GemmEpi rope = {GEMM_EPI_ROPE, nullptr, 0, D, hd};
         if ((st = gemm(s, ts, 2, xa, D, r->wqkv + (long)l * QS * D, D, qkv, QS, T, QS, D, 0, nullptr, nullptr, &rope)))
             return st;
-        hipLaunchKernelGGL(attn_fwd, dim3(T, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ao, T, D, QS, KV, hd, kv_mul,
-                           scale);
+        if (mfma_attn)
+            hipLaunchKernelGGL(mf_fwd[HQ - 1], dim3((T + 15) / 16, NH), dim3(kMT), mf_lds, s, qkv, att, ao, T, D, QS,
+                               scale, pitch);
+        else
+            hipLaunchKernelGGL(attn_fwd, dim3(T, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ao, T, D, QS, KV, hd,
+                               kv_mul, scale);
         // residual: rmid = rin + att_out . Wo^T
         if ((st = gemm(s, ts, 2, ao, D, r->wo + (long)l * D * D, D, rmid, D, T, D, D, 1, rin))) return st;
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, rmid, r->rms_ffn + (long)l * D, xf, D, none,
@@ -756,10 +1158,17 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         // Wo
         if ((st = gemm(s, ts, 0, dres(v), D, wo, D, ts->d_aout, D, R, D, D, 0))) return st;
         // attention
-        hipLaunchKernelGGL(attn_bwd_rows, dim3(R, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ts->d_aout, ts->ds, ts->d_q,
-                           T, D, QS, KV, hd, kv_mul, scale);
-        hipLaunchKernelGGL(attn_bwd_cols, dim3(R, NH), dim3(kAttnThreads), 2 * att_lds, s, qkv, att, ts->ds, ts->d_aout,
-                           ts->d_k, ts->d_v, T, R, D, QS, KV, hd, kv_mul);
+        if (mfma_attn) {
+            hipLaunchKernelGGL(mf_rows[HQ - 1], dim3((R + 15) / 16, NH), dim3(kMT), mf_lds, s, qkv, att, ts->d_aout,
+                               ts->ds, ts->d_q, T, R, D, QS, scale, pitch);
+            hipLaunchKernelGGL(mf_cols[HQ - 1], dim3((R + 15) / 16, NH), dim3(kMT), mc_lds, s, qkv, att, ts->ds,
+                               ts->d_aout, ts->d_k, ts->d_v, T, R, D, QS);
+        } else {
+            hipLaunchKernelGGL(attn_bwd_rows, dim3(R, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ts->d_aout, ts->ds,
+                               ts->d_q, T, D, QS, KV, hd, kv_mul, scale);
+            hipLaunchKernelGGL(attn_bwd_cols, dim3(R, NH), dim3(kAttnThreads), 2 * att_lds, s, qkv, att, ts->ds,
+                               ts->d_aout, ts->d_k, ts->d_v, T, R, D, QS, KV, hd, kv_mul);
+        }
         hipLaunchKernelGGL(k_rope_bwd_pack, dim3(blocks_for((long)R * D / 2, 256)), dim3(256), 0, s, ts->d_q, ts->d_k,
                            ts->d_v, dqkv, R, D, KV, QS, hd);
         PTMI_HIP(hipGetLastError());
