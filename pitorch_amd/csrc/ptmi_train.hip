@@ -79,6 +79,31 @@ __device__ __forceinline__ float block_max(float v, float *red) {
     return m;
 }
 
+// Sum / max over the 64 lanes of a wave, returned to every lane: DPP within
+// each row of 16 lanes (quad xor 1, quad xor 2, half-row mirror, row
+// mirror), then the four row results read as scalars.  No LDS round trips.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
 __device__ __forceinline__ float dot4(float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
 
 // ── forward kernels ──────────────────────────────────────────────────────
@@ -371,6 +396,136 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd_rows(float *d_out, const fl
     }
 }
 
+// ── RMSNorm rows, one wave per row ──────────────────────────────────────
+// The same two row kernels for D % 4 == 0 and D <= 256*NV: four rows per
+// 256-thread block, lane l holding float4s l, 64 + l, ... of its row in
+// registers, so every load of the row goes out together and the row sums
+// are DPP reductions without block barriers.
+
+// float4 i of row r of a split-K GEMM's output: sum_z parts[z] in z order,
+// eight partial loads in flight at a time.
+__device__ __forceinline__ float4 sum_splits4(const SplitK &pk, long i4) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 *p = reinterpret_cast<const float4 *>(pk.parts);
+    const long st4 = pk.stride / 4;
+    for (int z0 = 0; z0 < pk.splits; z0 += 8) {
+        float4 pv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) pv[u] = p[(long)min(z0 + u, pk.splits - 1) * st4 + i4];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const bool in = z0 + u < pk.splits;
+            v.x = in ? v.x + pv[u].x : v.x;
+            v.y = in ? v.y + pv[u].y : v.y;
+            v.z = in ? v.z + pv[u].z : v.z;
+            v.w = in ? v.w + pv[u].w : v.w;
+        }
+    }
+    return v;
+}
+
+__device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
+
+// k_rmsnorm_rows, one wave per row (rmsnorm, pt_ops.c:5-12).
+template <int NV>
+__global__ __launch_bounds__(256) void k_rmsnorm_rows_w(float *in, const float *w, float *out, int rows, int D,
+                                                       SplitK pk, const float *cin) {
+    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6), d4 = D / 4;
+    if (row >= rows) return;                                     // wave-uniform
+    const long r4 = (long)row * d4;
+    float4 *x4 = reinterpret_cast<float4 *>(in) + r4;
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    float4 xv[NV], wv[NV];
+#pragma unroll
+    for (int v = 0; v < NV; v++) wv[v] = w4[min(lane + 64 * v, d4 - 1)];
+    if (pk.splits > 0) {                                         // uniform
+        const float4 *c4 = reinterpret_cast<const float4 *>(cin);
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+            const int c = min(lane + 64 * v, d4 - 1);
+            xv[v] = sum_splits4(pk, r4 + c);
+            if (cin) xv[v] = add4(c4[r4 + c], xv[v]);
+            if (lane + 64 * v < d4) x4[c] = xv[v];
+        }
+    } else {
+#pragma unroll
+        for (int v = 0; v < NV; v++) xv[v] = x4[min(lane + 64 * v, d4 - 1)];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        const float q = xv[v].x * xv[v].x + xv[v].y * xv[v].y + xv[v].z * xv[v].z + xv[v].w * xv[v].w;
+        ss = lane + 64 * v < d4 ? ss + q : ss;
+    }
+    ss = wave_sum(ss);
+    const float inv = 1.0f / d_sqrtf(ss / D + 1e-5f);
+    float4 *o4 = reinterpret_cast<float4 *>(out) + r4;
+#pragma unroll
+    for (int v = 0; v < NV; v++)
+        if (lane + 64 * v < d4)
+            o4[lane + 64 * v] = make_float4(xv[v].x * inv * wv[v].x, xv[v].y * inv * wv[v].y,
+                                            xv[v].z * inv * wv[v].z, xv[v].w * inv * wv[v].w);
+}
+
+// k_rmsnorm_bwd_rows, one wave per row (pt_backward_ops.c:4-30).
+template <int NV>
+__global__ __launch_bounds__(256) void k_rmsnorm_bwd_rows_w(float *d_out, const float *d_in, float *d_o,
+                                                           const float *x, const float *w, float *inv_out, int rows,
+                                                           int D, SplitK pk) {
+    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6), d4 = D / 4;
+    if (row >= rows) return;                                     // wave-uniform
+    const long r4 = (long)row * d4;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x) + r4, *w4 = reinterpret_cast<const float4 *>(w);
+    float4 *g4 = reinterpret_cast<float4 *>(d_o) + r4;
+    float4 xv[NV], wv[NV], gv[NV], iv[NV];
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        const int c = min(lane + 64 * v, d4 - 1);
+        xv[v] = x4[c];
+        wv[v] = w4[c];
+        iv[v] = d_in ? reinterpret_cast<const float4 *>(d_in)[r4 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (pk.splits > 0) {                                         // uniform
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+            const int c = min(lane + 64 * v, d4 - 1);
+            gv[v] = sum_splits4(pk, r4 + c);
+            if (lane + 64 * v < d4) g4[c] = gv[v];
+        }
+    } else {
+#pragma unroll
+        for (int v = 0; v < NV; v++) gv[v] = g4[min(lane + 64 * v, d4 - 1)];
+    }
+    float ss = 0.0f, dot = 0.0f;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        const bool in = lane + 64 * v < d4;
+        const float q = xv[v].x * xv[v].x + xv[v].y * xv[v].y + xv[v].z * xv[v].z + xv[v].w * xv[v].w;
+        const float d = gv[v].x * wv[v].x * xv[v].x + gv[v].y * wv[v].y * xv[v].y + gv[v].z * wv[v].z * xv[v].z +
+                        gv[v].w * wv[v].w * xv[v].w;
+        ss = in ? ss + q : ss;
+        dot = in ? dot + d : dot;
+    }
+    ss = wave_sum(ss);
+    dot = wave_sum(dot);
+    ss = ss / D + 1e-5f;
+    const float inv = 1.0f / d_sqrtf(ss);
+    const float cd = inv * inv * inv / (float)D * dot;
+    if (lane == 0) inv_out[row] = inv;
+    float4 *o4 = reinterpret_cast<float4 *>(d_out) + r4;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        if (lane + 64 * v < d4) {
+            float4 o;
+            o.x = iv[v].x + (inv * gv[v].x * wv[v].x - cd * xv[v].x);
+            o.y = iv[v].y + (inv * gv[v].y * wv[v].y - cd * xv[v].y);
+            o.z = iv[v].z + (inv * gv[v].z * wv[v].z - cd * xv[v].z);
+            o.w = iv[v].w + (inv * gv[v].w * wv[v].w - cd * xv[v].w);
+            o4[lane + 64 * v] = o;
+        }
+    }
+}
+
 // The d_w half of every RMSNorm of the step in one launch: for norm
 // j = blockIdx.x / cb, d_w[i] = sum_t d_o[t][i]*x[t][i]*inv[t] (written: each
 // norm weight is used once per step); 64 columns per block, 16 interleaved
@@ -573,31 +728,6 @@ __device__ __forceinline__ void row_chunks(const float *row, int kw, float4 (&x)
         x[c] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (256 * c < kw) x[c] = *reinterpret_cast<const float4 *>(row + min(256 * c + 4 * lane, kw - 4));
     }
-}
-
-// Sum / max over the 64 lanes of a wave, returned to every lane: DPP within
-// each row of 16 lanes (quad xor 1, quad xor 2, half-row mirror, row
-// mirror), then the four row results read as scalars.  No LDS round trips.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float lane_f(float v, int l) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
-__device__ __forceinline__ float wave_sum(float v) {
-    v += dpp_f<0xB1>(v);
-    v += dpp_f<0x4E>(v);
-    v += dpp_f<0x141>(v);
-    v += dpp_f<0x140>(v);
-    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
-}
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));
-    v = fmaxf(v, dpp_f<0x4E>(v));
-    v = fmaxf(v, dpp_f<0x141>(v));
-    v = fmaxf(v, dpp_f<0x140>(v));
-    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 // Sums the kMW waves' 16 x 16*HQ tiles in wave order through LDS `red`
@@ -1067,6 +1197,24 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     // The one accumulation is the embedding's: with the classifier tied to
     // it, the classifier's dW (written first) is its starting value;
     // untied, its rows are cleared here.
+    // RMSNorm rows: one wave per row when D % 4 == 0 and D <= 2048, else one
+    // block per row.
+    using NormFn = void (*)(float *, const float *, float *, int, int, SplitK, const float *);
+    using NormBwdFn = void (*)(float *, const float *, float *, const float *, const float *, float *, int, int, SplitK);
+    static const NormFn norm_w[8] = {k_rmsnorm_rows_w<1>, k_rmsnorm_rows_w<2>, k_rmsnorm_rows_w<3>,
+                                     k_rmsnorm_rows_w<4>, k_rmsnorm_rows_w<5>, k_rmsnorm_rows_w<6>,
+                                     k_rmsnorm_rows_w<7>, k_rmsnorm_rows_w<8>};
+    static const NormBwdFn norm_bwd_w[8] = {k_rmsnorm_bwd_rows_w<1>, k_rmsnorm_bwd_rows_w<2>, k_rmsnorm_bwd_rows_w<3>,
+                                            k_rmsnorm_bwd_rows_w<4>, k_rmsnorm_bwd_rows_w<5>, k_rmsnorm_bwd_rows_w<6>,
+                                            k_rmsnorm_bwd_rows_w<7>, k_rmsnorm_bwd_rows_w<8>};
+    const int nv = (D + 255) / 256;
+    const bool wave_norm = D % 4 == 0 && nv <= 8;
+    auto norm_fwd = [&](float *in, const float *w, float *out, SplitK pk, const float *cin) {
+        if (wave_norm)
+            hipLaunchKernelGGL(norm_w[nv - 1], dim3((T + 3) / 4), dim3(256), 0, s, in, w, out, T, D, pk, cin);
+        else
+            hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, in, w, out, D, pk, cin);
+    };
     const bool tied = r->wcls == r->emb;
     if (!tied) fill0(s, G(r->emb), (long)V * D);
     // ── forward ──
@@ -1080,8 +1228,7 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         float *rin = ts->res + l * TD, *rmid = ts->res_att + l * TD, *rout = ts->res + (l + 1) * TD;
         float *xa = ts->xb_att + l * TD, *qkv = ts->qkv + (long)l * T * QS, *att = ts->att + (long)l * NH * T * T;
         float *ao = ts->att_out + l * TD, *xf = ts->xb_ffn + l * TD, *h13 = ts->h13 + (long)l * T * 2 * H;
-        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, rin, r->rms_att + (long)l * D, xa, D, pend,
-                           pend_cin);
+        norm_fwd(rin, r->rms_att + (long)l * D, xa, pend, pend_cin);
         // qkv = x . Wqkv^T with RoPE on the q and k columns in the GEMM's epilogue
         const GemmEpi rope = {GEMM_EPI_ROPE, nullptr, 0, D, hd};
         if ((st = gemm(s, ts, 2, xa, D, r->wqkv + (long)l * QS * D, D, qkv, QS, T, QS, D, 0, nullptr, nullptr, &rope)))
@@ -1094,8 +1241,7 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
                                kv_mul, scale);
         // residual: rmid = rin + att_out . Wo^T
         if ((st = gemm(s, ts, 2, ao, D, r->wo + (long)l * D * D, D, rmid, D, T, D, D, 1, rin))) return st;
-        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, rmid, r->rms_ffn + (long)l * D, xf, D, none,
-                           nullptr);
+        norm_fwd(rmid, r->rms_ffn + (long)l * D, xf, none, nullptr);
         // h13 = x . W13^T (rows interleaved w1/w3), sh = silu(h1)*h3 in the GEMM's epilogue
         const GemmEpi swiglu = {GEMM_EPI_SWIGLU, ts->sh, H, 0, 0};
         if ((st = gemm(s, ts, 2, xf, D, r->w13 + (long)l * 2 * H * D, D, h13, 2 * H, T, 2 * H, D, 0, nullptr, nullptr,
@@ -1104,8 +1250,7 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         if ((st = gemm(s, ts, 2, ts->sh, H, r->w2 + (long)l * D * H, H, rout, D, T, D, H, 1, rmid, &pend))) return st;
         pend_cin = rmid;
     }
-    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, ts->res + L * TD, r->rms_final, ts->x_final, D, pend,
-                       pend_cin);
+    norm_fwd(ts->res + L * TD, r->rms_final, ts->x_final, pend, pend_cin);
     if ((st = gemm(s, ts, 2, ts->x_final, D, r->wcls, D, ts->logits, V, T, V, D, 0))) return st;
     {
         using LossFn = void (*)(float *, const int *, int, int, float, float *);
@@ -1133,8 +1278,12 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     SplitK pk = {};                                       // split-K partials of d_xb[v], if deferred
     auto norm_bwd = [&](const float *x, const float *w) {
         // d_res[v+1] = d_res[v] + rmsnorm_backward(d_xb[v]); inverse norms kept per norm
-        hipLaunchKernelGGL(k_rmsnorm_bwd_rows, dim3(R), dim3(256), 0, s, dres(v + 1), v ? dres(v) : nullptr, dxb(v),
-                           x, w, ts->row_inv + (long)v * T, D, pk);
+        if (wave_norm)
+            hipLaunchKernelGGL(norm_bwd_w[nv - 1], dim3((R + 3) / 4), dim3(256), 0, s, dres(v + 1),
+                               v ? dres(v) : nullptr, dxb(v), x, w, ts->row_inv + (long)v * T, R, D, pk);
+        else
+            hipLaunchKernelGGL(k_rmsnorm_bwd_rows, dim3(R), dim3(256), 0, s, dres(v + 1), v ? dres(v) : nullptr,
+                               dxb(v), x, w, ts->row_inv + (long)v * T, D, pk);
         pk = SplitK{};
         v++;
     };

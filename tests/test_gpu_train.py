@@ -39,11 +39,12 @@ def tensor_slices(cfg):
 # head_dim 16 / 32 / 32 / 80 / 128 take the matrix-core attention kernels
 # (T = 16, 64, 2, 24, 144: whole, ragged and single 16-row tiles); head_dim
 # 24 and 36 (not multiples of 16) the per-position ones.  Vocab 1501 and 301
-# exercise the loss kernel's scalar tail (vocab % 4 != 0).
+# exercise the loss kernel's scalar tail (vocab % 4 != 0); dim 2304 the
+# block-per-row RMSNorm kernels (dim > 2048).
 @pytest.mark.parametrize("cfg,T", [((64, 160, 2, 4, 4, 512, 32), 16), ((96, 256, 1, 3, 3, 1000, 64), 64),
                                    ((64, 128, 2, 2, 2, 300, 8), 2), ((160, 256, 1, 2, 2, 1501, 24), 24),
                                    ((128, 256, 1, 1, 1, 1300, 160), 144), ((48, 128, 1, 2, 2, 400, 40), 40),
-                                   ((72, 128, 1, 2, 2, 301, 20), 19)])
+                                   ((72, 128, 1, 2, 2, 301, 20), 19), ((2304, 64, 1, 36, 36, 64, 8), 4)])
 def test_one_step_matches_oracle(cfg, T):
     blob = pa.synth_model(cfg, 11, 0.05)
     tokens = pa.seed_tokens(5, T, cfg[5])
