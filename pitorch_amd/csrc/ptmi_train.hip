@@ -355,12 +355,15 @@ __global__ __launch_bounds__(kLossThreads) void k_loss_rows_reg(float *lg_dl, co
     }
 }
 
-__global__ __launch_bounds__(256) void k_loss_reduce(const float *row_loss, int T, float *loss) {
-    __shared__ float red[4];
+// loss = mean of the R = T-1 row losses (pt_train.c:323-326), one block of
+// NW waves.
+template <int NW>
+__device__ __forceinline__ void loss_mean_block(const float *row_loss, int R, float *loss) {
+    __shared__ float red[NW];
     float l = 0.0f;
-    for (int t = threadIdx.x; t < T - 1; t += 256) l += row_loss[t];
-    l = block_sum<4>(l, red);
-    if (threadIdx.x == 0) *loss = l / (float)(T - 1);
+    for (int t = threadIdx.x; t < R; t += 64 * NW) l += row_loss[t];
+    l = block_sum<NW>(l, red);
+    if (threadIdx.x == 0) *loss = l / (float)R;
 }
 
 // ── backward kernels ─────────────────────────────────────────────────────
@@ -427,9 +430,11 @@ __device__ __forceinline__ float4 sum_splits4(const SplitK &pk, long i4) {
 __device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
 
 // k_rmsnorm_rows, one wave per row (rmsnorm, pt_ops.c:5-12).
+// With tok != nullptr the row is first gathered from the embedding table,
+// in[row] = emb[tok[row]] (pt_train.c:189-191), and stored.
 template <int NV>
 __global__ __launch_bounds__(256) void k_rmsnorm_rows_w(float *in, const float *w, float *out, int rows, int D,
-                                                       SplitK pk, const float *cin) {
+                                                       SplitK pk, const float *cin, const int *tok, const float *emb) {
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6), d4 = D / 4;
     if (row >= rows) return;                                     // wave-uniform
     const long r4 = (long)row * d4;
@@ -438,7 +443,15 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows_w(float *in, const float *
     float4 xv[NV], wv[NV];
 #pragma unroll
     for (int v = 0; v < NV; v++) wv[v] = w4[min(lane + 64 * v, d4 - 1)];
-    if (pk.splits > 0) {                                         // uniform
+    if (tok) {                                                   // uniform
+        const float4 *e4 = reinterpret_cast<const float4 *>(emb) + (long)tok[row] * d4;
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+            const int c = min(lane + 64 * v, d4 - 1);
+            xv[v] = e4[c];
+            if (lane + 64 * v < d4) x4[c] = xv[v];
+        }
+    } else if (pk.splits > 0) {                                  // uniform
         const float4 *c4 = reinterpret_cast<const float4 *>(cin);
 #pragma unroll
         for (int v = 0; v < NV; v++) {
@@ -534,11 +547,11 @@ struct NormDw {
     float *d_w;
     const float *d_o, *x, *inv;
 };
-__global__ __launch_bounds__(1024) void k_rmsnorm_bwd_dw(const NormDw *nd, int cb, int R, int D) {
+__device__ __forceinline__ void rmsnorm_dw_block(const NormDw *nd, int cb, int R, int D, int b) {
     __shared__ float part[16][64];
-    const NormDw e = nd[blockIdx.x / cb];
+    const NormDw e = nd[b / cb];
     const int c = threadIdx.x & 63, sl = threadIdx.x >> 6;
-    const int i = (blockIdx.x % cb) * 64 + c;
+    const int i = (b % cb) * 64 + c;
     float acc = 0.0f;
     if (i < D) {
 #pragma unroll 4
@@ -629,6 +642,15 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f4v mfma4(float a, float b, f4v c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// rope_backward (pt_backward_ops.c:52-69) of element c of a head's column
+// pair at position t, given its pair partner: o[i] = g0*c + g1*s,
+// o[i+1] = -g0*s + g1*c for the pair (g0, g1) = (col 2k, col 2k+1).
+__device__ __forceinline__ float rope_bwd_elem(float v, float pv, int col, int hd, int t) {
+    float cs, sn;
+    d_rope_cs(col & ~1, hd, t, &cs, &sn);
+    return (col & 1) ? -pv * sn + v * cs : v * cs + pv * sn;
 }
 
 // sc[i][16*kb + j] = mul * (a[r0+i] . b[16*kb+j]) over head_dim for this
@@ -731,7 +753,10 @@ __device__ __forceinline__ void row_chunks(const float *row, int kw, float4 (&x)
 }
 
 // Sums the kMW waves' 16 x 16*HQ tiles in wave order through LDS `red`
-// (kMW*16*16*HQ floats) and hands each element to out(i, c, value).
+// (kMW*16*16*HQ floats) and hands each element to out(i, c, value, pair),
+// pair being element (i, c^1): columns c and c^1 sit in lanes l and l^1
+// (16*HQ and kMT are even), and every pass over e has whole waves active
+// (16*16*HQ is a multiple of 64), so a DPP swap reads it.
 template <int HQ, typename F>
 __device__ __forceinline__ void attn_reduce(const f4v (&acc)[HQ], float *red, F &&out) {
     constexpr int HD = 16 * HQ;
@@ -746,7 +771,7 @@ __device__ __forceinline__ void attn_reduce(const f4v (&acc)[HQ], float *red, F 
         float v = red[e];
 #pragma unroll
         for (int w = 1; w < kMW; w++) v += red[w * 16 * HD + e];
-        out(e / HD, e % HD, v);
+        out(e / HD, e % HD, v, dpp_xor1(v));
     }
 }
 
@@ -829,7 +854,7 @@ __global__ __launch_bounds__(kMT) void k_attn_fwd_mfma(const float *qkv, float *
     __syncthreads();
     f4v acc[HQ];
     ws.run(lds, pitch, v, QS, T, nkb, acc);
-    attn_reduce<HQ>(acc, lds, [&](int i, int c, float o) {
+    attn_reduce<HQ>(acc, lds, [&](int i, int c, float o, float) {
         if (r0 + i < T) att_out[(long)(r0 + i) * D + h * HD + c] = o;
     });
 }
@@ -837,10 +862,11 @@ __global__ __launch_bounds__(kMT) void k_attn_fwd_mfma(const float *qkv, float *
 // Attention backward, row half (pt_train.c:780-811) for rows t < R in
 // [16*blockIdx.x, +16) of head blockIdx.y: d_att = d_aout.V^T into LDS, per
 // row the softmax backward dot and ds = att*(d_att - dot)*scale (kept for
-// the column half), then d_q = ds.K.  LDS as k_attn_fwd_mfma.
+// the column half), then d_q = ds.K, stored after rope_backward into the q
+// columns of the fused [dq | dk | dv] row d_qkv.  LDS as k_attn_fwd_mfma.
 template <int HQ>
 __global__ __launch_bounds__(kMT) void k_attn_bwd_rows_mfma(const float *qkv, const float *att, const float *d_aout,
-                                                           float *ds, float *d_q, int T, int R, int D, int QS,
+                                                           float *ds, float *d_qkv, int T, int R, int D, int QS,
                                                            float scale, int pitch) {
     extern __shared__ float lds[];
     constexpr int HD = 16 * HQ, RW = 16 / kMW;             // rows per wave
@@ -903,20 +929,22 @@ __global__ __launch_bounds__(kMT) void k_attn_bwd_rows_mfma(const float *qkv, co
     __syncthreads();
     f4v acc[HQ];
     ws.run(lds, pitch, k, QS, T, nkb, acc);
-    attn_reduce<HQ>(acc, lds, [&](int i, int c, float o) {
-        if (r0 + i < R) d_q[(long)(r0 + i) * D + h * HD + c] = o;
+    attn_reduce<HQ>(acc, lds, [&](int i, int c, float o, float po) {
+        const int t = r0 + i;
+        if (t < R) d_qkv[(long)t * QS + h * HD + c] = rope_bwd_elem(o, po, h * HD + c, HD, t);
     });
 }
 
 // Attention backward, column half, for keys t2 < R in [16*blockIdx.x, +16)
 // of head blockIdx.y: d_v[t2] = sum_{t2<=t<R} att[t][t2] d_aout[t] and
-// d_k[t2] = sum_{t2<=t<R} ds[t][t2] q[t].  ds holds only t2 <= t, so the
-// weights are selected (never multiplied) by that condition.  Dynamic LDS:
+// d_k[t2] = sum_{t2<=t<R} ds[t][t2] q[t], stored into the v and (after
+// rope_backward) k columns of d_qkv.  ds holds only t2 <= t, so the weights
+// are selected (never multiplied) by that condition.  Dynamic LDS:
 // kMW*16*hd floats.
 template <int HQ>
 __global__ __launch_bounds__(kMT) void k_attn_bwd_cols_mfma(const float *qkv, const float *att, const float *ds,
-                                                           const float *d_aout, float *d_k, float *d_v, int T, int R,
-                                                           int D, int QS) {
+                                                           const float *d_aout, float *d_qkv, int T, int R, int D,
+                                                           int QS) {
     extern __shared__ float lds[];
     constexpr int HD = 16 * HQ, U = HQ <= 3 ? 2 : 1;
     const int k0 = blockIdx.x * 16, h = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -956,11 +984,12 @@ __global__ __launch_bounds__(kMT) void k_attn_bwd_cols_mfma(const float *qkv, co
                 }
             }
     }
-    attn_reduce<HQ>(av, lds, [&](int i, int c, float o) {
-        if (k0 + i < R) d_v[(long)(k0 + i) * D + h * HD + c] = o;
+    attn_reduce<HQ>(av, lds, [&](int i, int c, float o, float) {
+        if (k0 + i < R) d_qkv[(long)(k0 + i) * QS + 2 * D + h * HD + c] = o;
     });
-    attn_reduce<HQ>(ak, lds, [&](int i, int c, float o) {
-        if (k0 + i < R) d_k[(long)(k0 + i) * D + h * HD + c] = o;
+    attn_reduce<HQ>(ak, lds, [&](int i, int c, float o, float po) {
+        const int t = k0 + i;
+        if (t < R) d_qkv[(long)t * QS + D + h * HD + c] = rope_bwd_elem(o, po, h * HD + c, HD, t);
     });
 }
 
@@ -990,22 +1019,21 @@ __global__ void k_rope_bwd_pack(const float *d_q, const float *d_k, const float 
 // every position with that token in ascending t.  One pass over tok marks
 // the block's positions in an LDS bit mask (any earlier one hands the token
 // to an earlier block); each column then walks the mask in ascending order.
-// Dynamic LDS: (R + 31) / 32 words.
-__global__ __launch_bounds__(256) void k_embed_bwd(const int *tok, const float *d_res, float *g_emb, int R, int D) {
-    extern __shared__ unsigned pmask[];
-    const int t = blockIdx.x, nw = (R + 31) / 32;
-    const int tk = tok[t];
-    for (int w = threadIdx.x; w < nw; w += 256) pmask[w] = 0u;
+// pmask: (R + 31) / 32 words of LDS.
+__device__ __forceinline__ void embed_bwd_block(const int *tok, const float *d_res, float *g_emb, int R, int D, int t,
+                                                unsigned *pmask) {
+    const int nw = (R + 31) / 32, tk = tok[t];
+    for (int w = threadIdx.x; w < nw; w += blockDim.x) pmask[w] = 0u;
     __syncthreads();
     int earlier = 0;
-    for (int k = threadIdx.x; k < R; k += 256) {
+    for (int k = threadIdx.x; k < R; k += blockDim.x) {
         if (tok[k] == tk) {
             if (k < t) earlier = 1;
             else atomicOr(&pmask[k >> 5], 1u << (k & 31));
         }
     }
     if (__syncthreads_or(earlier)) return;          // uniform: an earlier block owns this token
-    for (int j = threadIdx.x; j < D; j += 256) {
+    for (int j = threadIdx.x; j < D; j += blockDim.x) {
         float acc = g_emb[(long)tk * D + j];
         for (int w = 0; w < nw; w++) {
             for (unsigned bits = pmask[w]; bits; bits &= bits - 1)
@@ -1013,6 +1041,20 @@ __global__ __launch_bounds__(256) void k_embed_bwd(const int *tok, const float *
         }
         g_emb[(long)tk * D + j] = acc;
     }
+}
+
+// The step's last reductions, one launch of 1024-thread blocks: blocks
+// [0, nn) the RMSNorm dW columns, [nn, nn + R) the embedding backward of
+// position b - nn, and block nn + R the mean loss.  Dynamic LDS: the
+// embedding backward's (R + 31) / 32 mask words.
+__global__ __launch_bounds__(1024) void k_step_tail(const NormDw *nd, int cb, int nn, int R, int D, const int *tok,
+                                                    const float *d_res, float *g_emb, const float *row_loss,
+                                                    float *loss) {
+    extern __shared__ unsigned pmask[];
+    const int b = blockIdx.x;
+    if (b < nn) rmsnorm_dw_block(nd, cb, R, D, b);
+    else if (b < nn + R) embed_bwd_block(tok, d_res, g_emb, R, D, b - nn, pmask);
+    else loss_mean_block<16>(row_loss, R, loss);
 }
 
 // sgd_step (pt_train.c:870-873) over the whole device weight buffer; the
@@ -1175,8 +1217,7 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     using MfFwd = void (*)(const float *, float *, float *, int, int, int, float, int);
     using MfRows = void (*)(const float *, const float *, const float *, float *, float *, int, int, int, int, float,
                             int);
-    using MfCols = void (*)(const float *, const float *, const float *, const float *, float *, float *, int, int, int,
-                            int);
+    using MfCols = void (*)(const float *, const float *, const float *, const float *, float *, int, int, int, int);
     static const MfFwd mf_fwd[8] = {k_attn_fwd_mfma<1>, k_attn_fwd_mfma<2>, k_attn_fwd_mfma<3>, k_attn_fwd_mfma<4>,
                                     k_attn_fwd_mfma<5>, k_attn_fwd_mfma<6>, k_attn_fwd_mfma<7>, k_attn_fwd_mfma<8>};
     static const MfRows mf_rows[8] = {k_attn_bwd_rows_mfma<1>, k_attn_bwd_rows_mfma<2>, k_attn_bwd_rows_mfma<3>,
@@ -1199,7 +1240,8 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     // untied, its rows are cleared here.
     // RMSNorm rows: one wave per row when D % 4 == 0 and D <= 2048, else one
     // block per row.
-    using NormFn = void (*)(float *, const float *, float *, int, int, SplitK, const float *);
+    using NormFn = void (*)(float *, const float *, float *, int, int, SplitK, const float *, const int *,
+                            const float *);
     using NormBwdFn = void (*)(float *, const float *, float *, const float *, const float *, float *, int, int, SplitK);
     static const NormFn norm_w[8] = {k_rmsnorm_rows_w<1>, k_rmsnorm_rows_w<2>, k_rmsnorm_rows_w<3>,
                                      k_rmsnorm_rows_w<4>, k_rmsnorm_rows_w<5>, k_rmsnorm_rows_w<6>,
@@ -1209,16 +1251,19 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
                                             k_rmsnorm_bwd_rows_w<7>, k_rmsnorm_bwd_rows_w<8>};
     const int nv = (D + 255) / 256;
     const bool wave_norm = D % 4 == 0 && nv <= 8;
-    auto norm_fwd = [&](float *in, const float *w, float *out, SplitK pk, const float *cin) {
-        if (wave_norm)
-            hipLaunchKernelGGL(norm_w[nv - 1], dim3((T + 3) / 4), dim3(256), 0, s, in, w, out, T, D, pk, cin);
-        else
+    // embed: gather the rows from the embedding table first (layer 0)
+    auto norm_fwd = [&](float *in, const float *w, float *out, SplitK pk, const float *cin, bool embed) {
+        if (wave_norm) {
+            hipLaunchKernelGGL(norm_w[nv - 1], dim3((T + 3) / 4), dim3(256), 0, s, in, w, out, T, D, pk, cin,
+                               embed ? ts->tok : nullptr, r->emb);
+        } else {
+            if (embed) hipLaunchKernelGGL(k_embed_rows, dim3(T), dim3(256), 0, s, ts->tok, r->emb, in, D);
             hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, in, w, out, D, pk, cin);
+        }
     };
     const bool tied = r->wcls == r->emb;
     if (!tied) fill0(s, G(r->emb), (long)V * D);
     // ── forward ──
-    hipLaunchKernelGGL(k_embed_rows, dim3(T), dim3(256), 0, s, ts->tok, r->emb, ts->res, D);
     // A split-K w2 GEMM leaves its partial sums; the next RMSNorm completes
     // the residual stream row (adding the GEMM's residual input) and stores it.
     SplitK pend = {};
@@ -1228,7 +1273,7 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         float *rin = ts->res + l * TD, *rmid = ts->res_att + l * TD, *rout = ts->res + (l + 1) * TD;
         float *xa = ts->xb_att + l * TD, *qkv = ts->qkv + (long)l * T * QS, *att = ts->att + (long)l * NH * T * T;
         float *ao = ts->att_out + l * TD, *xf = ts->xb_ffn + l * TD, *h13 = ts->h13 + (long)l * T * 2 * H;
-        norm_fwd(rin, r->rms_att + (long)l * D, xa, pend, pend_cin);
+        norm_fwd(rin, r->rms_att + (long)l * D, xa, pend, pend_cin, l == 0);
         // qkv = x . Wqkv^T with RoPE on the q and k columns in the GEMM's epilogue
         const GemmEpi rope = {GEMM_EPI_ROPE, nullptr, 0, D, hd};
         if ((st = gemm(s, ts, 2, xa, D, r->wqkv + (long)l * QS * D, D, qkv, QS, T, QS, D, 0, nullptr, nullptr, &rope)))
@@ -1241,7 +1286,7 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
                                kv_mul, scale);
         // residual: rmid = rin + att_out . Wo^T
         if ((st = gemm(s, ts, 2, ao, D, r->wo + (long)l * D * D, D, rmid, D, T, D, D, 1, rin))) return st;
-        norm_fwd(rmid, r->rms_ffn + (long)l * D, xf, none, nullptr);
+        norm_fwd(rmid, r->rms_ffn + (long)l * D, xf, none, nullptr, false);
         // h13 = x . W13^T (rows interleaved w1/w3), sh = silu(h1)*h3 in the GEMM's epilogue
         const GemmEpi swiglu = {GEMM_EPI_SWIGLU, ts->sh, H, 0, 0};
         if ((st = gemm(s, ts, 2, xf, D, r->w13 + (long)l * 2 * H * D, D, h13, 2 * H, T, 2 * H, D, 0, nullptr, nullptr,
@@ -1250,7 +1295,7 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         if ((st = gemm(s, ts, 2, ts->sh, H, r->w2 + (long)l * D * H, H, rout, D, T, D, H, 1, rmid, &pend))) return st;
         pend_cin = rmid;
     }
-    norm_fwd(ts->res + L * TD, r->rms_final, ts->x_final, pend, pend_cin);
+    norm_fwd(ts->res + L * TD, r->rms_final, ts->x_final, pend, pend_cin, false);
     if ((st = gemm(s, ts, 2, ts->x_final, D, r->wcls, D, ts->logits, V, T, V, D, 0))) return st;
     {
         using LossFn = void (*)(float *, const int *, int, int, float, float *);
@@ -1264,7 +1309,6 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         hipLaunchKernelGGL(loss, dim3(T), dim3(kLossThreads), 0, s, ts->logits, ts->tok, T, V, 1.0f / (float)(T - 1),
                            ts->row_loss);
     }
-    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, s, ts->row_loss, T, ts->loss);
     PTMI_HIP(hipGetLastError());
 
     // ── backward ── (ts->logits now holds d_logits)
@@ -1309,17 +1353,17 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         // attention
         if (mfma_attn) {
             hipLaunchKernelGGL(mf_rows[HQ - 1], dim3((R + 15) / 16, NH), dim3(kMT), mf_lds, s, qkv, att, ts->d_aout,
-                               ts->ds, ts->d_q, T, R, D, QS, scale, pitch);
+                               ts->ds, dqkv, T, R, D, QS, scale, pitch);
             hipLaunchKernelGGL(mf_cols[HQ - 1], dim3((R + 15) / 16, NH), dim3(kMT), mc_lds, s, qkv, att, ts->ds,
-                               ts->d_aout, ts->d_k, ts->d_v, T, R, D, QS);
+                               ts->d_aout, dqkv, T, R, D, QS);
         } else {
             hipLaunchKernelGGL(attn_bwd_rows, dim3(R, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ts->d_aout, ts->ds,
                                ts->d_q, T, D, QS, KV, hd, kv_mul, scale);
             hipLaunchKernelGGL(attn_bwd_cols, dim3(R, NH), dim3(kAttnThreads), 2 * att_lds, s, qkv, att, ts->ds,
                                ts->d_aout, ts->d_k, ts->d_v, T, R, D, QS, KV, hd, kv_mul);
+            hipLaunchKernelGGL(k_rope_bwd_pack, dim3(blocks_for((long)R * D / 2, 256)), dim3(256), 0, s, ts->d_q,
+                               ts->d_k, ts->d_v, dqkv, R, D, KV, QS, hd);
         }
-        hipLaunchKernelGGL(k_rope_bwd_pack, dim3(blocks_for((long)R * D / 2, 256)), dim3(256), 0, s, ts->d_q, ts->d_k,
-                           ts->d_v, dqkv, R, D, KV, QS, hd);
         PTMI_HIP(hipGetLastError());
         // QKV
         if ((st = gemm(s, ts, 0, dqkv, QS, wqkv, D, dxb(v), D, R, D, QS, 0, nullptr, &pk))) return st;
@@ -1328,13 +1372,14 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     PTMI_HIP(hipGetLastError());
     // weight gradients: every TN GEMM in one launch, every RMSNorm dW in one
     if ((st = launch_gemm_tn_group(ts->dw_desc, ts->n_dw, ts->dw_tiles, ts->dw_vec, s))) return st;
+    // every RMSNorm dW, the embedding backward and the mean loss in one
     {
-        const int cb = (D + 63) / 64;
-        hipLaunchKernelGGL(k_rmsnorm_bwd_dw, dim3((unsigned)((2 * L + 1) * cb)), dim3(1024), 0, s,
-                           reinterpret_cast<const NormDw *>(ts->nd_desc), cb, R, D);
+        const int cb = (D + 63) / 64, nn = (2 * L + 1) * cb;
+        hipLaunchKernelGGL(k_step_tail, dim3((unsigned)(nn + R + 1)), dim3(1024), (size_t)(R + 31) / 32 * sizeof(unsigned),
+                           s, reinterpret_cast<const NormDw *>(ts->nd_desc), cb, nn, R, D, ts->tok, dres(v), G(r->emb),
+                           ts->row_loss, ts->loss);
         PTMI_HIP(hipGetLastError());
     }
-    hipLaunchKernelGGL(k_embed_bwd, dim3(R), dim3(256), (size_t)(R + 31) / 32 * sizeof(unsigned), s, ts->tok, dres(v), G(r->emb), R, D);
     // ── SGD ──
     hipLaunchKernelGGL(k_sgd, dim3(blocks_for((long)r->mem_floats, 256)), dim3(256), 0, s, r->mem, ts->gmem, ts->lr,
                        (long)r->mem_floats);
