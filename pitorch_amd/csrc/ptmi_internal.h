@@ -103,14 +103,22 @@ __device__ __forceinline__ void d_rope_cs(int i, int head_dim, int pos, float *c
 }
 
 // ── cross-lane reductions (wave64) ──────────────────────────────────────
-// Butterfly all-reduce over aligned groups of G lanes.  Lane distance 1
-// and 2 use DPP quad permutes, 4..16 use ds_swizzle (bit-mask mode, no LDS
-// allocation), 32 uses ds_bpermute.
+// All-reduce over aligned groups of G lanes, every step a VALU DPP move
+// within a row of 16 lanes: quad xor 1, quad xor 2, the half-row mirror
+// (lane i <-> 7-i: the two quads of an 8-lane group) and the row mirror
+// (i <-> 15-i: the two halves of a row).  Across rows, distance 16 uses
+// ds_swizzle (bit-mask mode, no LDS allocation) and 32 ds_bpermute.
 __device__ __forceinline__ float dpp_xor1(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float dpp_xor2(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float dpp_hmirror(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float dpp_mirror(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true));
 }
 template <int MASK>
 __device__ __forceinline__ float swz_xor(float v) {
@@ -126,8 +134,8 @@ template <int G>
 __device__ __forceinline__ float group_sum(float v) {
     if constexpr (G >= 2) v += dpp_xor1(v);
     if constexpr (G >= 4) v += dpp_xor2(v);
-    if constexpr (G >= 8) v += swz_xor<4>(v);
-    if constexpr (G >= 16) v += swz_xor<8>(v);
+    if constexpr (G >= 8) v += dpp_hmirror(v);
+    if constexpr (G >= 16) v += dpp_mirror(v);
     if constexpr (G >= 32) v += swz_xor<16>(v);
     if constexpr (G >= 64) v += xor32(v);
     return v;
@@ -137,8 +145,8 @@ template <int G>
 __device__ __forceinline__ float group_max(float v) {
     if constexpr (G >= 2) v = fmaxf(v, dpp_xor1(v));
     if constexpr (G >= 4) v = fmaxf(v, dpp_xor2(v));
-    if constexpr (G >= 8) v = fmaxf(v, swz_xor<4>(v));
-    if constexpr (G >= 16) v = fmaxf(v, swz_xor<8>(v));
+    if constexpr (G >= 8) v = fmaxf(v, dpp_hmirror(v));
+    if constexpr (G >= 16) v = fmaxf(v, dpp_mirror(v));
     if constexpr (G >= 32) v = fmaxf(v, swz_xor<16>(v));
     if constexpr (G >= 64) v = fmaxf(v, xor32(v));
     return v;
