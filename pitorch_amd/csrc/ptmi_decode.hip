@@ -18,6 +18,7 @@
 #include <cstring>
 #include <algorithm>
 #include <vector>
+#include <type_traits>
 
 namespace ptmi {
 
@@ -161,13 +162,19 @@ __global__ __launch_bounds__(kAttnWaves * 64) void k_attn_chunk(AttnParams a) {
             accumulate(base, v4, acc);
         }
     }
-#pragma unroll
-    for (int m = G; m < 64; m <<= 1) {
-        acc.x += __shfl_xor(acc.x, m);
-        acc.y += __shfl_xor(acc.y, m);
-        acc.z += __shfl_xor(acc.z, m);
-        acc.w += __shfl_xor(acc.w, m);
-    }
+    // sum over the wave's slots (lanes with equal lane % G): rows of 16
+    // pair i with i+8 by a DPP rotate (G = 8), then the permlane swaps
+    static_assert(G == 8 || G == 16 || G == 32, "lanes per row");
+    auto slot_sum = [](float v) {
+        if constexpr (G == 8)
+            v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));
+        if constexpr (G <= 16) v = xsum16(v);
+        return xsum32(v);
+    };
+    acc.x = slot_sum(acc.x);
+    acc.y = slot_sum(acc.y);
+    acc.z = slot_sum(acc.z);
+    acc.w = slot_sum(acc.w);
     if (slot == 0 && has) {
         red[wave][4 * sub + 0] = acc.x;
         red[wave][4 * sub + 1] = acc.y;
@@ -227,11 +234,34 @@ __global__ __launch_bounds__(1024) void k_argmax_step(const float *logits, int n
         const float v = logits[i];
         if (v > bv) { bv = v; bi = i; }
     }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const float ov = __shfl_xor(bv, m);
-        const int oi = __shfl_xor(bi, m);
+    // wave argmax, ties to the smaller index (a symmetric choice, so any
+    // pairing of lanes forms the same result): DPP within rows of 16, then
+    // the permlane swaps across rows and halves
+    auto take = [&](float ov, int oi) {
         if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    };
+    auto dpp_pair = [&](auto ctrl) {
+        constexpr int C = decltype(ctrl)::value;
+        take(__int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(bv), C, 0xF, 0xF, true)),
+             __builtin_amdgcn_mov_dpp(bi, C, 0xF, 0xF, true));
+    };
+    dpp_pair(std::integral_constant<int, 0xB1>{});
+    dpp_pair(std::integral_constant<int, 0x4E>{});
+    dpp_pair(std::integral_constant<int, 0x141>{});
+    dpp_pair(std::integral_constant<int, 0x140>{});
+    {
+        int ih;
+        const int il = pl16i(bi, ih);
+        const LanePair p = pl16(bv);
+        bv = p.lo; bi = il;
+        take(p.hi, ih);
+    }
+    {
+        int ih;
+        const int il = pl32i(bi, ih);
+        const LanePair p = pl32(bv);
+        bv = p.lo; bi = il;
+        take(p.hi, ih);
     }
     if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
     __syncthreads();

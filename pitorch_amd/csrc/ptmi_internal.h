@@ -103,11 +103,12 @@ __device__ __forceinline__ void d_rope_cs(int i, int head_dim, int pos, float *c
 }
 
 // ── cross-lane reductions (wave64) ──────────────────────────────────────
-// All-reduce over aligned groups of G lanes, every step a VALU DPP move
-// within a row of 16 lanes: quad xor 1, quad xor 2, the half-row mirror
-// (lane i <-> 7-i: the two quads of an 8-lane group) and the row mirror
-// (i <-> 15-i: the two halves of a row).  Across rows, distance 16 uses
-// ds_swizzle (bit-mask mode, no LDS allocation) and 32 ds_bpermute.
+// All-reduce over aligned groups of G lanes, every step a VALU cross-lane
+// move: within a row of 16 lanes DPP quad xor 1, quad xor 2, the half-row
+// mirror (lane i <-> 7-i: the two quads of an 8-lane group) and the row
+// mirror (i <-> 15-i: the two halves of a row); across rows the gfx950
+// permlane swaps, which hand every lane both values of the row pair (16)
+// or wave half pair (32).
 __device__ __forceinline__ float dpp_xor1(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
 }
@@ -120,15 +121,31 @@ __device__ __forceinline__ float dpp_hmirror(float v) {
 __device__ __forceinline__ float dpp_mirror(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true));
 }
-template <int MASK>
-__device__ __forceinline__ float swz_xor(float v) {
-    static_assert(MASK == 4 || MASK == 8 || MASK == 16, "swizzle xor mask");
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (MASK << 10) | 0x1F));
+// Lane l's value and lane l^16's (pl16) or l^32's (pl32), as (lower row or
+// half first, upper second) in every lane: v_permlane16_swap /
+// v_permlane32_swap of v with itself.
+struct LanePair { float lo, hi; };
+__device__ __forceinline__ LanePair pl16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+    return {__int_as_float(r[0]), __int_as_float(r[1])};
 }
-__device__ __forceinline__ float xor32(float v) {
-    int lane = __lane_id();
-    return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __float_as_int(v)));
+__device__ __forceinline__ LanePair pl32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    return {__int_as_float(r[0]), __int_as_float(r[1])};
 }
+__device__ __forceinline__ int pl16i(int v, int &hi) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    hi = r[1];
+    return r[0];
+}
+__device__ __forceinline__ int pl32i(int v, int &hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    hi = r[1];
+    return r[0];
+}
+// v + (lane l^16's v), v + (lane l^32's v)
+__device__ __forceinline__ float xsum16(float v) { const LanePair p = pl16(v); return p.lo + p.hi; }
+__device__ __forceinline__ float xsum32(float v) { const LanePair p = pl32(v); return p.lo + p.hi; }
 
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
@@ -136,8 +153,8 @@ __device__ __forceinline__ float group_sum(float v) {
     if constexpr (G >= 4) v += dpp_xor2(v);
     if constexpr (G >= 8) v += dpp_hmirror(v);
     if constexpr (G >= 16) v += dpp_mirror(v);
-    if constexpr (G >= 32) v += swz_xor<16>(v);
-    if constexpr (G >= 64) v += xor32(v);
+    if constexpr (G >= 32) v = xsum16(v);
+    if constexpr (G >= 64) v = xsum32(v);
     return v;
 }
 
@@ -147,8 +164,8 @@ __device__ __forceinline__ float group_max(float v) {
     if constexpr (G >= 4) v = fmaxf(v, dpp_xor2(v));
     if constexpr (G >= 8) v = fmaxf(v, dpp_hmirror(v));
     if constexpr (G >= 16) v = fmaxf(v, dpp_mirror(v));
-    if constexpr (G >= 32) v = fmaxf(v, swz_xor<16>(v));
-    if constexpr (G >= 64) v = fmaxf(v, xor32(v));
+    if constexpr (G >= 32) { const LanePair p = pl16(v); v = fmaxf(p.lo, p.hi); }
+    if constexpr (G >= 64) { const LanePair p = pl32(v); v = fmaxf(p.lo, p.hi); }
     return v;
 }
 

@@ -10,7 +10,7 @@
 //    wave: x is read once per wave, never re-staged per row.
 //  * Two row passes are issued before either is reduced so each lane keeps
 //    2*IT independent 16-byte loads in flight.
-//  * Row sums are combined with DPP / ds_swizzle butterflies (no LDS tree);
+//  * Row sums are combined with DPP / permlane cross-lane moves (no LDS tree);
 //    LDS holds only the <=64 finished row values a wave hands to its
 //    epilogue.
 // Reduction order differs from the reference's sequential j loop
