@@ -10,11 +10,11 @@
 // so QKV and w1|w3 are one GEMM each in both directions.
 //
 // Non-GEMM ops keep the reference's element-wise arithmetic; their sums
-// (RMSNorm squares, softmax sums, attention dot products, column gradient
-// accumulations) are block reductions, so their addition order differs
-// from the reference's sequential loops, as in the GEMMs.  The embedding
-// gradient keeps the reference's order exactly (one lane per column and
-// token, positions ascending).
+// (RMSNorm squares, softmax sums, column gradient accumulations) are wave
+// or block reductions and the attention products run on the matrix cores,
+// so their addition order differs from the reference's sequential loops, as
+// in the GEMMs.  The embedding gradient keeps the reference's order exactly
+// (per token and column, positions ascending).
 #include "ptmi_model.h"
 
 #include <cmath>
