@@ -4,9 +4,10 @@
 // Per layer, five launches:
 //   1. QKV matvec   : RMSNorm prologue (+ embedding gather on layer 0),
 //                     RoPE epilogue, K/V written straight into the cache
-//   2. attention    : (head, 64-position chunk) workgroups, partial softmax;
-//                     the last chunk of each head to finish combines them
-//   3. Wo matvec    : residual-add epilogue
+//   2. attention    : (head, chunk of positions) workgroups, each leaving
+//                     its chunk's partial softmax sums
+//   3. Wo matvec    : attention-combine prologue (merges the chunks of every
+//                     head), residual-add epilogue
 //   4. w1|w3 matvec : RMSNorm prologue, rows interleaved, SwiGLU epilogue
 //   5. w2 matvec    : residual-add epilogue
 // then the classifier matvec (final RMSNorm prologue) and one argmax
@@ -479,6 +480,8 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
     m->max_T = max_T;
     const size_t D = c.dim, H = c.hidden, V = c.vocab, S = c.seq_len, KV = c.kv_dim, L = c.n_layers;
     // attention chunks: <= 8 per head, 64..kMaxAttnChunk positions each
+    // (seq_len 1024: 128; 64- and 256-position chunks measured slower, the
+    // first by its costlier combine, the second by its longer streams)
     const int per = (c.seq_len + 7) / 8;
     m->attn_chunk = std::min(kMaxAttnChunk, std::max(64, (per + 63) / 64 * 64));
     m->attn_chunks = (c.seq_len + m->attn_chunk - 1) / m->attn_chunk;
