@@ -8,7 +8,7 @@
 // Block tile TMxTN (64x64, or 32x32 for small output grids), K step 32,
 // 256 threads = 4 waves in a 2x2 grid, each wave a (TM/2)x(TN/2) sub-tile
 // of 16x16 MFMA blocks.  Tiles are staged in LDS k-major (As[k][m],
-// Bs[k][n]) so every MFMA operand read is 16 consecutive floats.  Two K
+// Bs[k][n], columns XOR-swizzled so no LDS access has bank conflicts).  Two K
 // tiles are in flight in registers while a third feeds the matrix cores
 // from LDS (double-buffered), so each tile's global latency is covered by
 // two K steps of MFMAs.  Operand layout of the 16x16x4 f32 MFMA (CDNA3/4):
@@ -104,31 +104,56 @@ __device__ __forceinline__ void load_tile(const float *P, long ld, int idx_lim, 
     }
 }
 
-template <bool KMAJOR, int R, int PD>
-__device__ __forceinline__ void store_tile(float (*S)[R + PD], int tid, const float (&r)[R * BK / 256]) {
+// LDS holds each operand tile k-major, S[k][col] with rows of R floats, the
+// column XOR-swizzled by row (and, for 64-wide k-major tiles, by column
+// half) so that, with LDS's 32 banks and a wave64 b32 access served as two
+// half-waves (b128 as four 8-lane groups), every access below is
+// conflict-free:
+//  * the MFMA operand reads (a half-wave reads rows k, k+1 at 16 columns):
+//    bit 4 of the swizzle differs between rows k and k+1;
+//  * the transposing b32 stores of !KMAJOR operands (a half-wave writes one
+//    row per k group at 8 or 4 consecutive columns): the swizzle's bits
+//    3..4 (R = 64) or 2..4 (R = 32) take a different value per k group;
+//  * the b128 stores of KMAJOR operands (8 lanes write one row, 4 floats
+//    each, at a stride of E floats): for R = 64 the upper column half
+//    moves by 4 banks.
+// Bits 0..1 are never swizzled, so float4 chunks stay whole.
+template <bool KMAJOR, int R>
+__device__ __forceinline__ int lds_col(int r, int c) {
+    if constexpr (KMAJOR) {
+        if constexpr (R == 64) return c ^ ((r & 1) << 4) ^ (((c >> 5) & 1) << 2);
+        return c ^ ((r & 1) << 4);
+    } else if constexpr (R == 64) {
+        return c ^ ((((r & 1) ^ ((r >> 3) & 1)) << 4) | (((r >> 4) & 1) << 3));
+    } else {
+        return c ^ ((((r & 1) ^ ((r >> 2) & 1)) << 4) | (((r >> 3) & 1) << 3) | (((r >> 4) & 1) << 2));
+    }
+}
+
+template <bool KMAJOR, int R>
+__device__ __forceinline__ void store_tile(float (*S)[R], int tid, const float (&r)[R * BK / 256]) {
     constexpr int E = R * BK / 256;
     if (KMAJOR) {
         const int k = tid / (R / E), i = E * (tid % (R / E));
 #pragma unroll
-        for (int c = 0; c < E; c++) S[k][i + c] = r[c];
+        for (int c = 0; c < E; c += 4)
+            *reinterpret_cast<float4 *>(&S[k][lds_col<KMAJOR, R>(k, i + c)]) =
+                make_float4(r[c], r[c + 1], r[c + 2], r[c + 3]);
     } else {
         const int i = tid / (BK / E), k = E * (tid % (BK / E));
 #pragma unroll
-        for (int c = 0; c < E; c++) S[k + c][i] = r[c];
+        for (int c = 0; c < E; c++) S[k + c][lds_col<KMAJOR, R>(k + c, i)] = r[c];
     }
 }
 
-// One TMxTN output tile of g at (m0, n0) over K range split z.
-// LDS rows are padded so that a row's start moves by 16 banks from the
-// previous row for 64-wide tiles (the two k rows one half-wave reads
-// for the MFMA operands then fall on disjoint banks).
+// One TMxTN output tile of g at (m0, n0) over K range split z.  The LDS
+// tiles use the swizzled layout of lds_col.
 template <bool AT, bool BT, int TM, int TN, int P, bool VEC, int EPI = GEMM_EPI_NONE>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int z) {
     constexpr int FM = TM / 32, FN = TN / 32;          // 16x16 MFMA blocks per wave
     constexpr int EA = TM * BK / 256, EB = TN * BK / 256;
-    constexpr int PA = TM == 64 ? 16 : 4, PB = TN == 64 ? 16 : 4;
-    __shared__ float As[2][BK][TM + PA];
-    __shared__ float Bs[2][BK][TN + PB];
+    __shared__ float As[2][BK][TM];
+    __shared__ float Bs[2][BK][TN];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int li = lane & 15, lk = lane >> 4;
@@ -150,8 +175,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
         load_tile<!BT, TN, VEC>(g.B, g.ldb, g.N, n0, kb + s * BK, kend, tid, xb);
     };
     auto store = [&](int s, const float (&xa)[EA], const float (&xb)[EB]) {
-        store_tile<AT, TM, PA>(As[s & 1], tid, xa);
-        store_tile<!BT, TN, PB>(Bs[s & 1], tid, xb);
+        store_tile<AT, TM>(As[s & 1], tid, xa);
+        store_tile<!BT, TN>(Bs[s & 1], tid, xb);
     };
     auto compute = [&](int s) {
         const int buf = s & 1;
@@ -159,9 +184,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
         for (int kk = 0; kk < BK; kk += 4) {
             float a[FM], b[FN];
 #pragma unroll
-            for (int i = 0; i < FM; i++) a[i] = As[buf][kk + lk][wm * (TM / 2) + i * 16 + li];
+            for (int i = 0; i < FM; i++) a[i] = As[buf][kk + lk][lds_col<AT, TM>(kk + lk, wm * (TM / 2) + i * 16 + li)];
 #pragma unroll
-            for (int j = 0; j < FN; j++) b[j] = Bs[buf][kk + lk][wn * (TN / 2) + j * 16 + li];
+            for (int j = 0; j < FN; j++) b[j] = Bs[buf][kk + lk][lds_col<!BT, TN>(kk + lk, wn * (TN / 2) + j * 16 + li)];
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
