@@ -178,20 +178,29 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
         store_tile<AT, TM>(As[s & 1], tid, xa);
         store_tile<!BT, TN>(Bs[s & 1], tid, xb);
     };
+    // The operands of k group kk+4 are read from LDS before the MFMAs of
+    // group kk issue, so their latency overlaps those MFMAs.
     auto compute = [&](int s) {
         const int buf = s & 1;
+        float a[2][FM], b[2][FN];
+        auto read = [&](int kk, float (&ar)[FM], float (&br)[FN]) {
+#pragma unroll
+            for (int i = 0; i < FM; i++) ar[i] = As[buf][kk + lk][lds_col<AT, TM>(kk + lk, wm * (TM / 2) + i * 16 + li)];
+#pragma unroll
+            for (int j = 0; j < FN; j++) br[j] = Bs[buf][kk + lk][lds_col<!BT, TN>(kk + lk, wn * (TN / 2) + j * 16 + li)];
+        };
+        read(0, a[0], b[0]);
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 4) {
-            float a[FM], b[FN];
-#pragma unroll
-            for (int i = 0; i < FM; i++) a[i] = As[buf][kk + lk][lds_col<AT, TM>(kk + lk, wm * (TM / 2) + i * 16 + li)];
-#pragma unroll
-            for (int j = 0; j < FN; j++) b[j] = Bs[buf][kk + lk][lds_col<!BT, TN>(kk + lk, wn * (TN / 2) + j * 16 + li)];
+            const int c = (kk / 4) & 1;
+            if (kk + 4 < BK) read(kk + 4, a[c ^ 1], b[c ^ 1]);
+            __builtin_amdgcn_sched_barrier(0);              // keep the reads ahead of the MFMAs
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
                 for (int j = 0; j < FN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c][i], b[c][j], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
