@@ -299,6 +299,28 @@ def pmc_workload(pa, name, positions):
     print(f"[bench] pmc workload: {positions} positions of {name}, then the calibration copy", file=sys.stderr)
 
 
+def pmc_gemm(pa, reps):
+    """Every training GEMM shape of stories15M at T=256, `reps` launches
+    each, enqueued directly (no graph) with one synchronisation per shape:
+    the workload of the GEMM counter passes."""
+    from pitorch_amd._hip import DeviceArray
+
+    L = pa.load_ptmi()
+    shapes = train_gemm_shapes(pa.STORIES["stories15M"], 256)
+    A = DeviceArray.from_host(pa.seed_uniform(1, max(M * K for _, M, N, K, _ in shapes)))
+    B = DeviceArray.from_host(pa.seed_uniform(2, max(K * N for _, M, N, K, _ in shapes)))
+    C = DeviceArray(max(M * N for _, M, N, K, _ in shapes))
+    for op, M, N, K, _ in shapes:
+        lda = K if op != 1 else M
+        ldb = N if op != 2 else K
+        for _ in range(reps):
+            pa._ffi.check(L.ptmi_gemm_dev(op, A.ptr, lda, B.ptr, ldb, C.ptr, N, M, N, K, 0, None))
+        pa._ffi.check(L.ptmi_sync())
+    for a in (A, B, C):
+        a.free()
+    print(f"[bench] pmc gemm workload: {len(shapes)} training GEMM shapes x {reps}", file=sys.stderr)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -313,6 +335,9 @@ def main():
                          "kernel trace on this image: the profiler's host side faults)")
     ap.add_argument("--only-train", action="store_true",
                     help="run only the training leg and print its JSON (for counter profiles), not the bench line")
+    ap.add_argument("--pmc-gemm", type=int, default=0, metavar="REPS",
+                    help="only enqueue every training GEMM shape REPS times without graphs (workload for "
+                         "rocprofv3 --pmc passes), print nothing on stdout")
     ap.add_argument("--pmc-workload", type=int, default=0, metavar="POSITIONS",
                     help="counter-profile workload, no timing: POSITIONS decode steps of the --config model "
                          "enqueued without graphs, 8 at a time (rocprofv3 --pmc faults on its host side with "
@@ -329,6 +354,9 @@ def main():
 
     if args.only_train:
         print(json.dumps(bench_train(pa)), flush=True)
+        return
+    if args.pmc_gemm:
+        pmc_gemm(pa, args.pmc_gemm)
         return
     if args.pmc_workload:
         pmc_workload(pa, args.config, args.pmc_workload)
