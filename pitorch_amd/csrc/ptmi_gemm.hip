@@ -40,6 +40,9 @@ struct GemmArgs {
     float *partial;        // split-K workspace [splits][M][N] or null
     int k_per_split;
     GemmEpi epi;           // fused element-wise epilogue (whole-K launches only)
+    float *upd;            // fused SGD step of the weight C is the gradient of (TnGemm), or null
+    const float *lr;
+    const unsigned *keep;
 };
 
 // One GEMM of a grouped launch: its arguments and its range of tiles.
@@ -234,6 +237,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
         }
     }
 
+    const float lrv = g.upd ? *g.lr : 0.0f;
     // C[4*(l/16)+r][l%16] of each 16x16 block; columns n and n^1 of a row sit
     // in lanes l and l^1, which the fused epilogues pair with a DPP swap
     // (every lane reaches it: bounds are checked after).
@@ -286,7 +290,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
                     g.partial[((long)z * g.M + m) * g.N + n] = v;
                 } else {
                     const long o = (long)m * g.ldc + n;
-                    g.C[o] = g.accumulate ? g.Cin[o] + v : v;
+                    const float cv = g.accumulate ? g.Cin[o] + v : v;
+                    g.C[o] = cv;
+                    // sgd_step (pt_train.c:870-873) on the weight this gradient belongs to
+                    if (g.upd && !(g.keep && ((g.keep[m >> 5] >> (m & 31)) & 1u))) g.upd[o] -= lrv * cv;
                 }
             }
         }
@@ -347,6 +354,7 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
     g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc;
     g.M = M; g.N = N; g.K = K; g.accumulate = accumulate;
     g.Cin = Cin ? Cin : C;
+    g.upd = nullptr; g.lr = nullptr; g.keep = nullptr;
     // float4 loads when both operands have aligned rows and a contiguous
     // extent that is a multiple of 4 (M for A^T, K for A; K for B^T, N for B)
     const bool vec = al16(A) && lda % 4 == 0 && (AT ? M : K) % 4 == 0 && al16(B) && ldb % 4 == 0 &&
@@ -412,7 +420,8 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
 
 size_t gemm_group_desc_bytes(int n) { return sizeof(GemmGroupDesc) * (size_t)n; }
 
-int gemm_tn_group_prepare(const TnGemm *list, int n, void *host_desc, int *tiles_total, int *vec_out) {
+int gemm_tn_group_prepare(const TnGemm *list, int n, const float *lr, void *host_desc, int *tiles_total,
+                          int *vec_out) {
     GemmGroupDesc *d = static_cast<GemmGroupDesc *>(host_desc);
     int t = 0, vec = 1;
     for (int i = 0; i < n; i++) {
@@ -423,6 +432,8 @@ int gemm_tn_group_prepare(const TnGemm *list, int n, void *host_desc, int *tiles
         g = GemmArgs{};
         g.A = e.A; g.lda = e.lda; g.B = e.B; g.ldb = e.ldb; g.C = e.C; g.ldc = e.ldc; g.Cin = e.C;
         g.M = e.M; g.N = e.N; g.K = e.K; g.accumulate = 0; g.partial = nullptr; g.k_per_split = e.K;
+        if (e.upd && !lr) return set_error(PTMI_ERR_ARG, "grouped gemm %d: update without a learning rate", i);
+        g.upd = e.upd; g.lr = lr; g.keep = e.keep;
         if (!(al16(e.A) && e.lda % 4 == 0 && e.M % 4 == 0 && al16(e.B) && e.ldb % 4 == 0 && e.N % 4 == 0)) vec = 0;
         d[i].tiles_n = (e.N + 31) / 32;
         d[i].tile0 = t;

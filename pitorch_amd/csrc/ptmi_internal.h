@@ -343,14 +343,20 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
 // Grouped C[M,N] = A^T.B GEMMs (TN; A stored [K][M]; C written, not
 // accumulated), one launch of 32x32 tiles over all of them.  prepare fills host_desc (gemm_group_desc_bytes(n)
 // bytes); the caller copies it to device memory for the launch.
+// upd != null: the SGD step of the weight whose gradient C is, fused into
+// the epilogue: upd[m][n] -= *lr * C[m][n] (same layout as C), except rows
+// m whose bit is set in keep (their gradient is completed, and the weight
+// updated, by a later kernel).
 struct TnGemm {
     const float *A; long lda;
     const float *B; long ldb;
     float *C; long ldc;
     int M, N, K;
+    float *upd = nullptr;
+    const unsigned *keep = nullptr;
 };
 size_t gemm_group_desc_bytes(int n);
-int gemm_tn_group_prepare(const TnGemm *list, int n, void *host_desc, int *tiles_total, int *vec);
+int gemm_tn_group_prepare(const TnGemm *list, int n, const float *lr, void *host_desc, int *tiles_total, int *vec);
 int launch_gemm_tn_group(const void *dev_desc, int n, int tiles_total, int vec, hipStream_t s);
 
 // ── library state ───────────────────────────────────────────────────────

@@ -42,6 +42,11 @@ struct TrainState {
     float *ws;
     size_t ws_floats = 0;
     float *lr;                  // device copy of the step's learning rate
+    // Bit t of tok_bits: token t is the input at some position < T-1.  Set by
+    // the forward's embedding gather, read by the classifier dW GEMM (which
+    // leaves those embedding rows' SGD step to the embedding backward), and
+    // cleared by the embedding backward, so it is all zero between steps.
+    unsigned *tok_bits;
     // The step for one T, captured once (PTMI_TRAIN_EAGER=1: plain launches).
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -108,8 +113,10 @@ __device__ __forceinline__ float dot4(float4 a, float4 b) { return a.x * b.x + a
 
 // ── forward kernels ──────────────────────────────────────────────────────
 
-__global__ void k_embed_rows(const int *tok, const float *emb, float *out, int D) {   // pt_train.c:189-191
-    const int t = blockIdx.x;
+// (also marks tok[t] in tok_bits for t < R)
+__global__ void k_embed_rows(const int *tok, const float *emb, float *out, int D, unsigned *tok_bits, int R) {
+    const int t = blockIdx.x;                                    // pt_train.c:189-191
+    if (threadIdx.x == 0 && t < R) atomicOr(&tok_bits[tok[t] >> 5], 1u << (tok[t] & 31));
     const float *src = emb + (long)tok[t] * D;
     for (int i = threadIdx.x; i < D; i += blockDim.x) out[(long)t * D + i] = src[i];
 }
@@ -431,10 +438,12 @@ __device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(
 
 // k_rmsnorm_rows, one wave per row (rmsnorm, pt_ops.c:5-12).
 // With tok != nullptr the row is first gathered from the embedding table,
-// in[row] = emb[tok[row]] (pt_train.c:189-191), and stored.
+// in[row] = emb[tok[row]] (pt_train.c:189-191), and stored; rows < rows-1
+// also mark their token in tok_bits.
 template <int NV>
 __global__ __launch_bounds__(256) void k_rmsnorm_rows_w(float *in, const float *w, float *out, int rows, int D,
-                                                       SplitK pk, const float *cin, const int *tok, const float *emb) {
+                                                       SplitK pk, const float *cin, const int *tok, const float *emb,
+                                                       unsigned *tok_bits) {
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6), d4 = D / 4;
     if (row >= rows) return;                                     // wave-uniform
     const long r4 = (long)row * d4;
@@ -444,7 +453,9 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows_w(float *in, const float *
 #pragma unroll
     for (int v = 0; v < NV; v++) wv[v] = w4[min(lane + 64 * v, d4 - 1)];
     if (tok) {                                                   // uniform
-        const float4 *e4 = reinterpret_cast<const float4 *>(emb) + (long)tok[row] * d4;
+        const int tk = tok[row];
+        if (lane == 0 && row < rows - 1) atomicOr(&tok_bits[tk >> 5], 1u << (tk & 31));
+        const float4 *e4 = reinterpret_cast<const float4 *>(emb) + (long)tk * d4;
 #pragma unroll
         for (int v = 0; v < NV; v++) {
             const int c = min(lane + 64 * v, d4 - 1);
@@ -543,11 +554,13 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd_rows_w(float *d_out, const 
 // j = blockIdx.x / cb, d_w[i] = sum_t d_o[t][i]*x[t][i]*inv[t] (written: each
 // norm weight is used once per step); 64 columns per block, 16 interleaved
 // row slices summed in LDS.
+// With the weight's SGD step (pt_train.c:870-873): w[i] -= lr * d_w[i].
 struct NormDw {
     float *d_w;
     const float *d_o, *x, *inv;
+    float *w;
 };
-__device__ __forceinline__ void rmsnorm_dw_block(const NormDw *nd, int cb, int R, int D, int b) {
+__device__ __forceinline__ void rmsnorm_dw_block(const NormDw *nd, int cb, int R, int D, int b, float lr) {
     __shared__ float part[16][64];
     const NormDw e = nd[b / cb];
     const int c = threadIdx.x & 63, sl = threadIdx.x >> 6;
@@ -563,6 +576,7 @@ __device__ __forceinline__ void rmsnorm_dw_block(const NormDw *nd, int cb, int R
         float g = 0.0f;
         for (int k = 0; k < 16; k++) g += part[k][c];
         e.d_w[i] = g;
+        e.w[i] -= lr * g;
     }
 }
 
@@ -1019,9 +1033,10 @@ __global__ void k_rope_bwd_pack(const float *d_q, const float *d_k, const float 
 // every position with that token in ascending t.  One pass over tok marks
 // the block's positions in an LDS bit mask (any earlier one hands the token
 // to an earlier block); each column then walks the mask in ascending order.
-// pmask: (R + 31) / 32 words of LDS.
-__device__ __forceinline__ void embed_bwd_block(const int *tok, const float *d_res, float *g_emb, int R, int D, int t,
-                                                unsigned *pmask) {
+// The owner block then applies the row's SGD step (pt_train.c:870-873) and
+// clears the token's bit in tok_bits.  pmask: (R + 31) / 32 words of LDS.
+__device__ __forceinline__ void embed_bwd_block(const int *tok, const float *d_res, float *g_emb, float *w_emb,
+                                                unsigned *tok_bits, float lr, int R, int D, int t, unsigned *pmask) {
     const int nw = (R + 31) / 32, tk = tok[t];
     for (int w = threadIdx.x; w < nw; w += blockDim.x) pmask[w] = 0u;
     __syncthreads();
@@ -1040,28 +1055,26 @@ __device__ __forceinline__ void embed_bwd_block(const int *tok, const float *d_r
                 acc += d_res[(long)(32 * w + __builtin_ctz(bits)) * D + j];
         }
         g_emb[(long)tk * D + j] = acc;
+        w_emb[(long)tk * D + j] -= lr * acc;
     }
+    if (threadIdx.x == 0) atomicAnd(&tok_bits[tk >> 5], ~(1u << (tk & 31)));
 }
 
-// The step's last reductions, one launch of 1024-thread blocks: blocks
-// [0, nn) the RMSNorm dW columns, [nn, nn + R) the embedding backward of
-// position b - nn, and block nn + R the mean loss.  Dynamic LDS: the
-// embedding backward's (R + 31) / 32 mask words.
+// The step's last reductions and updates, one launch of 1024-thread blocks:
+// blocks [0, nn) the RMSNorm dW columns with their SGD steps, [nn, nn + R)
+// the embedding backward (and SGD step) of position b - nn's token, and
+// block nn + R the mean loss.  Dynamic LDS: the embedding backward's
+// (R + 31) / 32 mask words.
 __global__ __launch_bounds__(1024) void k_step_tail(const NormDw *nd, int cb, int nn, int R, int D, const int *tok,
-                                                    const float *d_res, float *g_emb, const float *row_loss,
+                                                    const float *d_res, float *g_emb, float *w_emb,
+                                                    unsigned *tok_bits, const float *lr, const float *row_loss,
                                                     float *loss) {
     extern __shared__ unsigned pmask[];
     const int b = blockIdx.x;
-    if (b < nn) rmsnorm_dw_block(nd, cb, R, D, b);
-    else if (b < nn + R) embed_bwd_block(tok, d_res, g_emb, R, D, b - nn, pmask);
+    const float lrv = *lr;
+    if (b < nn) rmsnorm_dw_block(nd, cb, R, D, b, lrv);
+    else if (b < nn + R) embed_bwd_block(tok, d_res, g_emb, w_emb, tok_bits, lrv, R, D, b - nn, pmask);
     else loss_mean_block<16>(row_loss, R, loss);
-}
-
-// sgd_step (pt_train.c:870-873) over the whole device weight buffer; the
-// learning rate is read from device memory so a captured step serves any lr.
-__global__ void k_sgd(float *w, const float *g, const float *lr, long n) {
-    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) w[i] -= *lr * g[i];
 }
 
 // Zero fill (pt_zero_grads, pt_train.c:425-427), a kernel rather than a
@@ -1101,12 +1114,13 @@ int train_create(ptmi_model *m) {
         m->res->mem_floats,                                    // grads
         (2 * L + 2) * T * D, (2 * L + 1) * T * D, T * H, L * T * 2 * H, L * T * H, T * D, T * D, T * KV, T * KV,
         L * T * QS, NH * T * T, (2 * L + 1) * T, T, 64, ts->ws_floats, T, 1,
-        (gemm_group_desc_bytes(4 * (int)L + 1) + 3) / 4, (sizeof(NormDw) * (2 * L + 1) + 3) / 4};
+        (gemm_group_desc_bytes(4 * (int)L + 1) + 3) / 4, (sizeof(NormDw) * (2 * L + 1) + 3) / 4, (V + 31) / 32};
     float *dw_desc = nullptr;
     float **dst[] = {&ts->res, &ts->res_att, &ts->xb_att, &ts->qkv, &ts->att, &ts->att_out, &ts->xb_ffn, &ts->h13,
                      &ts->sh, &ts->x_final, &ts->logits, &ts->gmem, &ts->d_res, &ts->d_xb, &ts->d_sh, &ts->d_h13,
                      &ts->shb, &ts->d_aout, &ts->d_q, &ts->d_k, &ts->d_v, &ts->d_qkv, &ts->ds, &ts->row_inv,
-                     &ts->row_loss, &ts->loss, &ts->ws, (float **)&ts->tok, &ts->lr, &dw_desc, &ts->nd_desc};
+                     &ts->row_loss, &ts->loss, &ts->ws, (float **)&ts->tok, &ts->lr, &dw_desc, &ts->nd_desc,
+                     (float **)&ts->tok_bits};
     const int nbuf = (int)(sizeof(sizes) / sizeof(sizes[0]));
     size_t total = 0;
     for (int i = 0; i < nbuf; i++) total += align_up(sizes[i], 64);
@@ -1158,12 +1172,19 @@ int train_descriptors(ptmi_model *m, int T) {
     const int D = c.dim, H = c.hidden, L = c.n_layers, V = c.vocab, KV = c.kv_dim, QS = D + 2 * KV, R = T - 1;
     const long TD = (long)T * D;
     auto G = [&](const float *p) { return ts->gmem + (p - r->mem); };
+    auto W = [&](const float *p) { return r->mem + (p - r->mem); };     // the weight, writable (SGD)
     auto dres = [&](int k) { return ts->d_res + (long)k * TD; };
     auto dxb = [&](int k) { return ts->d_xb + (long)k * TD; };
+    // Every weight's SGD step (pt_sgd_update, pt_train.c:870-896) is fused
+    // into the kernel that writes its gradient: the dW GEMMs' epilogues, the
+    // RMSNorm dW reductions, and, for the embedding rows of this step's
+    // tokens, the embedding backward.  A classifier tied to the embedding
+    // leaves those rows (bits of tok_bits) to the embedding backward.
+    const bool tied = r->wcls == r->emb;
     std::vector<TnGemm> g;
     std::vector<NormDw> nd;
-    g.push_back({ts->logits, V, ts->x_final, D, G(r->wcls), D, V, D, R});
-    nd.push_back({G(r->rms_final), dxb(0), ts->res + L * TD, ts->row_inv});
+    g.push_back({ts->logits, V, ts->x_final, D, G(r->wcls), D, V, D, R, W(r->wcls), tied ? ts->tok_bits : nullptr});
+    nd.push_back({G(r->rms_final), dxb(0), ts->res + L * TD, ts->row_inv, W(r->rms_final)});
     int v = 1;
     for (int l = L - 1; l >= 0; l--) {
         const float *xa = ts->xb_att + l * TD, *xf = ts->xb_ffn + l * TD, *ao = ts->att_out + l * TD;
@@ -1172,18 +1193,18 @@ int train_descriptors(ptmi_model *m, int T) {
         const float *wo = r->wo + (long)l * D * D, *wqkv = r->wqkv + (long)l * QS * D;
         const float *dh13 = ts->d_h13 + (long)l * T * 2 * H, *shb = ts->shb + (long)l * T * H;
         const float *dqkv = ts->d_qkv + (long)l * T * QS;
-        g.push_back({dres(v), D, shb, H, G(w2), H, D, H, R});                  // FFN reads d_res[v]
-        g.push_back({dh13, 2 * H, xf, D, G(w13), D, 2 * H, D, R});
-        nd.push_back({G(r->rms_ffn + (long)l * D), dxb(v), rmid, ts->row_inv + (long)v * T});
+        g.push_back({dres(v), D, shb, H, G(w2), H, D, H, R, W(w2)});            // FFN reads d_res[v]
+        g.push_back({dh13, 2 * H, xf, D, G(w13), D, 2 * H, D, R, W(w13)});
+        nd.push_back({G(r->rms_ffn + (long)l * D), dxb(v), rmid, ts->row_inv + (long)v * T, W(r->rms_ffn + (long)l * D)});
         v++;
-        g.push_back({dres(v), D, ao, D, G(wo), D, D, D, R});                   // Wo reads d_res[v+1]
-        g.push_back({dqkv, QS, xa, D, G(wqkv), D, QS, D, R});
-        nd.push_back({G(r->rms_att + (long)l * D), dxb(v), rin, ts->row_inv + (long)v * T});
+        g.push_back({dres(v), D, ao, D, G(wo), D, D, D, R, W(wo)});             // Wo reads d_res[v+1]
+        g.push_back({dqkv, QS, xa, D, G(wqkv), D, QS, D, R, W(wqkv)});
+        nd.push_back({G(r->rms_att + (long)l * D), dxb(v), rin, ts->row_inv + (long)v * T, W(r->rms_att + (long)l * D)});
         v++;
     }
     std::vector<char> host(gemm_group_desc_bytes((int)g.size()));
     int tiles = 0, vec = 0, st;
-    if ((st = gemm_tn_group_prepare(g.data(), (int)g.size(), host.data(), &tiles, &vec))) return st;
+    if ((st = gemm_tn_group_prepare(g.data(), (int)g.size(), ts->lr, host.data(), &tiles, &vec))) return st;
     PTMI_HIP(hipMemcpy(ts->dw_desc, host.data(), host.size(), hipMemcpyHostToDevice));
     PTMI_HIP(hipMemcpy(ts->nd_desc, nd.data(), nd.size() * sizeof(NormDw), hipMemcpyHostToDevice));
     ts->n_dw = (int)g.size();
@@ -1241,7 +1262,7 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     // RMSNorm rows: one wave per row when D % 4 == 0 and D <= 2048, else one
     // block per row.
     using NormFn = void (*)(float *, const float *, float *, int, int, SplitK, const float *, const int *,
-                            const float *);
+                            const float *, unsigned *);
     using NormBwdFn = void (*)(float *, const float *, float *, const float *, const float *, float *, int, int, SplitK);
     static const NormFn norm_w[8] = {k_rmsnorm_rows_w<1>, k_rmsnorm_rows_w<2>, k_rmsnorm_rows_w<3>,
                                      k_rmsnorm_rows_w<4>, k_rmsnorm_rows_w<5>, k_rmsnorm_rows_w<6>,
@@ -1255,9 +1276,10 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     auto norm_fwd = [&](float *in, const float *w, float *out, SplitK pk, const float *cin, bool embed) {
         if (wave_norm) {
             hipLaunchKernelGGL(norm_w[nv - 1], dim3((T + 3) / 4), dim3(256), 0, s, in, w, out, T, D, pk, cin,
-                               embed ? ts->tok : nullptr, r->emb);
+                               embed ? ts->tok : nullptr, r->emb, ts->tok_bits);
         } else {
-            if (embed) hipLaunchKernelGGL(k_embed_rows, dim3(T), dim3(256), 0, s, ts->tok, r->emb, in, D);
+            if (embed) hipLaunchKernelGGL(k_embed_rows, dim3(T), dim3(256), 0, s, ts->tok, r->emb, in, D, ts->tok_bits,
+                                          T - 1);
             hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, in, w, out, D, pk, cin);
         }
     };
@@ -1377,13 +1399,10 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         const int cb = (D + 63) / 64, nn = (2 * L + 1) * cb;
         hipLaunchKernelGGL(k_step_tail, dim3((unsigned)(nn + R + 1)), dim3(1024), (size_t)(R + 31) / 32 * sizeof(unsigned),
                            s, reinterpret_cast<const NormDw *>(ts->nd_desc), cb, nn, R, D, ts->tok, dres(v), G(r->emb),
-                           ts->row_loss, ts->loss);
+                           r->emb, ts->tok_bits, ts->lr, ts->row_loss, ts->loss);
         PTMI_HIP(hipGetLastError());
     }
-    // ── SGD ──
-    hipLaunchKernelGGL(k_sgd, dim3(blocks_for((long)r->mem_floats, 256)), dim3(256), 0, s, r->mem, ts->gmem, ts->lr,
-                       (long)r->mem_floats);
-    PTMI_HIP(hipGetLastError());
+    // SGD: every update happened in the kernel that wrote its gradient
     return PTMI_OK;
 }
 

@@ -86,6 +86,51 @@ def test_loss_curve_15M_matches_reference():
     m.close()
 
 
+def untie(blob, cfg, seed):
+    """The same model with its own classifier: negative vocab_size in the
+    header and a wcls tensor after freq_cis (llama2.c's unshared layout)."""
+    V, D = cfg[5], cfg[0]
+    h = np.frombuffer(blob[:28].tobytes(), np.int32).copy()
+    h[5] = -V
+    wcls = pa.seed_uniform(seed, V * D, -0.05, 0.05)
+    return np.concatenate([h.view(np.uint8), blob[28:], wcls.view(np.uint8)])
+
+
+@pytest.mark.parametrize("untied", [False, True])
+def test_steps_with_changing_tokens_match_oracle(untied):
+    """Three SGD steps over different token sequences and lengths, with the
+    classifier tied to the embedding and untied: losses and every updated
+    weight tensor agree with the oracle's.  The SGD steps are fused into the
+    gradient producers; with a tied classifier the embedding rows of a
+    step's tokens are updated by the embedding backward and the others by
+    the classifier dW GEMM, so a row handed over in one step and not in the
+    next must be updated by the GEMM again."""
+    cfg = (64, 160, 2, 4, 4, 512, 32)
+    blob = pa.synth_model(cfg, 15, 0.05)
+    if untied:
+        blob = untie(blob, cfg, 16)
+    w0 = np.frombuffer(blob.tobytes(), np.float32, offset=28).copy()
+    om = OracleModel(blob.copy(), max_T=24)
+    m = pa.Model(blob, max_T=24)
+    for step in range(3):
+        tokens = pa.seed_tokens(20 + step, 24 - 5 * step, cfg[5])
+        lo, lg = om.train_step(tokens, 0.05), m.train_step(tokens, 0.05)
+        assert abs(lg - lo) <= 1e-4 * abs(lo), (step, lg, lo)
+    wa = np.frombuffer(m.read_weights().tobytes(), np.float32, offset=28)
+    wb = np.frombuffer(om.blob.tobytes(), np.float32, offset=28)
+    assert wa.size == wb.size == w0.size
+    sl, n = tensor_slices(cfg)
+    if untied:
+        V, D = cfg[5], cfg[0]
+        sl["wcls"] = slice(w0.size - V * D, w0.size)
+    for name, s in sl.items():
+        ua, ub = (wa[s] - w0[s]).astype(np.float64), (wb[s] - w0[s]).astype(np.float64)
+        assert np.linalg.norm(ub) > 0, name
+        assert np.linalg.norm(ua - ub) / np.linalg.norm(ub) < 1e-3, name
+    m.close()
+    om.close()
+
+
 def test_trained_weights_drive_decode():
     """After device SGD, decode uses the updated device weights: logits equal
     the oracle's decode on the oracle's own trained blob."""
