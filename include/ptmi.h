@@ -139,6 +139,28 @@ int  ptmi_model_profile(ptmi_model_t *m, int first_token, int n_steps,
  * backward, SGD on the device copy of the weights.                     */
 int  ptmi_model_train_step(ptmi_model_t *m, const int *tokens, int T, float lr,
                            float *loss);
+/* One device-timed span of a traced training step: the reference's trace
+ * event (pitorch/profiler/trace.h:24-33, pt_trace_event_t) with times from
+ * HIP events on the step's stream.  name/cat are static strings with the
+ * reference's span names (pt.c:339-364, pt_train.c:171-866): train_step,
+ * zero_grads, forward, embedding, layer, qkv, attention, wo, ffn,
+ * classifier, loss, backward, weight_grads, sgd; layer = -1 outside the
+ * layers; depth = nesting depth (train_step is 0).                      */
+typedef struct {
+    const char *name;
+    const char *cat;        /* "train", "fwd", "bwd" */
+    int         layer;
+    int         depth;
+    double      start_us;   /* from the beginning of train_step */
+    double      dur_us;
+} ptmi_span_t;
+/* ptmi_model_train_step run without the graph, with HIP events around the
+ * phases (pt_train_step with ctx->trace enabled, pt.c:339-364).  Spans are
+ * written in the order they end, as trace.c records them; *n_spans gets
+ * the step's span count, and a buffer of fewer than that many spans is an
+ * error (nothing is written to it; the step has run).                  */
+int  ptmi_model_train_step_trace(ptmi_model_t *m, const int *tokens, int T, float lr, float *loss,
+                                 ptmi_span_t *spans, int max_spans, int *n_spans);
 /* Copy the device weights back into a host blob of the same layout
  * (file order, pitorch/model/llama2.c:49-70).                           */
 int  ptmi_model_read_weights(ptmi_model_t *m, void *blob, size_t bytes);

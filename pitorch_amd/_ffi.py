@@ -10,6 +10,12 @@ _c_int_p = ctypes.POINTER(ctypes.c_int)
 _vp = ctypes.c_void_p
 
 
+class Span(ctypes.Structure):
+    """ptmi_span_t (include/ptmi.h)."""
+    _fields_ = [("name", ctypes.c_char_p), ("cat", ctypes.c_char_p), ("layer", ctypes.c_int),
+                ("depth", ctypes.c_int), ("start_us", ctypes.c_double), ("dur_us", ctypes.c_double)]
+
+
 def lib_dir():
     return os.path.join(_HERE, "lib")
 
@@ -69,6 +75,8 @@ def load_ptmi():
     _sig(L, "ptmi_model_decode_async", i, [_vp, i, i])
     _sig(L, "ptmi_model_profile", i, [_vp, i, i, _c_float_p, _c_int_p])
     _sig(L, "ptmi_model_train_step", i, [_vp, _c_int_p, i, f, _c_float_p])
+    _sig(L, "ptmi_model_train_step_trace", i,
+         [_vp, _c_int_p, i, f, _c_float_p, ctypes.POINTER(Span), i, ctypes.POINTER(i)])
     _sig(L, "ptmi_model_read_weights", i, [_vp, _vp, sz])
     _sig(L, "ptmi_model_read_grads", i, [_vp, _c_float_p, sz])
     _ptmi = L
@@ -91,6 +99,16 @@ def load_host():
     _sig(H, "pt_seed_tokens", None, [u64, ctypes.c_int, ctypes.c_int, _c_int_p])
     _sig(H, "pt_seed_uniform", None, [u64, u64, ctypes.c_float, ctypes.c_float, _c_float_p])
     _sig(H, "pt_file_size", u64, [_vp])
+    cp, i, u32, f = ctypes.c_char_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_float
+    _sig(H, "pt_trace_size", ctypes.c_size_t, [])
+    _sig(H, "pt_trace_init", None, [_vp])
+    _sig(H, "pt_trace_begin", None, [_vp, cp, cp, i])
+    _sig(H, "pt_trace_end", None, [_vp])
+    _sig(H, "pt_trace_reset", None, [_vp])
+    _sig(H, "pt_trace_add", None, [_vp, cp, cp, i, i, u32, u32])
+    _sig(H, "pt_time_us", u32, [])
+    _sig(H, "pt_trace_write_json", None, [_vp, cp])
+    _sig(H, "pt_trace_write_meta", None, [cp, cp, cp, i, i, i, cp, i, i, f, f, f, cp])
     _host = H
     return H
 
@@ -222,6 +240,20 @@ class Model:
         check(self.L.ptmi_model_train_step(self.h, tokens.ctypes.data_as(_c_int_p), len(tokens), lr,
                                            ctypes.byref(loss)))
         return loss.value
+
+    def train_step_trace(self, tokens, lr, max_spans=4096):
+        """The same step run without the graph, with its device-timed spans
+        (ptmi_model_train_step_trace): (loss, [dict(name, cat, layer, depth,
+        start_us, dur_us)]) in the order the spans end."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        loss = ctypes.c_float()
+        buf = (Span * max_spans)()
+        n = ctypes.c_int()
+        check(self.L.ptmi_model_train_step_trace(self.h, tokens.ctypes.data_as(_c_int_p), len(tokens), lr,
+                                                 ctypes.byref(loss), buf, max_spans, ctypes.byref(n)))
+        spans = [dict(name=s.name.decode(), cat=s.cat.decode(), layer=s.layer, depth=s.depth,
+                      start_us=s.start_us, dur_us=s.dur_us) for s in buf[:n.value]]
+        return loss.value, spans
 
     def read_weights(self):
         out = np.empty_like(self.blob)

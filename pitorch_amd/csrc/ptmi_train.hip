@@ -1216,7 +1216,40 @@ int train_descriptors(ptmi_model *m, int T) {
 
 // The whole step on stream s; T fixed, tokens and lr read from device
 // memory (ts->tok, ts->lr), so it can be captured once per T.
-int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
+// Device-timed spans of one training step, for the reference's trace
+// (pitorch/profiler/trace.c): begin/end record HIP events on the step's
+// stream around the launches of a phase, nested like pt_train.c's
+// pt_trace_begin/pt_trace_end calls.  Only used for eager (uncaptured)
+// steps; spans are kept in the order they end, as trace.c records them.
+struct TrainTracer {
+    struct Rec { const char *name, *cat; int layer, depth; hipEvent_t b, e; };
+    std::vector<Rec> open, done;
+    hipStream_t s;
+    int begin(const char *name, const char *cat, int layer) {
+        Rec r = {name, cat, layer, (int)open.size(), nullptr, nullptr};
+        PTMI_HIP(hipEventCreate(&r.b));
+        PTMI_HIP(hipEventCreate(&r.e));
+        PTMI_HIP(hipEventRecord(r.b, s));
+        open.push_back(r);
+        return PTMI_OK;
+    }
+    int end() {
+        if (open.empty()) return set_error(PTMI_ERR_STATE, "trace span end without begin");
+        Rec r = open.back();
+        open.pop_back();
+        PTMI_HIP(hipEventRecord(r.e, s));
+        done.push_back(r);
+        return PTMI_OK;
+    }
+    void release() {
+        for (Rec &r : open) { (void)hipEventDestroy(r.b); (void)hipEventDestroy(r.e); }
+        for (Rec &r : done) { (void)hipEventDestroy(r.b); (void)hipEventDestroy(r.e); }
+        open.clear();
+        done.clear();
+    }
+};
+
+int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr) {
     TrainState *ts = m->train;
     const Resident *r = m->res;
     const Config &c = m->c;
@@ -1226,6 +1259,11 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     const long TD = (long)T * D;
     auto G = [&](const float *p) { return ts->gmem + (p - r->mem); };   // grad of a weight tensor
     int st;
+    // span markers for the traced step (no-ops otherwise)
+#define SPAN(name_, cat_, layer_) \
+    do { if (tr && (st = tr->begin(name_, cat_, layer_))) return st; } while (0)
+#define SPAN_END() \
+    do { if (tr && (st = tr->end())) return st; } while (0)
     const size_t att_lds = (size_t)T * sizeof(float);
     // G lanes per head row: the smallest of 8/16/32 with 4*G >= head_dim
     const int hd4 = hd / 4;
@@ -1284,8 +1322,16 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         }
     };
     const bool tied = r->wcls == r->emb;
+    SPAN("train_step", "train", -1);                      // pt.c:339-364
+    SPAN("zero_grads", "train", -1);
     if (!tied) fill0(s, G(r->emb), (long)V * D);
+    SPAN_END();
     // ── forward ──
+    // Spans follow pt_train.c's (pt_forward_train :171-329): the embedding
+    // gather runs inside layer 0's first RMSNorm, so "embedding" is empty.
+    SPAN("forward", "fwd", -1);
+    SPAN("embedding", "fwd", -1);
+    SPAN_END();
     // A split-K w2 GEMM leaves its partial sums; the next RMSNorm completes
     // the residual stream row (adding the GEMM's residual input) and stores it.
     SplitK pend = {};
@@ -1295,19 +1341,27 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         float *rin = ts->res + l * TD, *rmid = ts->res_att + l * TD, *rout = ts->res + (l + 1) * TD;
         float *xa = ts->xb_att + l * TD, *qkv = ts->qkv + (long)l * T * QS, *att = ts->att + (long)l * NH * T * T;
         float *ao = ts->att_out + l * TD, *xf = ts->xb_ffn + l * TD, *h13 = ts->h13 + (long)l * T * 2 * H;
+        SPAN("layer", "fwd", l);
+        SPAN("qkv", "fwd", l);
         norm_fwd(rin, r->rms_att + (long)l * D, xa, pend, pend_cin, l == 0);
         // qkv = x . Wqkv^T with RoPE on the q and k columns in the GEMM's epilogue
         const GemmEpi rope = {GEMM_EPI_ROPE, nullptr, 0, D, hd};
         if ((st = gemm(s, ts, 2, xa, D, r->wqkv + (long)l * QS * D, D, qkv, QS, T, QS, D, 0, nullptr, nullptr, &rope)))
             return st;
+        SPAN_END();
+        SPAN("attention", "fwd", l);
         if (mfma_attn)
             hipLaunchKernelGGL(mf_fwd[HQ - 1], dim3((T + 15) / 16, NH), dim3(kMT), mf_lds, s, qkv, att, ao, T, D, QS,
                                scale, pitch);
         else
             hipLaunchKernelGGL(attn_fwd, dim3(T, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ao, T, D, QS, KV, hd,
                                kv_mul, scale);
+        SPAN_END();
         // residual: rmid = rin + att_out . Wo^T
+        SPAN("wo", "fwd", l);
         if ((st = gemm(s, ts, 2, ao, D, r->wo + (long)l * D * D, D, rmid, D, T, D, D, 1, rin))) return st;
+        SPAN_END();
+        SPAN("ffn", "fwd", l);
         norm_fwd(rmid, r->rms_ffn + (long)l * D, xf, none, nullptr, false);
         // h13 = x . W13^T (rows interleaved w1/w3), sh = silu(h1)*h3 in the GEMM's epilogue
         const GemmEpi swiglu = {GEMM_EPI_SWIGLU, ts->sh, H, 0, 0};
@@ -1316,9 +1370,14 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
             return st;
         if ((st = gemm(s, ts, 2, ts->sh, H, r->w2 + (long)l * D * H, H, rout, D, T, D, H, 1, rmid, &pend))) return st;
         pend_cin = rmid;
+        SPAN_END();
+        SPAN_END();
     }
+    SPAN("classifier", "fwd", -1);
     norm_fwd(ts->res + L * TD, r->rms_final, ts->x_final, pend, pend_cin, false);
     if ((st = gemm(s, ts, 2, ts->x_final, D, r->wcls, D, ts->logits, V, T, V, D, 0))) return st;
+    SPAN_END();
+    SPAN("loss", "fwd", -1);
     {
         using LossFn = void (*)(float *, const int *, int, int, float, float *);
         const int slots = (V / 4 + kLossThreads - 1) / kLossThreads;
@@ -1333,6 +1392,8 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
     }
     PTMI_HIP(hipGetLastError());
 
+    SPAN_END();
+    SPAN_END();
     // ── backward ── (ts->logits now holds d_logits)
     // The dX chain runs here; the weight gradients (25 TN GEMMs and 2L+1
     // RMSNorm dW reductions) only read buffers written once per step, so
@@ -1353,8 +1414,11 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         pk = SplitK{};
         v++;
     };
+    SPAN("backward", "bwd", -1);                          // pt_backward, pt_train.c:549-866
+    SPAN("classifier", "bwd", -1);
     if ((st = gemm(s, ts, 0, ts->logits, V, r->wcls, D, dxb(0), D, R, D, V, 0, nullptr, &pk))) return st;
     norm_bwd(ts->res + L * TD, r->rms_final);
+    SPAN_END();
     for (int l = L - 1; l >= 0; l--) {
         const float *rin = ts->res + l * TD, *rmid = ts->res_att + l * TD;
         const float *qkv = ts->qkv + (long)l * T * QS, *att = ts->att + (long)l * NH * T * T;
@@ -1366,13 +1430,19 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
         // FFN
         // d_sh = d_res . W2, consumed in the GEMM's epilogue by the swiglu
         // backward: d_h13 (interleaved d_h1, d_h3) and shb = silu(h1)*h3
+        SPAN("layer", "bwd", l);
+        SPAN("ffn", "bwd", l);
         GemmEpi sgb = {GEMM_EPI_SWIGLU_BWD, dh13, 2 * H, 0, 0, shb, H, h13, 2 * H};
         if ((st = gemm(s, ts, 0, dres(v), D, w2, H, ts->d_sh, H, R, H, D, 0, nullptr, nullptr, &sgb))) return st;
         if ((st = gemm(s, ts, 0, dh13, 2 * H, w13, D, dxb(v), D, R, D, 2 * H, 0, nullptr, &pk))) return st;
         norm_bwd(rmid, r->rms_ffn + (long)l * D);
+        SPAN_END();
         // Wo
+        SPAN("wo", "bwd", l);
         if ((st = gemm(s, ts, 0, dres(v), D, wo, D, ts->d_aout, D, R, D, D, 0))) return st;
+        SPAN_END();
         // attention
+        SPAN("attention", "bwd", l);
         if (mfma_attn) {
             hipLaunchKernelGGL(mf_rows[HQ - 1], dim3((R + 15) / 16, NH), dim3(kMT), mf_lds, s, qkv, att, ts->d_aout,
                                ts->ds, dqkv, T, R, D, QS, scale, pitch);
@@ -1387,13 +1457,20 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
                                ts->d_k, ts->d_v, dqkv, R, D, KV, QS, hd);
         }
         PTMI_HIP(hipGetLastError());
+        SPAN_END();
         // QKV
+        SPAN("qkv", "bwd", l);
         if ((st = gemm(s, ts, 0, dqkv, QS, wqkv, D, dxb(v), D, R, D, QS, 0, nullptr, &pk))) return st;
         norm_bwd(rin, r->rms_att + (long)l * D);
+        SPAN_END();
+        SPAN_END();
     }
     PTMI_HIP(hipGetLastError());
     // weight gradients: every TN GEMM in one launch, every RMSNorm dW in one
+    SPAN("weight_grads", "bwd", -1);
     if ((st = launch_gemm_tn_group(ts->dw_desc, ts->n_dw, ts->dw_tiles, ts->dw_vec, s))) return st;
+    SPAN_END();
+    SPAN("embedding", "bwd", -1);
     // every RMSNorm dW, the embedding backward and the mean loss in one
     {
         const int cb = (D + 63) / 64, nn = (2 * L + 1) * cb;
@@ -1402,8 +1479,16 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s) {
                            r->emb, ts->tok_bits, ts->lr, ts->row_loss, ts->loss);
         PTMI_HIP(hipGetLastError());
     }
-    // SGD: every update happened in the kernel that wrote its gradient
+    SPAN_END();
+    SPAN_END();                                           // backward
+    // SGD (pt_sgd_update, pt_train.c:870-896): every update happened in the
+    // kernel that wrote its gradient, so its span is empty.
+    SPAN("sgd", "train", -1);
+    SPAN_END();
+    SPAN_END();                                           // train_step
     return PTMI_OK;
+#undef SPAN
+#undef SPAN_END
 }
 
 }  // namespace
@@ -1414,7 +1499,9 @@ using namespace ptmi;
 
 extern "C" {
 
-int ptmi_model_train_step(ptmi_model_t *m, const int *tokens, int T, float lr, float *loss) {
+// Checks a train step's arguments, uploads its tokens and learning rate and
+// builds the descriptor tables for T.
+static int train_prepare(ptmi_model_t *m, const int *tokens, int T, float lr) {
     if (!m || !tokens) return set_error(PTMI_ERR_ARG, "NULL argument");
     if (!m->train) return set_error(PTMI_ERR_STATE, "model created with max_T = 0 (no training buffers)");
     if (T < 2 || T > m->train->T_max) return set_error(PTMI_ERR_ARG, "T=%d outside [2, max_T=%d]", T, m->train->T_max);
@@ -1424,8 +1511,14 @@ int ptmi_model_train_step(ptmi_model_t *m, const int *tokens, int T, float lr, f
     TrainState *ts = m->train;
     PTMI_HIP(hipMemcpyAsync(ts->tok, tokens, (size_t)T * sizeof(int), hipMemcpyHostToDevice, s));
     PTMI_HIP(hipMemcpyAsync(ts->lr, &lr, sizeof(float), hipMemcpyHostToDevice, s));
-    int st = train_descriptors(m, T);
+    return train_descriptors(m, T);
+}
+
+int ptmi_model_train_step(ptmi_model_t *m, const int *tokens, int T, float lr, float *loss) {
+    int st = train_prepare(m, tokens, T, lr);
     if (st) return st;
+    hipStream_t s = lib_stream();
+    TrainState *ts = m->train;
     if (ts->eager) {
         if ((st = enqueue_train(m, T, s))) return st;
     } else {
@@ -1455,6 +1548,48 @@ int ptmi_model_train_step(ptmi_model_t *m, const int *tokens, int T, float lr, f
     PTMI_HIP(hipStreamSynchronize(s));
     if (loss) *loss = l;
     return PTMI_OK;
+}
+
+int ptmi_model_train_step_trace(ptmi_model_t *m, const int *tokens, int T, float lr, float *loss,
+                                ptmi_span_t *spans, int max_spans, int *n_spans) {
+    if (!n_spans || (max_spans > 0 && !spans) || max_spans < 0) return set_error(PTMI_ERR_ARG, "bad span buffer");
+    *n_spans = 0;
+    int st = train_prepare(m, tokens, T, lr);
+    if (st) return st;
+    hipStream_t s = lib_stream();
+    TrainTracer tr;
+    tr.s = s;
+    st = enqueue_train(m, T, s, &tr);
+    float l = 0.0f;
+    if (!st) {
+        const hipError_t e = hipMemcpyAsync(&l, m->train->loss, sizeof(float), hipMemcpyDeviceToHost, s);
+        if (e != hipSuccess) st = hip_check(e, "loss copy");
+    }
+    const hipError_t es = hipStreamSynchronize(s);
+    if (!st && es != hipSuccess) st = hip_check(es, "hipStreamSynchronize(traced train step)");
+    if (!st && !tr.open.empty()) st = set_error(PTMI_ERR_STATE, "unclosed trace span %s", tr.open.back().name);
+    const TrainTracer::Rec *root = nullptr;
+    for (const auto &r : tr.done)
+        if (r.depth == 0) root = &r;
+    if (!st && !root) st = set_error(PTMI_ERR_STATE, "traced step has no root span");
+    if (!st) {
+        *n_spans = (int)tr.done.size();
+        if (max_spans < *n_spans) {
+            st = set_error(PTMI_ERR_ARG, "span buffer holds %d, the step has %d spans", max_spans, *n_spans);
+        } else {
+            for (size_t i = 0; i < tr.done.size() && !st; i++) {
+                const auto &r = tr.done[i];
+                float a = 0.0f, d = 0.0f;
+                hipError_t e = hipEventElapsedTime(&a, root->b, r.b);
+                if (e == hipSuccess) e = hipEventElapsedTime(&d, r.b, r.e);
+                if (e != hipSuccess) { st = hip_check(e, "hipEventElapsedTime(trace span)"); break; }
+                spans[i] = ptmi_span_t{r.name, r.cat, r.layer, r.depth, 1e3 * a, 1e3 * d};
+            }
+        }
+    }
+    tr.release();
+    if (!st && loss) *loss = l;
+    return st;
 }
 
 // Gradient buffer in pt_grads_t order (pt_train.c:342-370): converted from

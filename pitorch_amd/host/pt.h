@@ -39,6 +39,51 @@ typedef struct {
 typedef void (*pt_matvec_fn)(const float *W, const float *x, float *y,
                              int out_dim, int in_dim);
 
+/* ── trace (pitorch/profiler/trace.h:21-101): spans as Chrome-Tracing
+ * JSON.  All functions are no-ops when t is NULL or t->enabled is 0.   */
+#define PT_TRACE_MAX_EVENTS 4096
+#define PT_TRACE_MAX_DEPTH  32
+
+typedef struct {
+    const char *name;
+    const char *cat;       /* "fwd", "bwd", "train" */
+    uint32_t    ts_us;     /* start (microseconds) */
+    uint32_t    dur_us;    /* duration (microseconds) */
+    int8_t      layer;     /* transformer layer, -1 = none */
+    int8_t      depth;     /* nesting depth */
+    uint32_t    hw_cycles; /* reference: V3D QPU cycles; 0 here */
+    uint32_t    hw_stall;  /* reference: V3D TMU stall cycles; 0 here */
+} pt_trace_event_t;
+
+typedef struct {
+    pt_trace_event_t events[PT_TRACE_MAX_EVENTS];
+    int              count;
+    int              enabled;
+    struct {
+        const char *name;
+        const char *cat;
+        uint32_t    ts_us;
+        int8_t      layer;
+    } stack[PT_TRACE_MAX_DEPTH];
+    int              depth;
+} pt_trace_t;
+
+void     pt_trace_init(pt_trace_t *t);
+void     pt_trace_begin(pt_trace_t *t, const char *name, const char *cat, int layer);
+void     pt_trace_end(pt_trace_t *t);
+void     pt_trace_reset(pt_trace_t *t);
+uint32_t pt_time_us(void);
+void     pt_trace_write_json(const pt_trace_t *t, const char *path);
+void     pt_trace_write_meta(const char *path, const char *name, const char *model, int dim, int layers,
+                             int vocab, const char *device, int num_qpus, int steps, float lr,
+                             float final_loss, float total_time_s, const char *notes);
+/* No reference counterpart: record an already finished span (the device
+ * step's spans are added this way), and sizeof(pt_trace_t) for callers
+ * that allocate it from another language.                              */
+void     pt_trace_add(pt_trace_t *t, const char *name, const char *cat, int layer, int depth,
+                      uint32_t ts_us, uint32_t dur_us);
+size_t   pt_trace_size(void);
+
 /* pitorch/pt.h:23-44, with the device model in place of host buffers. */
 typedef struct {
     pt_config_t   cfg;
@@ -50,6 +95,8 @@ typedef struct {
     size_t        weight_bytes;
     ptmi_model_t *dev;
     float        *logits;        /* host copy, filled on demand */
+    pt_trace_t   *trace;         /* pt_enable_trace; NULL = off */
+    int           trace_owned;   /* allocated by pt_enable_trace */
 } pt_context_t;
 
 /* ── model file (pitorch/model/llama2.c:9-47) ── */
@@ -75,6 +122,14 @@ void pt_print_config(const pt_context_t *ctx);
  * of positions run (stops after a sampled BOS/EOS, pt_text.c:354).     */
 int  pt_generate_ids(pt_context_t *ctx, const int *prompt, int n_prompt,
                      int max_tokens, int *out);
+
+/* ── profiling (pt.c:322-335): with a trace enabled, pt_train_step runs
+ * the device step without its graph and records the reference's spans
+ * (train_step, zero_grads, forward, layer, qkv, attention, wo, ffn,
+ * classifier, loss, backward, weight_grads, embedding, sgd) with HIP-event
+ * times.  preallocated = NULL: the context allocates (and pt_free frees) it. */
+void pt_enable_trace(pt_context_t *ctx, pt_trace_t *preallocated);
+void pt_disable_trace(pt_context_t *ctx);
 
 /* ── training (pt.c:339-364) ── */
 float pt_train_step(pt_context_t *ctx, const int *tokens, int T, float lr);

@@ -10,8 +10,11 @@
  *   pt_demo generate D H L NH NKV V S MODEL_SEED PROMPT_SEED N_PROMPT MAX_TOKENS
  *       prints "prompt: ..." and the chosen ids twice: from pt_generate_ids
  *       and from a pt_forward_step loop with prompt forcing
- *   pt_demo train D H L NH NKV V S MODEL_SEED TRAIN_SEED T LR STEPS
- *       prints "loss <step> <value>" per pt_train_step
+ *   pt_demo train D H L NH NKV V S MODEL_SEED TRAIN_SEED T LR STEPS [TRACE_DIR]
+ *       prints "loss <step> <value>" per pt_train_step; with TRACE_DIR the
+ *       steps run traced (pt_enable_trace, as the reference's
+ *       dev/host/test_train_profiled.c:44-104) and TRACE_DIR/trace.json and
+ *       TRACE_DIR/meta.json are written
  *
  * Exit status 0 on success; failures abort with a message, as the
  * reference's panic() does.
@@ -25,7 +28,7 @@
 static void usage(void) {
     fprintf(stderr,
             "usage: pt_demo generate D H L NH NKV V S MODEL_SEED PROMPT_SEED N_PROMPT MAX_TOKENS\n"
-            "       pt_demo train    D H L NH NKV V S MODEL_SEED TRAIN_SEED T LR STEPS\n");
+            "       pt_demo train    D H L NH NKV V S MODEL_SEED TRAIN_SEED T LR STEPS [TRACE_DIR]\n");
     exit(2);
 }
 
@@ -81,14 +84,30 @@ static int generate(const pt_config_t *cfg, unsigned long long mseed, unsigned l
 }
 
 static int train(const pt_config_t *cfg, unsigned long long mseed, unsigned long long tseed, int T, float lr,
-                 int steps) {
+                 int steps, const char *trace_dir) {
     size_t bytes;
     void *blob = synth(cfg, mseed, &bytes);
     pt_context_t ctx;
     pt_gpu_init(&ctx, blob, bytes, T);
+    if (trace_dir) pt_enable_trace(&ctx, NULL);
     int *tokens = malloc(sizeof(int) * (size_t)T);
     pt_seed_tokens(tseed, T, cfg->vocab_size, tokens);
-    for (int s = 0; s < steps; s++) printf("loss %d %.6f\n", s, pt_train_step(&ctx, tokens, T, lr));
+    const uint32_t t0 = pt_time_us();
+    float loss = 0.0f;
+    for (int s = 0; s < steps; s++) {
+        loss = pt_train_step(&ctx, tokens, T, lr);
+        printf("loss %d %.6f\n", s, loss);
+    }
+    if (trace_dir) {
+        char path[1024];
+        snprintf(path, sizeof path, "%s/trace.json", trace_dir);
+        pt_trace_write_json(ctx.trace, path);
+        printf("trace %s %d events\n", path, ctx.trace->count);
+        snprintf(path, sizeof path, "%s/meta.json", trace_dir);
+        pt_trace_write_meta(path, "synthetic training, traced", "synthetic", cfg->dim, cfg->n_layers,
+                            cfg->vocab_size, "mi355x", 0, steps, lr, loss, (float)(pt_time_us() - t0) * 1e-6f,
+                            "device spans timed with HIP events");
+    }
     if (pt_sync_weights(&ctx) != 0) {
         fprintf(stderr, "pt_demo: pt_sync_weights: %s\n", ptmi_last_error());
         return 1;
@@ -102,11 +121,11 @@ static int train(const pt_config_t *cfg, unsigned long long mseed, unsigned long
 int main(int argc, char **argv) {
     if (argc < 2) usage();
     const int gen = !strcmp(argv[1], "generate"), trn = !strcmp(argv[1], "train");
-    if (!(gen && argc == 13) && !(trn && argc == 14)) usage();
+    if (!(gen && argc == 13) && !(trn && (argc == 14 || argc == 15))) usage();
     pt_config_t cfg;
     int *f = &cfg.dim;
     for (int i = 0; i < 7; i++) f[i] = atoi(argv[2 + i]);
     const unsigned long long mseed = strtoull(argv[9], NULL, 10), seed2 = strtoull(argv[10], NULL, 10);
     if (gen) return generate(&cfg, mseed, seed2, atoi(argv[11]), atoi(argv[12]));
-    return train(&cfg, mseed, seed2, atoi(argv[11]), (float)atof(argv[12]), atoi(argv[13]));
+    return train(&cfg, mseed, seed2, atoi(argv[11]), (float)atof(argv[12]), atoi(argv[13]), argc == 15 ? argv[14] : NULL);
 }

@@ -43,6 +43,9 @@ void pt_free(pt_context_t *ctx) {
     if (ctx->weight_data) ptmi_unregister_weights(ctx->weight_data);
     free(ctx->logits);
     ctx->logits = NULL;
+    if (ctx->trace_owned) free(ctx->trace);
+    ctx->trace = NULL;
+    ctx->trace_owned = 0;
 }
 
 /* pt.c:267-271: forward `token` at ctx->pos, pos++, greedy next token. */
@@ -89,9 +92,40 @@ int pt_generate_ids(pt_context_t *ctx, const int *prompt, int n_prompt, int max_
     return n;
 }
 
-/* pt.c:339-364 */
+/* pt.c:322-335 */
+void pt_enable_trace(pt_context_t *ctx, pt_trace_t *preallocated) {
+    if (preallocated) {
+        if (ctx->trace_owned) free(ctx->trace);
+        ctx->trace = preallocated;
+        ctx->trace_owned = 0;
+    } else if (!ctx->trace) {
+        ctx->trace = (pt_trace_t *)malloc(sizeof(pt_trace_t));
+        ctx->trace_owned = ctx->trace != NULL;
+    }
+    if (ctx->trace) pt_trace_init(ctx->trace);
+}
+
+void pt_disable_trace(pt_context_t *ctx) {
+    if (ctx->trace) ctx->trace->enabled = 0;
+}
+
+/* pt.c:339-364.  Traced: the device step's spans, placed on the host clock
+ * at the call, in the order the device step ends them. */
 int pt_try_train_step(pt_context_t *ctx, const int *tokens, int T, float lr, float *loss) {
-    return ptmi_model_train_step(ctx->dev, tokens, T, lr, loss);
+    pt_trace_t *tr = ctx->trace;
+    if (!tr || !tr->enabled) return ptmi_model_train_step(ctx->dev, tokens, T, lr, loss);
+    ptmi_span_t *spans = (ptmi_span_t *)malloc(sizeof(ptmi_span_t) * PT_TRACE_MAX_EVENTS);
+    if (!spans) return ptmi_model_train_step(ctx->dev, tokens, T, lr, loss);
+    int n = 0;
+    const uint32_t t0 = pt_time_us();
+    const int st = ptmi_model_train_step_trace(ctx->dev, tokens, T, lr, loss, spans, PT_TRACE_MAX_EVENTS, &n);
+    if (st == 0) {
+        for (int i = 0; i < n; i++)
+            pt_trace_add(tr, spans[i].name, spans[i].cat, spans[i].layer, tr->depth + spans[i].depth,
+                         t0 + (uint32_t)(spans[i].start_us + 0.5), (uint32_t)(spans[i].dur_us + 0.5));
+    }
+    free(spans);
+    return st;
 }
 
 float pt_train_step(pt_context_t *ctx, const int *tokens, int T, float lr) {

@@ -1,0 +1,88 @@
+"""GPU: the traced training step (ptmi_model_train_step_trace) and the
+host trace API behind pt_enable_trace (pitorch/pt.c:322-364,
+pitorch/profiler/trace.c).
+
+* The traced step runs the same kernels without the graph: its loss and
+  updated weights equal the untraced step's exactly.
+* Its spans carry the reference's names (pt.c:339-364, pt_train.c:171-866)
+  and nest: every span lies inside its parent, in the order trace.c
+  records them (children end first).
+* pt_demo (a C caller of pt.h) writes trace.json / meta.json as the
+  reference's dev/host/test_train_profiled.c does.
+"""
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import pitorch_amd as pa
+
+pytestmark = pytest.mark.gpu
+CFG = (64, 160, 2, 4, 4, 512, 32)
+PER_LAYER = ["layer", "qkv", "attention", "wo", "ffn"]
+
+
+def expected_names(L):
+    top = ["train_step", "zero_grads", "forward", "embedding", "classifier", "loss", "backward", "classifier",
+           "weight_grads", "embedding", "sgd"]
+    return sorted(top + PER_LAYER * (2 * L))
+
+
+def check_nesting(spans, slack):
+    """spans in end order, each with depth/start/dur: every span of depth d > 0
+    lies inside the next span (in end order) of depth d - 1."""
+    for i, s in enumerate(spans):
+        if s["depth"] == 0:
+            continue
+        parent = next(p for p in spans[i + 1:] if p["depth"] == s["depth"] - 1)
+        assert parent["start"] - slack <= s["start"], (s, parent)
+        assert s["start"] + s["dur"] <= parent["start"] + parent["dur"] + slack, (s, parent)
+
+
+def test_traced_step_equals_untraced_and_spans_nest():
+    blob = pa.synth_model(CFG, 31, 0.05)
+    tokens = pa.seed_tokens(32, 16, CFG[5])
+    a, b = pa.Model(blob.copy(), max_T=16), pa.Model(blob.copy(), max_T=16)
+    for _ in range(2):
+        la, spans = a.train_step_trace(tokens, 0.05)
+        lb = b.train_step(tokens, 0.05)
+        assert la == lb
+    assert np.array_equal(a.read_weights(), b.read_weights())
+    assert sorted(s["name"] for s in spans) == expected_names(CFG[2])
+    assert spans[-1]["name"] == "train_step" and spans[-1]["depth"] == 0 and spans[-1]["start_us"] == 0.0
+    check_nesting([dict(depth=s["depth"], start=s["start_us"], dur=s["dur_us"]) for s in spans], 1e-3)
+    for s in spans:
+        assert s["dur_us"] >= 0.0
+        if s["name"] in ("qkv", "attention", "wo", "ffn", "weight_grads", "loss"):
+            assert s["dur_us"] > 0.0, s
+        assert (s["layer"] >= 0) == (s["name"] in PER_LAYER)
+    depth1 = sum(s["dur_us"] for s in spans if s["depth"] == 1)
+    assert depth1 <= spans[-1]["dur_us"] + 1e-3
+    with pytest.raises(pa.PtmiError):
+        a.train_step_trace(tokens, 0.05, max_spans=3)             # buffer smaller than the step's spans
+    a.close()
+    b.close()
+
+
+def test_c_caller_writes_trace_json(tmp_path):
+    demo = os.path.join(pa.lib_dir(), "pt_demo")
+    args = [demo, "train", *map(str, CFG), "33", "34", "16", "0.05", "2"]
+    plain = subprocess.run(args, capture_output=True, text=True, timeout=120)
+    traced = subprocess.run(args + [str(tmp_path)], capture_output=True, text=True, timeout=120)
+    assert plain.returncode == 0 and traced.returncode == 0, traced.stderr[-2000:]
+    losses = lambda out: [ln for ln in out.splitlines() if ln.startswith("loss ")]
+    assert losses(plain.stdout) == losses(traced.stdout)
+    ev = json.load(open(tmp_path / "trace.json"))
+    L = CFG[2]
+    assert len(ev) == 2 * (11 + 10 * L)
+    names = sorted(e["name"].split("_", 1)[1] if e["name"][0] == "L" and e["name"][1].isdigit() else e["name"]
+                   for e in ev[: len(ev) // 2])
+    assert names == expected_names(L)
+    assert all(e["ph"] == "X" and e["cat"] in ("train", "fwd", "bwd") for e in ev)
+    assert {e["name"] for e in ev if e["name"].startswith("L")} == {f"L{l}_{n}" for l in range(L) for n in PER_LAYER}
+    steps = [e for e in ev if e["name"] == "train_step"]
+    assert len(steps) == 2 and steps[0]["ts"] + steps[0]["dur"] <= steps[1]["ts"] + 1
+    meta = json.load(open(tmp_path / "meta.json"))
+    assert meta["steps"] == 2 and meta["layers"] == L and meta["device"] == "mi355x"
