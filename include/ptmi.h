@@ -154,8 +154,10 @@ typedef struct {
     double      start_us;   /* from the beginning of train_step */
     double      dur_us;
 } ptmi_span_t;
-/* ptmi_model_train_step run without the graph, with HIP events around the
- * phases (pt_train_step with ctx->trace enabled, pt.c:339-364).  Spans are
+/* ptmi_model_train_step with HIP events around the phases (pt_train_step
+ * with ctx->trace enabled, pt.c:339-364), enqueued without the graph
+ * behind a short bounded busy kernel, so the step's kernels run back to
+ * back and the spans time device work.  Spans are
  * written in the order they end, as trace.c records them; *n_spans gets
  * the step's span count, and a buffer of fewer than that many spans is an
  * error (nothing is written to it; the step has run).                  */

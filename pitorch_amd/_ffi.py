@@ -242,7 +242,7 @@ class Model:
         return loss.value
 
     def train_step_trace(self, tokens, lr, max_spans=4096):
-        """The same step run without the graph, with its device-timed spans
+        """The same step with its device-timed spans
         (ptmi_model_train_step_trace): (loss, [dict(name, cat, layer, depth,
         start_us, dur_us)]) in the order the spans end."""
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)

@@ -1077,6 +1077,16 @@ __global__ __launch_bounds__(1024) void k_step_tail(const NormDw *nd, int cb, in
     else loss_mean_block<16>(row_loss, R, loss);
 }
 
+// One wave of dependent FMAs for a fixed count (several ms): it holds the
+// stream while the host enqueues a traced step behind it.  The store is
+// never taken; it keeps the loop live.
+constexpr int kHoldIters = 1 << 20;
+__global__ void k_hold(float *sink, int iters) {
+    float v = (float)threadIdx.x;
+    for (int i = 0; i < iters; i++) v = fmaf(v, 0.999f, 1.0f);
+    if (v == -1.0f) *sink = v;
+}
+
 // Zero fill (pt_zero_grads, pt_train.c:425-427), a kernel rather than a
 // memset node so the step can be captured.
 __global__ void k_fill0(float *p, long n) {
@@ -1219,8 +1229,8 @@ int train_descriptors(ptmi_model *m, int T) {
 // Device-timed spans of one training step, for the reference's trace
 // (pitorch/profiler/trace.c): begin/end record HIP events on the step's
 // stream around the launches of a phase, nested like pt_train.c's
-// pt_trace_begin/pt_trace_end calls.  Only used for eager (uncaptured)
-// steps; spans are kept in the order they end, as trace.c records them.
+// pt_trace_begin/pt_trace_end calls; spans are kept in the order they end,
+// as trace.c records them.
 struct TrainTracer {
     struct Rec { const char *name, *cat; int layer, depth; hipEvent_t b, e; };
     std::vector<Rec> open, done;
@@ -1550,6 +1560,8 @@ int ptmi_model_train_step(ptmi_model_t *m, const int *tokens, int T, float lr, f
     return PTMI_OK;
 }
 
+static float *ts_sink(ptmi_model_t *m) { return m->train->ws; }
+
 int ptmi_model_train_step_trace(ptmi_model_t *m, const int *tokens, int T, float lr, float *loss,
                                 ptmi_span_t *spans, int max_spans, int *n_spans) {
     if (!n_spans || (max_spans > 0 && !spans) || max_spans < 0) return set_error(PTMI_ERR_ARG, "bad span buffer");
@@ -1559,6 +1571,12 @@ int ptmi_model_train_step_trace(ptmi_model_t *m, const int *tokens, int T, float
     hipStream_t s = lib_stream();
     TrainTracer tr;
     tr.s = s;
+    // The traced step is enqueued eagerly (events do not time graph nodes)
+    // behind a bounded busy kernel that holds the stream while the host
+    // enqueues it, so its kernels then run back to back and the spans time
+    // device work, not the host's enqueue gaps.
+    hipLaunchKernelGGL(k_hold, dim3(1), dim3(64), 0, s, ts_sink(m), kHoldIters);
+    PTMI_HIP(hipGetLastError());
     st = enqueue_train(m, T, s, &tr);
     float l = 0.0f;
     if (!st) {

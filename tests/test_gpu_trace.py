@@ -2,7 +2,7 @@
 host trace API behind pt_enable_trace (pitorch/pt.c:322-364,
 pitorch/profiler/trace.c).
 
-* The traced step runs the same kernels without the graph: its loss and
+* The traced step runs the same kernels (eagerly, behind a busy kernel): its loss and
   updated weights equal the untraced step's exactly.
 * Its spans carry the reference's names (pt.c:339-364, pt_train.c:171-866)
   and nest: every span lies inside its parent, in the order trace.c
