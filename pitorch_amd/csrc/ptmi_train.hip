@@ -310,7 +310,10 @@ __global__ __launch_bounds__(kLossThreads) void k_loss_rows(float *lg_dl, const 
 // logits and one exp per element.  The maximum comes first, then the sum of
 // e^(x - max) (the reference's loss order, pt_train.c:311-323), and the
 // gradient is formed from the kept exps.  Loads are unconditional (clamped
-// to the row) and out-of-row slots are dropped by selects.
+// to the row) and out-of-row slots are dropped by selects.  The gradient
+// rows are written with nontemporal stores: a 1024-thread block streaming
+// its 128 KB row out with ordinary stores measured 2x slower (a row-copy
+// probe: 19.8 vs 9.2 us for 32.8 MB).
 template <int NS>
 __global__ __launch_bounds__(kLossThreads) void k_loss_rows_reg(float *lg_dl, const int *tok, int T, int V,
                                                                 float inv_T1, float *row_loss) {
@@ -346,18 +349,18 @@ __global__ __launch_bounds__(kLossThreads) void k_loss_rows_reg(float *lg_dl, co
     const float sum = block_sum<kLossThreads / 64>(s, red);
     if (tid == 0) row_loss[t] = -(xt - mx - d_logf(sum));
     const float scale = (1.0f / sum) * inv_T1;
+    typedef float fx4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int i = 0; i < NS; i++) {
         const int v = tid + i * kLossThreads;
         if (v < n4) {
-            float4 d;
-            d.x = x[i].x * scale;
-            d.y = x[i].y * scale;
-            d.z = x[i].z * scale;
-            d.w = x[i].w * scale;
+            fx4 d = {x[i].x * scale, x[i].y * scale, x[i].z * scale, x[i].w * scale};
             const int b = 4 * v;
-            if (target >= b && target < b + 4) (&d.x)[target - b] -= inv_T1;
-            row4[v] = d;
+            d.x = target == b ? d.x - inv_T1 : d.x;
+            d.y = target == b + 1 ? d.y - inv_T1 : d.y;
+            d.z = target == b + 2 ? d.z - inv_T1 : d.z;
+            d.w = target == b + 3 ? d.w - inv_T1 : d.w;
+            __builtin_nontemporal_store(d, reinterpret_cast<fx4 *>(row4) + v);
         }
     }
 }
