@@ -131,15 +131,21 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
     // Rows past the end re-read the wave's last row; their sums are dropped.
     constexpr int kIterRows = NP * RPP;
     float4 wv[NP][IT];
+    // Weight rows are read with nontemporal loads: each is read once per
+    // step, and the hint keeps this stream from evicting the weights that
+    // prefetch blocks have staged in L2 for the next kernels (decode
+    // 3498 -> 3565 tok/s, stories110M).
+    typedef float fx4 __attribute__((ext_vector_type(4)));
     auto load_rows = [&](int base) {
 #pragma unroll
         for (int q = 0; q < NP; q++) {
             const int r = max(0, min(base + q * RPP + slot, nrows - 1));   // idle waves read row 0
-            const float4 *w = reinterpret_cast<const float4 *>(p.W + (long)(row0 + r) * p.ld);
+            const fx4 *w = reinterpret_cast<const fx4 *>(p.W + (long)(row0 + r) * p.ld);
 #pragma unroll
             for (int it = 0; it < IT; it++) {
                 const int c = sub + it * LPR;
-                wv[q][it] = w[it < IT - 1 ? c : min(c, n4 - 1)];
+                const fx4 t = __builtin_nontemporal_load(w + (it < IT - 1 ? c : min(c, n4 - 1)));
+                wv[q][it] = make_float4(t.x, t.y, t.z, t.w);
             }
         }
     };
