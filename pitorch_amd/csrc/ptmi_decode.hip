@@ -88,9 +88,16 @@ __global__ __launch_bounds__(kAttnWaves * 64) void k_attn_chunk(AttnParams a) {
     const float4 *vbase = reinterpret_cast<const float4 *>(a.vc + ko) + sub_c;
     const long row4 = a.kv_dim >> 2;                     // float4 per cache row
 
+    // K/V rows with nontemporal loads: read once per step, they should not
+    // evict the w1|w3 weights this launch's prefetch blocks stage in L2.
+    typedef float fx4 __attribute__((ext_vector_type(4)));
     auto load_rows = [&](const float4 *src, int base, float4 (&dst)[kAttnUnroll]) {
 #pragma unroll
-        for (int u = 0; u < kAttnUnroll; u++) dst[u] = src[(long)min(base + u * RPI + slot, t1 - 1) * row4];
+        for (int u = 0; u < kAttnUnroll; u++) {
+            const fx4 t = __builtin_nontemporal_load(
+                reinterpret_cast<const fx4 *>(src + (long)min(base + u * RPI + slot, t1 - 1) * row4));
+            dst[u] = make_float4(t.x, t.y, t.z, t.w);
+        }
     };
     auto score_rows = [&](int base, const float4 (&k4)[kAttnUnroll]) {
 #pragma unroll
