@@ -28,6 +28,7 @@ namespace {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int BK = 32;
+constexpr int kXcdGrid = 768;             // grids this large take their tiles in XCD order
 constexpr int kRing64 = 2, kRing32 = 2;   // K tiles in flight per block tile size
 
 struct GemmArgs {
@@ -181,22 +182,25 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
         store_tile<AT, TM>(As[s & 1], tid, xa);
         store_tile<!BT, TN>(Bs[s & 1], tid, xb);
     };
-    // The operands of k group kk+4 are read from LDS before the MFMAs of
-    // group kk issue, so their latency overlaps those MFMAs.
+    // The operands of k group kk+4*RA are read from LDS before the MFMAs of
+    // group kk issue, so their latency overlaps RA groups of MFMAs (RA = 2
+    // and 3 measured no faster).
+    constexpr int RA = 1;
     auto compute = [&](int s) {
         const int buf = s & 1;
-        float a[2][FM], b[2][FN];
+        float a[RA + 1][FM], b[RA + 1][FN];
         auto read = [&](int kk, float (&ar)[FM], float (&br)[FN]) {
 #pragma unroll
             for (int i = 0; i < FM; i++) ar[i] = As[buf][kk + lk][lds_col<AT, TM>(kk + lk, wm * (TM / 2) + i * 16 + li)];
 #pragma unroll
             for (int j = 0; j < FN; j++) br[j] = Bs[buf][kk + lk][lds_col<!BT, TN>(kk + lk, wn * (TN / 2) + j * 16 + li)];
         };
-        read(0, a[0], b[0]);
+#pragma unroll
+        for (int r = 0; r < RA; r++) read(4 * r, a[r], b[r]);
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 4) {
-            const int c = (kk / 4) & 1;
-            if (kk + 4 < BK) read(kk + 4, a[c ^ 1], b[c ^ 1]);
+            const int c = (kk / 4) % (RA + 1);
+            if (kk + 4 * RA < BK) read(kk + 4 * RA, a[(kk / 4 + RA) % (RA + 1)], b[(kk / 4 + RA) % (RA + 1)]);
             __builtin_amdgcn_sched_barrier(0);              // keep the reads ahead of the MFMAs
 #pragma unroll
             for (int i = 0; i < FM; i++)
@@ -300,16 +304,39 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
     }
 }
 
+// Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its
+// own L2.  Block b runs tile xcd_tile(b): XCD c gets the c-th contiguous
+// range of the tiles, in order, so tiles that read the same operand tile
+// run together on one XCD and fetch it into that L2 once.
+__device__ __forceinline__ int xcd_tile(int b, int total) {
+    const int q = total >> 3, r = total & 7, c = b & 7;
+    return c * q + min(c, r) + (b >> 3);
+}
+
+// Grids of kXcdGrid blocks and more take tiles in xcd_tile order: split
+// index slowest; within a split, neighbouring tiles share the tile of the
+// larger operand (A's rows when M > N, else B's columns).  Smaller grids
+// (at most a few blocks per CU, no reuse to gain) keep the grid's order.
 template <bool AT, bool BT, int TM, int TN, int P, bool VEC, int EPI = GEMM_EPI_NONE>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
-    gemm_tile<AT, BT, TM, TN, P, VEC, EPI>(g, blockIdx.y * TM, blockIdx.x * TN, blockIdx.z);
+    const int gx = gridDim.x, gy = gridDim.y, per_z = gx * gy, total = per_z * gridDim.z;
+    int m = blockIdx.y, n = blockIdx.x, z = blockIdx.z;
+    if (total >= kXcdGrid) {                                        // uniform
+        const int t = xcd_tile(blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z), total);
+        z = t / per_z;
+        const int u = t - z * per_z;
+        if (g.M > g.N) m = u / gx, n = u - m * gx;
+        else n = u / gy, m = u - n * gy;
+    }
+    gemm_tile<AT, BT, TM, TN, P, VEC, EPI>(g, m * TM, n * TN, z);
 }
 
 // Grouped TN GEMMs (32x32 tiles, whole K): block b runs tile
-// b - d.tile0 of the descriptor d whose tile range holds b.
+// t = xcd_tile(b) - d.tile0 of the descriptor d whose tile range holds it;
+// tiles run along N first, so neighbours share the A^T tile.
 template <int TM, int TN, bool VEC>
 __global__ __launch_bounds__(256) void k_gemm_tn_group(const GemmGroupDesc *d, int n) {
-    const int b = blockIdx.x;
+    const int b = xcd_tile(blockIdx.x, gridDim.x);
     int i = 0;
     while (i + 1 < n && d[i + 1].tile0 <= b) i++;
     const GemmGroupDesc &e = d[i];

@@ -113,6 +113,36 @@ def test_gemm_dev_ops_with_strides(op):
         a.free()
 
 
+# Grids of 768 blocks and more take their tiles in XCD order (each XCD a
+# contiguous tile range, ordered along the larger operand): ragged M, N and
+# K on 64x64 and 32x32 tiles, split K for the NN forms; a NaN-filled C shows
+# any tile left unwritten.
+@pytest.mark.parametrize("op,M,N,K", [(2, 200, 20000, 300), (2, 260, 20000, 300), (0, 255, 320, 30000),
+                                      (0, 130, 288, 30000), (1, 30004, 288, 130), (1, 32000, 256, 131)])
+def test_gemm_dev_large_grids(op, M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    if op == 0:
+        A = rng.uniform(-1, 1, (M, K)); B = rng.uniform(-1, 1, (K, N))
+        Aop, Bop = A, B
+    elif op == 1:
+        A = rng.uniform(-1, 1, (K, M)); B = rng.uniform(-1, 1, (K, N))
+        Aop, Bop = A.T, B
+    else:
+        A = rng.uniform(-1, 1, (M, K)); B = rng.uniform(-1, 1, (N, K))
+        Aop, Bop = A, B.T
+    A, B = A.astype(np.float32), B.astype(np.float32)
+    dA, dB = DeviceArray.from_host(A), DeviceArray.from_host(B)
+    dC = DeviceArray.from_host(np.full((M, N), np.nan, np.float32))
+    L = pa.load_ptmi()
+    assert L.ptmi_gemm_dev(op, dA.ptr, A.shape[1], dB.ptr, B.shape[1], dC.ptr, N, M, N, K, 0, None) == 0
+    assert L.ptmi_sync() == 0
+    got = dC.download().reshape(M, N)
+    Af, Bf = Aop.astype(np.float32).astype(np.float64), Bop.astype(np.float32).astype(np.float64)
+    assert bound_ok(got, Af @ Bf, np.abs(Af) @ np.abs(Bf), K)
+    for a in (dA, dB, dC):
+        a.free()
+
+
 def test_gemm_errors():
     L = pa.load_ptmi()
     A = np.ones((4, 4), np.float32)
