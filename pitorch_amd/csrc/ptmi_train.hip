@@ -882,14 +882,37 @@ __global__ __launch_bounds__(kMT) void k_attn_fwd_mfma(const float *qkv, float *
 // the column half), then d_q = ds.K, stored after rope_backward into the q
 // columns of the fused [dq | dk | dv] row d_qkv.  LDS as k_attn_fwd_mfma.
 template <int HQ>
-__global__ __launch_bounds__(kMT) void k_attn_bwd_rows_mfma(const float *qkv, const float *att, const float *d_aout,
-                                                           float *ds, float *d_qkv, int T, int R, int D, int QS,
-                                                           float scale, int pitch) {
+// With d_res non-null (D a multiple of 4*kMW), the block first computes its
+// own tile of d_aout = d_res . Wo (backward_input of the Wo projection,
+// pt_train.c:729-730: rows [r0, r0+16), head h's columns), each wave over
+// a D/kMW slice of the contraction summed in wave order, and writes it for
+// the column kernel; the first dot product below reads it back.
+__global__ __launch_bounds__(kMT) void k_attn_bwd_rows_mfma(const float *qkv, const float *att, float *d_aout,
+                                                           const float *d_res, const float *wo, float *ds,
+                                                           float *d_qkv, int T, int R, int D, int QS, float scale,
+                                                           int pitch) {
     extern __shared__ float lds[];
     constexpr int HD = 16 * HQ, RW = 16 / kMW;             // rows per wave
     const int r0 = blockIdx.x * 16, h = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nkb = (min(r0 + 16, R) + 15) / 16, kw = nkb * 16;
     const float *k = qkv + D + h * HD, *v = qkv + 2 * D + h * HD;
+    if (d_res) {                                            // uniform
+        const int li = lane & 15, g = lane >> 4, ks = D / kMW, k0 = wave * ks;
+        const float *ap = d_res + (long)min(r0 + li, R - 1) * D + k0 + g;
+        const float *bp = wo + (long)(k0 + g) * D + h * HD + li;
+        f4v acc[HQ];
+#pragma unroll
+        for (int cb = 0; cb < HQ; cb++) acc[cb] = f4v{0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < ks; s += 4) {
+            const float a = ap[s];
+#pragma unroll
+            for (int cb = 0; cb < HQ; cb++) acc[cb] = mfma4(a, bp[(long)s * D + cb * 16], acc[cb]);
+        }
+        attn_reduce<HQ>(acc, lds, [&](int i, int c, float o, float) {
+            if (r0 + i < R) d_aout[(long)(r0 + i) * D + h * HD + c] = o;
+        });
+        __syncthreads();                                   // the tile is written; lds is free again
+    }
     // this wave's att rows (keys < n, clamped), fetched with the GEMM operands
     float ar[RW][kAttnChunks][4];
 #pragma unroll
@@ -1287,7 +1310,8 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr
     // to 128), a row fits the softmax's registers and the LDS fits in 64 KB;
     // otherwise the per-position ones.
     using MfFwd = void (*)(const float *, float *, float *, int, int, int, float, int);
-    using MfRows = void (*)(const float *, const float *, const float *, float *, float *, int, int, int, int, float,
+    using MfRows = void (*)(const float *, const float *, float *, const float *, const float *, float *, float *, int,
+                            int, int, int, float,
                             int);
     using MfCols = void (*)(const float *, const float *, const float *, const float *, float *, int, int, int, int);
     static const MfFwd mf_fwd[8] = {k_attn_fwd_mfma<1>, k_attn_fwd_mfma<2>, k_attn_fwd_mfma<3>, k_attn_fwd_mfma<4>,
@@ -1450,15 +1474,17 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr
         if ((st = gemm(s, ts, 0, dh13, 2 * H, w13, D, dxb(v), D, R, D, 2 * H, 0, nullptr, &pk))) return st;
         norm_bwd(rmid, r->rms_ffn + (long)l * D);
         SPAN_END();
-        // Wo
+        // Wo: d_aout = d_res . Wo, inside the matrix-core attention rows
+        // kernel when D splits over its waves in whole MFMA k steps
+        const bool wo_fused = mfma_attn && D % (4 * kMW) == 0;
         SPAN("wo", "bwd", l);
-        if ((st = gemm(s, ts, 0, dres(v), D, wo, D, ts->d_aout, D, R, D, D, 0))) return st;
+        if (!wo_fused && (st = gemm(s, ts, 0, dres(v), D, wo, D, ts->d_aout, D, R, D, D, 0))) return st;
         SPAN_END();
         // attention
         SPAN("attention", "bwd", l);
         if (mfma_attn) {
             hipLaunchKernelGGL(mf_rows[HQ - 1], dim3((R + 15) / 16, NH), dim3(kMT), mf_lds, s, qkv, att, ts->d_aout,
-                               ts->ds, dqkv, T, R, D, QS, scale, pitch);
+                               wo_fused ? dres(v) : nullptr, wo, ts->ds, dqkv, T, R, D, QS, scale, pitch);
             hipLaunchKernelGGL(mf_cols[HQ - 1], dim3((R + 15) / 16, NH), dim3(kMT), mc_lds, s, qkv, att, ts->ds,
                                ts->d_aout, dqkv, T, R, D, QS);
         } else {
