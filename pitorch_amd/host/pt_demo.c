@@ -22,6 +22,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/stat.h>
 
 #include "pt.h"
 
@@ -100,8 +101,15 @@ static int train(const pt_config_t *cfg, unsigned long long mseed, unsigned long
     }
     if (trace_dir) {
         char path[1024];
+        mkdir(trace_dir, 0755);                 /* as dev/host/test_train_profiled.c:88 */
         snprintf(path, sizeof path, "%s/trace.json", trace_dir);
         pt_trace_write_json(ctx.trace, path);
+        FILE *check = fopen(path, "r");
+        if (!check) {
+            fprintf(stderr, "pt_demo: could not write %s\n", path);
+            return 1;
+        }
+        fclose(check);
         printf("trace %s %d events\n", path, ctx.trace->count);
         snprintf(path, sizeof path, "%s/meta.json", trace_dir);
         pt_trace_write_meta(path, "synthetic training, traced", "synthetic", cfg->dim, cfg->n_layers,
