@@ -69,12 +69,16 @@ def test_traced_step_equals_untraced_and_spans_nest():
 def test_c_caller_writes_trace_json(tmp_path):
     demo = os.path.join(pa.lib_dir(), "pt_demo")
     args = [demo, "train", *map(str, CFG), "33", "34", "16", "0.05", "2"]
+    out = tmp_path / "trace"                   # created by pt_demo, as the reference's profiled test does
     plain = subprocess.run(args, capture_output=True, text=True, timeout=120)
-    traced = subprocess.run(args + [str(tmp_path)], capture_output=True, text=True, timeout=120)
+    traced = subprocess.run(args + [str(out)], capture_output=True, text=True, timeout=120)
     assert plain.returncode == 0 and traced.returncode == 0, traced.stderr[-2000:]
     losses = lambda out: [ln for ln in out.splitlines() if ln.startswith("loss ")]
     assert losses(plain.stdout) == losses(traced.stdout)
-    ev = json.load(open(tmp_path / "trace.json"))
+    # a trace that cannot be written is an error, not a silent success
+    bad = subprocess.run(args + [str(tmp_path / "no" / "such" / "dir")], capture_output=True, text=True, timeout=120)
+    assert bad.returncode != 0 and "could not write" in bad.stderr
+    ev = json.load(open(out / "trace.json"))
     L = CFG[2]
     assert len(ev) == 2 * (11 + 10 * L)
     names = sorted(e["name"].split("_", 1)[1] if e["name"][0] == "L" and e["name"][1].isdigit() else e["name"]
@@ -84,5 +88,5 @@ def test_c_caller_writes_trace_json(tmp_path):
     assert {e["name"] for e in ev if e["name"].startswith("L")} == {f"L{l}_{n}" for l in range(L) for n in PER_LAYER}
     steps = [e for e in ev if e["name"] == "train_step"]
     assert len(steps) == 2 and steps[0]["ts"] + steps[0]["dur"] <= steps[1]["ts"] + 1
-    meta = json.load(open(tmp_path / "meta.json"))
+    meta = json.load(open(out / "meta.json"))
     assert meta["steps"] == 2 and meta["layers"] == L and meta["device"] == "mi355x"
