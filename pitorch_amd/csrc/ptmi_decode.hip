@@ -43,8 +43,10 @@ __device__ __forceinline__ float dot4(float4 a, float4 b, float acc) {
     return fmaf(a.w, b.w, acc);
 }
 
-constexpr int kAttnWaves = 4;
-constexpr int kAttnUnroll = 8;
+// 8 waves of 4 loads in flight cover a 128-position chunk in one batch
+// (G = 16): 3664 tok/s against 3589 for 4 waves of 8 and 3376 for 16 of 2.
+constexpr int kAttnWaves = 8;
+constexpr int kAttnUnroll = 4;
 constexpr int kMaxAttnChunk = 512;
 
 // llama2.c:153-177, split over (head, chunk of positions) workgroups so the
