@@ -410,8 +410,9 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd_rows(float *d_out, const fl
 }
 
 // ── RMSNorm rows, one wave per row ──────────────────────────────────────
-// The same two row kernels for D % 4 == 0 and D <= 256*NV: four rows per
-// 256-thread block, lane l holding float4s l, 64 + l, ... of its row in
+// The same two row kernels for D % 4 == 0 and D <= 256*NV: one wave per
+// row (launched as one-wave blocks, so the rows spread over as many CUs as
+// possible), lane l holding float4s l, 64 + l, ... of its row in
 // registers, so every load of the row goes out together and the row sums
 // are DPP reductions without block barriers.
 
@@ -447,7 +448,7 @@ template <int NV>
 __global__ __launch_bounds__(256) void k_rmsnorm_rows_w(float *in, const float *w, float *out, int rows, int D,
                                                        SplitK pk, const float *cin, const int *tok, const float *emb,
                                                        unsigned *tok_bits) {
-    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6), d4 = D / 4;
+    const int lane = threadIdx.x & 63, row = blockIdx.x * (int)(blockDim.x >> 6) + (threadIdx.x >> 6), d4 = D / 4;
     if (row >= rows) return;                                     // wave-uniform
     const long r4 = (long)row * d4;
     float4 *x4 = reinterpret_cast<float4 *>(in) + r4;
@@ -499,7 +500,7 @@ template <int NV>
 __global__ __launch_bounds__(256) void k_rmsnorm_bwd_rows_w(float *d_out, const float *d_in, float *d_o,
                                                            const float *x, const float *w, float *inv_out, int rows,
                                                            int D, SplitK pk) {
-    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6), d4 = D / 4;
+    const int lane = threadIdx.x & 63, row = blockIdx.x * (int)(blockDim.x >> 6) + (threadIdx.x >> 6), d4 = D / 4;
     if (row >= rows) return;                                     // wave-uniform
     const long r4 = (long)row * d4;
     const float4 *x4 = reinterpret_cast<const float4 *>(x) + r4, *w4 = reinterpret_cast<const float4 *>(w);
@@ -1350,7 +1351,7 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr
     // embed: gather the rows from the embedding table first (layer 0)
     auto norm_fwd = [&](float *in, const float *w, float *out, SplitK pk, const float *cin, bool embed) {
         if (wave_norm) {
-            hipLaunchKernelGGL(norm_w[nv - 1], dim3((T + 3) / 4), dim3(256), 0, s, in, w, out, T, D, pk, cin,
+            hipLaunchKernelGGL(norm_w[nv - 1], dim3(T), dim3(64), 0, s, in, w, out, T, D, pk, cin,
                                embed ? ts->tok : nullptr, r->emb, ts->tok_bits);
         } else {
             if (embed) hipLaunchKernelGGL(k_embed_rows, dim3(T), dim3(256), 0, s, ts->tok, r->emb, in, D, ts->tok_bits,
@@ -1443,7 +1444,7 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr
     auto norm_bwd = [&](const float *x, const float *w) {
         // d_res[v+1] = d_res[v] + rmsnorm_backward(d_xb[v]); inverse norms kept per norm
         if (wave_norm)
-            hipLaunchKernelGGL(norm_bwd_w[nv - 1], dim3((R + 3) / 4), dim3(256), 0, s, dres(v + 1),
+            hipLaunchKernelGGL(norm_bwd_w[nv - 1], dim3(R), dim3(64), 0, s, dres(v + 1),
                                v ? dres(v) : nullptr, dxb(v), x, w, ts->row_inv + (long)v * T, R, D, pk);
         else
             hipLaunchKernelGGL(k_rmsnorm_bwd_rows, dim3(R), dim3(256), 0, s, dres(v + 1), v ? dres(v) : nullptr,
