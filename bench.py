@@ -1,13 +1,17 @@
 """Benchmark: stories110M-shaped fp32 greedy decode on one MI355X.
 
-One step = one decode token (one hipGraph launch of the device-resident
-pt_forward_step: 85 projections + attention + argmax), synthetic random-init
-weights ~N(0, 0.02), positions 0..K-1 of a 1024-position KV cache (the cache
-is zeroed and restarted inside the timed region when K > seq_len).
+One step = one full greedy decode of the 1024-position context (BASELINE
+config 4): pt_generate over token ids (prompt forcing, then argmax), each
+position one hipGraph launch of the device-resident pt_forward_step (85
+projections + attention + argmax), positions 0..1023 of the KV cache,
+synthetic random-init weights ~N(0, 0.02).  `value` = decoded tokens per
+second over the K timed decodes.
 
 Prints ONE JSON line: decode tok/s as `value`, the dominant kernel's HBM
-roofline (per-launch HIP-event timing of eager steps, algorithmic bytes per
-launch) and the reference's own CPU decode timed on a bounded sample.
+roofline (per-launch HIP-event timing of eager steps over all 1024
+positions, algorithmic bytes per launch, counter-measured HBM traffic) and
+the reference's own CPU decode timed on a bounded sample, pinned to one
+core.
 """
 import argparse
 import json
@@ -81,7 +85,10 @@ def matvec_sweep(pa, footprint_mb=1536, reps_max=2048):
     footprint well above the 256 MB MALL so every launch reads HBM.  The
     launches are captured back to back in a hipGraph on the library stream
     and timed with HIP events around its replay, so host launch cost is not
-    in the figure."""
+    in the figure.  Each shape is timed with the default kernel (x held in
+    registers per wave) and with the ablation kernel that re-reads x for
+    every row pass (ptmi_matvec_dev_xreread, the counterpart of the
+    reference's smatvec_tmu_no_packing baseline)."""
     from pitorch_amd._hip import DeviceArray, Event, Graph
     L = pa.load_ptmi()
     stream = L.ptmi_stream()
@@ -92,33 +99,53 @@ def matvec_sweep(pa, footprint_mb=1536, reps_max=2048):
     for d, n in SWEEP:
         stride = (d * n + 63) // 64 * 64
         copies = max(1, min(big.n // stride, reps_max))
-        pa._ffi.check(L.ptmi_matvec_dev(big.ptr, n, x.ptr, y.ptr, d, n, None))
-        pa._ffi.check(L.ptmi_sync())
+        row = {"d": d, "n": n}
+        for tag, entry in (("", L.ptmi_matvec_dev), ("x_reread_", L.ptmi_matvec_dev_xreread)):
+            pa._ffi.check(entry(big.ptr, n, x.ptr, y.ptr, d, n, None))
+            pa._ffi.check(L.ptmi_sync())
 
-        def enqueue():
-            for i in range(copies):
-                pa._ffi.check(L.ptmi_matvec_dev(big.ptr + 4 * i * stride, n, x.ptr, y.ptr, d, n, stream))
+            def enqueue():
+                for i in range(copies):
+                    pa._ffi.check(entry(big.ptr + 4 * i * stride, n, x.ptr, y.ptr, d, n, stream))
 
-        g = Graph(stream, enqueue)
-        g.launch()
-        e0, e1 = Event(), Event()
-        e0.record(stream)
-        g.launch()
-        e1.record(stream)
-        us = e0.elapsed_ms(e1) * 1e3 / copies
-        g.free()
-        gbs = matvec_bytes(d, n) / (us * 1e-6) / 1e9
-        out.append({"d": d, "n": n, "us": round(us, 2), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            g = Graph(stream, enqueue)
+            g.launch()
+            e0, e1 = Event(), Event()
+            e0.record(stream)
+            g.launch()
+            e1.record(stream)
+            us = e0.elapsed_ms(e1) * 1e3 / copies
+            g.free()
+            gbs = matvec_bytes(d, n) / (us * 1e-6) / 1e9
+            row.update({tag + "us": round(us, 2), tag + "GBps": round(gbs, 1)})
+            if not tag:
+                row["frac"] = round(gbs / HBM_PEAK_GBS, 4)
+        out.append(row)
     for a in (big, x, y):
         a.free()
     return out
 
 
+class pinned_to_one_core:
+    """Run the block on one host core only (the reference path is
+    single-threaded; the survey's CPU baseline is `taskset -c 0`): the
+    lowest-numbered core this process may use (core 0 where it is allowed)."""
+
+    def __enter__(self):
+        self.saved = os.sched_getaffinity(0)
+        self.core = min(self.saved)
+        os.sched_setaffinity(0, {self.core})
+        return self
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.saved)
+
+
 def cpu_extra():
     """The reference's own host code (oracle/_ref, -O2 -ffp-contract=off,
-    1 thread) on the other measured paths: its smatvec_cpu at every sweep
-    shape (~0.2 s each) and one pt_train_step of the 15M training
-    configuration (T=256, same blob and ids; ~10 s)."""
+    1 thread pinned to one core) on the other measured paths: its
+    smatvec_cpu at every sweep shape (~0.2 s each) and one pt_train_step
+    of the 15M training configuration (T=256, same blob and ids; ~10 s)."""
     import ctypes
 
     import numpy as np
@@ -129,25 +156,27 @@ def cpu_extra():
     if R is None:
         return None
     sweep = []
-    for d, n in SWEEP:
-        W = pa.seed_uniform(4, d * n)
-        xx = pa.seed_uniform(5, n)
-        yy = np.zeros(d, np.float32)
-        k, t0 = 0, time.perf_counter()
-        while k < 2 or time.perf_counter() - t0 < 0.2:
-            R.smatvec_cpu(P(W), P(xx), P(yy), d, n)
-            k += 1
-        us = (time.perf_counter() - t0) * 1e6 / k
-        sweep.append({"d": d, "n": n, "us": round(us, 1), "GBps": round(matvec_bytes(d, n) / (us * 1e-6) / 1e9, 2)})
-    cfg = pa.STORIES["stories15M"]
-    blob = pa.synth_model(cfg, pa.SEED_MODEL["stories15M"])
-    tok = pa.seed_tokens(pa.SEED_TRAIN, 256, cfg[5]).astype(np.int32)
-    ctx = R.ref_ctx_new(P(blob), 256)
-    t0 = time.perf_counter()
-    R.ref_train_step(ctx, tok.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), 256, 1e-3)
-    train_s = time.perf_counter() - t0
-    R.ref_ctx_free(ctx)
-    return {"cores": 1, "kind": "reference", "matvec_sweep": sweep,
+    with pinned_to_one_core() as pin:
+        for d, n in SWEEP:
+            W = pa.seed_uniform(4, d * n)
+            xx = pa.seed_uniform(5, n)
+            yy = np.zeros(d, np.float32)
+            k, t0 = 0, time.perf_counter()
+            while k < 2 or time.perf_counter() - t0 < 0.2:
+                R.smatvec_cpu(P(W), P(xx), P(yy), d, n)
+                k += 1
+            us = (time.perf_counter() - t0) * 1e6 / k
+            sweep.append({"d": d, "n": n, "us": round(us, 1),
+                          "GBps": round(matvec_bytes(d, n) / (us * 1e-6) / 1e9, 2)})
+        cfg = pa.STORIES["stories15M"]
+        blob = pa.synth_model(cfg, pa.SEED_MODEL["stories15M"])
+        tok = pa.seed_tokens(pa.SEED_TRAIN, 256, cfg[5]).astype(np.int32)
+        ctx = R.ref_ctx_new(P(blob), 256)
+        t0 = time.perf_counter()
+        R.ref_train_step(ctx, tok.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), 256, 1e-3)
+        train_s = time.perf_counter() - t0
+        R.ref_ctx_free(ctx)
+    return {"cores": 1, "kind": "reference", "pinned": f"core {pin.core}", "matvec_sweep": sweep,
             "train_step": {"workload": "stories15M, T=256, lr=1e-3, 1 step", "s_per_step": round(train_s, 2)}}
 
 
@@ -161,12 +190,11 @@ def cpu_model():
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(blob, prompt, budget_s=12.0, max_tokens=96):
+def cpu_baseline(blob, prompt, budget_s=15.0, max_tokens=512):
     """The reference's own host decode (oracle/_ref: pitorch/pt.c
-    pt_forward_step with smatvec_cpu, built -O2 -ffp-contract=off),
-    single thread, on the same 110M blob and prompt."""
-    import ctypes
-
+    pt_forward_step with smatvec_cpu, built -O2 -ffp-contract=off), one
+    thread pinned to one core, on the same 110M blob and prompt: positions
+    0..n-1 of the same greedy decode, as many as fit the time budget."""
     from tests._oracle import P, ref
     R = ref()
     if R is None:
@@ -174,17 +202,18 @@ def cpu_baseline(blob, prompt, budget_s=12.0, max_tokens=96):
     ctx = R.ref_ctx_new(P(blob), 0)
     tok = int(prompt[0])
     n = 0
-    t0 = time.perf_counter()
-    while n < max_tokens and time.perf_counter() - t0 < budget_s:
-        nxt = R.ref_forward_step(ctx, tok)
-        tok = int(prompt[n + 1]) if n + 1 < len(prompt) else nxt
-        n += 1
-    dt = time.perf_counter() - t0
+    with pinned_to_one_core() as pin:
+        t0 = time.perf_counter()
+        while n < max_tokens and time.perf_counter() - t0 < budget_s:
+            nxt = R.ref_forward_step(ctx, tok)
+            tok = int(prompt[n + 1]) if n + 1 < len(prompt) else nxt
+            n += 1
+        dt = time.perf_counter() - t0
     R.ref_ctx_free(ctx)
-    del ctypes
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": 1, "kind": "reference",
-            "sample": f"first {n} positions of the stories110M greedy decode (same blob and prompt), "
-                      f"1 thread, {cpu_model()}, host nproc={os.cpu_count()}"}
+            "sample": f"positions 0..{n - 1} of the stories110M greedy decode (same blob and prompt; the "
+                      f"GPU figure covers 0..1023), 1 thread pinned to core {pin.core} of {cpu_model()}, "
+                      f"host nproc={os.cpu_count()}"}
 
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
@@ -324,8 +353,8 @@ def pmc_gemm(pa, reps):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1024)
-    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--steps", type=int, default=5, help="timed full 1024-position decodes")
+    ap.add_argument("--warmup", type=int, default=1, help="untimed full decodes first")
     ap.add_argument("--config", default="stories110M")
     ap.add_argument("--profile-steps", type=int, default=1024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -371,29 +400,25 @@ def main():
     L = pa.load_ptmi()
     print(f"[bench] {name} model resident ({blob.nbytes / 1e6:.1f} MB)", file=sys.stderr, flush=True)
 
-    # warmup
-    m.reset_kv()
-    m.decode_async(int(prompt[0]), min(args.warmup, S))
-    pa._ffi.check(L.ptmi_sync())
+    # warmup: full decodes (graph replays at every position, steady clocks)
+    gen = lambda: m.generate(prompt, S, stop_on_eos=False)
+    for _ in range(args.warmup):
+        gen()
 
-    # timed decode
-    m.reset_kv()
+    # timed: K full decodes of positions 0..S-1, back to back (each one
+    # zeroes the KV cache, forces the prompt, then decodes greedily; the
+    # host waits once per decode)
     pa._ffi.check(L.ptmi_sync())
-    left = args.steps
     t0 = time.perf_counter()
-    first = True
-    while left > 0:
-        n = min(left, S)
-        if not first:
-            m.reset_kv()
-        m.decode_async(int(prompt[0]), n)
-        left -= n
-        first = False
+    for _ in range(args.steps):
+        toks = gen()
+        assert len(toks) == S
     pa._ffi.check(L.ptmi_sync())
     dt = time.perf_counter() - t0
-    tok_s = args.steps / dt
-    print(f"[bench] decode {args.steps} steps in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s", file=sys.stderr,
-          flush=True)
+    n_tok = args.steps * S
+    tok_s = n_tok / dt
+    print(f"[bench] {args.steps} decodes x {S} positions in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s",
+          file=sys.stderr, flush=True)
 
     # per-kernel durations: eager steps over the same positions, each launch
     # bracketed by HIP events that the command processor stamps at the
@@ -416,8 +441,8 @@ def main():
     kernel_ms = sum(e["total_ms"] for e in breakdown.values()) / n_prof
     for r, e in breakdown.items():
         print(f"[bench] {r:12s} {json.dumps(e)}", file=sys.stderr, flush=True)
-    step_bytes = decode_bytes_per_token(cfg, [p % S for p in range(args.steps)])
-    step_gbs = step_bytes / (dt / args.steps) / 1e9
+    step_bytes = decode_bytes_per_token(cfg, range(S))
+    step_gbs = step_bytes / (dt / n_tok) / 1e9
 
     m.close()
     del blob
@@ -434,9 +459,8 @@ def main():
     del blob
     cpu_more = None if args.no_cpu else cpu_extra()
     # measured HBM bytes per launch of the dominant kernel (fetch + write,
-    # counter-calibrated); only for the workload the committed passes ran
-    default_run = args.steps == 1024 and args.profile_steps == 1024 and args.warmup == 32
-    traffic = committed_traffic(dominant, name) if default_run else None
+    # counter-calibrated), from the committed passes over all S positions
+    traffic = committed_traffic(dominant, name) if n_prof == S else None
 
     line = {
         "metric": "decode tok/s + matvec HBM GB/s (% peak), stories110M-shape fp32, 1 GPU",
@@ -445,15 +469,15 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(dt * 1e3 / args.steps, 5),
+        "ms_per_step": round(dt * 1e3 / args.steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (random-init N(0,0.02) weights, seeded prompt ids)",
         "config": {"workload": f"{name}-shaped greedy decode, hipGraph per token", "model_shape": list(cfg),
-                   "positions": f"0..{min(args.steps, S) - 1} (KV cache restarts every {S})",
-                   "batch": 1},
+                   "step": f"one full greedy decode of positions 0..{S - 1} (pt_generate over ids)",
+                   "positions": f"0..{S - 1}", "tokens_timed": n_tok, "batch": 1},
         "roofline": {"bound": "hbm", "kernel": f"decode[{dominant}]", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "bytes_per_launch": dom["bytes_per_launch"], "avg_us": dom["avg_us"]},

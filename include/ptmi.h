@@ -51,11 +51,18 @@ int         ptmi_sync(void);            /* wait for the stream         */
  * row-interleaved [w1|w3]); afterwards any host pointer into the blob's
  * weight tensors passed to ptmi_matvec resolves to its device copy.
  * Replaces: the Pi's weights-in-ARM-RAM read through the TMU bus alias
- * (pitorch/ops/matvec/matvec.c:13-30).                                 */
+ * (pitorch/ops/matvec/matvec.c:13-30).
+ * Registrations are counted holds on one device copy per blob address:
+ * each ptmi_register_weights call and each live ptmi_model over the blob
+ * holds it, and the copy is freed when the last hold ends.  Registering a
+ * blob whose size or 28-byte header differs from the registration still
+ * held at that address fails with PTMI_ERR_STATE.                       */
 int ptmi_register_weights(const void *blob, size_t bytes);
 /* Re-upload [ptr, ptr+bytes) of a registered blob after host writes
  * (pitorch/train/pt_train.c:870-896 mutates W in place).               */
 int ptmi_invalidate(const void *ptr, size_t bytes);
+/* End one ptmi_register_weights hold.  Refused (PTMI_ERR_STATE) while a
+ * model created over the blob is alive: destroy the models first.       */
 int ptmi_unregister_weights(const void *blob);
 
 /* ── matvec: y[out_dim] = W[out_dim, in_dim] . x[in_dim] ──────────────
@@ -73,6 +80,15 @@ int  ptmi_matvec_checked(const float *W, const float *x, float *y, int out_dim, 
  * synchronisation.  ld = row stride of W in floats (>= in_dim).        */
 int  ptmi_matvec_dev(const float *dW, long ld, const float *dx, float *dy,
                      int out_dim, int in_dim, void *stream);
+/* Ablation baseline, same arguments and result: the same kernel geometry,
+ * but every row pass re-reads its slice of x from memory instead of
+ * holding it in registers for the whole wave.  The counterpart of the
+ * reference's smatvec_tmu_no_packing (pitorch/ops/matvec/
+ * matvec_no_packing.c:1-10,25-85), which re-packs x for every dispatch
+ * and is kept there as the baseline of that design choice.  Needs
+ * in_dim % 4 == 0, in_dim <= 2304, 16-byte aligned rows.               */
+int  ptmi_matvec_dev_xreread(const float *dW, long ld, const float *dx, float *dy,
+                             int out_dim, int in_dim, void *stream);
 
 /* ── training GEMMs (fp32, MFMA) ──────────────────────────────────────
  * C[M,N] (+)= A[M,K] . B[K,N], all row-major.  Replaces sgemm_rect_tmu
@@ -81,12 +97,28 @@ int  ptmi_matvec_dev(const float *dW, long ld, const float *dx, float *dy,
  * Host pointers.                                                        */
 int ptmi_sgemm_rect(const float *A, const float *B, float *C,
                     int M, int K, int N, int accumulate);
+/* Exactly the signature of sgemm_rect_tmu (pitorch/ops/gemm/gemm_rect.h:
+ * 24-26): num_qpus selects nothing (the matrix cores need no worker
+ * count) but must lie in 1..12 as there (gemm_rect.c:34); no N%16
+ * constraint (:33).  Panics (stderr + abort) on error, as the
+ * reference's demand() does.                                            */
+void ptmi_sgemm_rect_tmu(const float *A, const float *B, float *C,
+                         int M, int K, int N, int num_qpus, int accumulate);
+/* Exactly the signature of sgemm_cpu (pitorch/ops/gemm/gemm.h:19-20):
+ * C[M,N] = A[M,K] . B[K,N] on the GPU.  Panics on error.               */
+void ptmi_sgemm_cpu(const float *A, const float *B, float *C, int M, int K, int N);
 /* dW[out,in] += sum_t dY[t,out] * X[t,in]  (TN GEMM, no host transpose).
- * Same arguments as matmul_backward_weight_batched
- * (pitorch/train/pt_train.c:475-477).  Host pointers.                   */
-int ptmi_matmul_backward_weight_batched(float *d_W, const float *d_y_all,
-                                        const float *x_all, int out_dim,
-                                        int in_dim, int T);
+ * Exactly the signature of matmul_backward_weight_batched
+ * (pitorch/train/pt_train.c:475-477, void); T = 1 is the rank-1
+ * matmul_backward_weight (pitorch/train/pt_backward_ops.c:43-49).
+ * Host pointers.  Panics on error.                                      */
+void ptmi_matmul_backward_weight_batched(float *d_W, const float *d_y_all,
+                                         const float *x_all, int out_dim,
+                                         int in_dim, int T);
+/* Same, returning a status instead of panicking. */
+int  ptmi_matmul_backward_weight_batched_checked(float *d_W, const float *d_y_all,
+                                                 const float *x_all, int out_dim,
+                                                 int in_dim, int T);
 /* dX[T,in] (+)= dY[T,out] . W[out,in]  (NN GEMM).  The batched form of
  * backward_input_pretrans/matmul_backward_input (pt_train.c:442-453,
  * pt_backward_ops.c:32-41) without the host transpose.  Host pointers. */
@@ -142,10 +174,12 @@ int  ptmi_model_train_step(ptmi_model_t *m, const int *tokens, int T, float lr,
 /* One device-timed span of a traced training step: the reference's trace
  * event (pitorch/profiler/trace.h:24-33, pt_trace_event_t) with times from
  * HIP events on the step's stream.  name/cat are static strings with the
- * reference's span names (pt.c:339-364, pt_train.c:171-866): train_step,
- * zero_grads, forward, embedding, layer, qkv, attention, wo, ffn,
- * classifier, loss, backward, weight_grads, sgd; layer = -1 outside the
- * layers; depth = nesting depth (train_step is 0).                      */
+ * reference's span tree (pt.c:339-364, pt_train.c:171-866): train_step,
+ * zero_grads, forward, embedding, layer, qkv, attention, ffn, classifier,
+ * loss, backward, cls_transpose, cls_weight_grad, transpose, wo, sgd,
+ * plus weight_grads (the layers' weight gradients in one launch, which
+ * the reference computes inside each layer's spans); layer = -1 outside
+ * the layers; depth = nesting depth (train_step is 0).                  */
 typedef struct {
     const char *name;
     const char *cat;        /* "train", "fwd", "bwd" */

@@ -27,3 +27,21 @@ float ref_train_step(pt_context_t *c, const int *tokens, int T, float lr) {
 }
 const float *ref_grads(pt_context_t *c, int *n) { *n = c->grads._n_params; return c->grads._mem; }
 const float *ref_train_logits(pt_context_t *c) { return c->acts.logits; }
+
+/* pt_train_step, then `after(blob, bytes)`: the reference-side binding of
+ * the drop-in for training.  pt_sgd_update (pitorch/train/pt_train.c:
+ * 870-896) rewrites the host weights in place, so a caller whose
+ * ctx->matvec serves resident device copies (ptmi_matvec) must re-upload
+ * them after every step: after = ptmi_invalidate. */
+typedef int (*ref_after_fn)(const void *, size_t);
+float ref_train_step_then(pt_context_t *c, const int *tokens, int T, float lr, ref_after_fn after,
+                          const void *blob, size_t bytes) {
+    float loss = pt_train_step(c, tokens, T, lr);
+    if (after) after(blob, bytes);
+    return loss;
+}
+
+/* The reference's trace (pitorch/pt.c:322-335, profiler/trace.c). */
+void ref_enable_trace(pt_context_t *c) { pt_enable_trace(c, NULL); }
+pt_trace_t *ref_trace(pt_context_t *c) { return c->trace; }
+size_t ref_trace_size(void) { return sizeof(pt_trace_t); }

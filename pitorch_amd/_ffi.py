@@ -59,8 +59,12 @@ def load_ptmi():
     _sig(L, "ptmi_matvec", None, [_vp, _vp, _vp, i, i])
     _sig(L, "ptmi_matvec_checked", i, [_vp, _vp, _vp, i, i])
     _sig(L, "ptmi_matvec_dev", i, [_vp, ctypes.c_long, _vp, _vp, i, i, _vp])
+    _sig(L, "ptmi_matvec_dev_xreread", i, [_vp, ctypes.c_long, _vp, _vp, i, i, _vp])
     _sig(L, "ptmi_sgemm_rect", i, [_vp, _vp, _vp, i, i, i, i])
-    _sig(L, "ptmi_matmul_backward_weight_batched", i, [_vp, _vp, _vp, i, i, i])
+    _sig(L, "ptmi_sgemm_rect_tmu", None, [_vp, _vp, _vp, i, i, i, i, i])
+    _sig(L, "ptmi_sgemm_cpu", None, [_vp, _vp, _vp, i, i, i])
+    _sig(L, "ptmi_matmul_backward_weight_batched", None, [_vp, _vp, _vp, i, i, i])
+    _sig(L, "ptmi_matmul_backward_weight_batched_checked", i, [_vp, _vp, _vp, i, i, i])
     _sig(L, "ptmi_matmul_backward_input_batched", i, [_vp, _vp, _vp, i, i, i, i])
     _sig(L, "ptmi_gemm_dev", i, [i, _vp, ctypes.c_long, _vp, ctypes.c_long, _vp, ctypes.c_long,
                                  i, i, i, i, _vp])
@@ -188,8 +192,8 @@ class Model:
 
     def close(self):
         if self.h:
+            # the model's hold on the blob's registration ends here
             self.L.ptmi_model_destroy(self.h)
-            self.L.ptmi_unregister_weights(_ptr(self.blob))
             self.h = None
 
     def __del__(self):

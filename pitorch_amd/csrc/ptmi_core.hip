@@ -65,6 +65,7 @@ int ensure_init() { return g.inited ? PTMI_OK : init_device(0); }
 
 hipStream_t lib_stream() { return g.stream; }
 
+
 float *scratch_buf(int slot, size_t floats) {
     if (slot < 0 || slot >= 4) return nullptr;
     if (floats <= g.scratch_cap[slot]) return g.scratch[slot];
@@ -184,17 +185,39 @@ int download_resident(Resident *r, void *blob, hipStream_t s) {
     return PTMI_OK;
 }
 
-Resident *register_blob(const void *blob, size_t bytes, int *status) {
+// A blob is looked up by its host address.  An existing registration is
+// shared only when the size and the 28-byte header are the ones it was
+// registered with; anything else at that address is an error (the caller
+// must release the old registration first), so a new blob at a reused
+// address never silently runs on another blob's device copy.
+Resident *register_blob(const void *blob, size_t bytes, bool explicit_hold, int *status) {
     *status = ensure_init();
     if (*status) return nullptr;
-    if (Resident *r = find_resident(blob)) {
-        if (r->blob == (const char *)blob) return r;
-        *status = set_error(PTMI_ERR_ARG, "blob overlaps an already registered blob");
+    if (!blob || bytes < 28) {
+        *status = set_error(PTMI_ERR_ARG, "blob too small for the 28-byte header");
         return nullptr;
+    }
+    if (Resident *r = find_resident(blob)) {
+        if (r->blob != (const char *)blob) {
+            *status = set_error(PTMI_ERR_ARG, "blob overlaps an already registered blob");
+            return nullptr;
+        }
+        if (r->bytes != bytes || memcmp(r->header, blob, sizeof(r->header)) != 0) {
+            *status = set_error(PTMI_ERR_STATE,
+                                "a different blob (%zu bytes) is still registered at %p: release it first",
+                                r->bytes, blob);
+            return nullptr;
+        }
+        if (explicit_hold) r->explicit_holds++;
+        else r->model_holds++;
+        return r;
     }
     Resident *r = new Resident();
     r->blob = (const char *)blob;
     r->bytes = bytes;
+    memcpy(r->header, blob, sizeof(r->header));
+    r->explicit_holds = explicit_hold ? 1 : 0;
+    r->model_holds = explicit_hold ? 0 : 1;
     if ((*status = parse_config(blob, bytes, &r->c))) { delete r; return nullptr; }
     host_offsets(r);
     if (28 + r->off_end * sizeof(float) > bytes) {
@@ -226,6 +249,24 @@ Resident *register_blob(const void *blob, size_t bytes, int *status) {
     }
     g.residents.push_back(r);
     return r;
+}
+
+static void free_resident(Resident *r) {
+    for (size_t i = 0; i < g.residents.size(); i++) {
+        if (g.residents[i] == r) {
+            g.residents.erase(g.residents.begin() + i);
+            break;
+        }
+    }
+    (void)hipStreamSynchronize(g.stream);
+    (void)hipFree(r->mem);
+    delete r;
+}
+
+void release_blob(Resident *r) {
+    if (!r) return;
+    if (r->model_holds > 0) r->model_holds--;
+    if (r->model_holds == 0 && r->explicit_holds == 0) free_resident(r);
 }
 
 // Map a host pointer W (row start inside a registered tensor) to the device
@@ -313,7 +354,7 @@ int ptmi_sync(void) {
 
 int ptmi_register_weights(const void *blob, size_t bytes) {
     int st = PTMI_OK;
-    register_blob(blob, bytes, &st);
+    register_blob(blob, bytes, true, &st);
     return st;
 }
 
@@ -329,15 +370,15 @@ int ptmi_invalidate(const void *ptr, size_t bytes) {
 }
 
 int ptmi_unregister_weights(const void *blob) {
-    for (size_t i = 0; i < g.residents.size(); i++) {
-        Resident *r = g.residents[i];
-        if (r->blob == (const char *)blob) {
-            (void)hipStreamSynchronize(g.stream);
-            (void)hipFree(r->mem);
-            delete r;
-            g.residents.erase(g.residents.begin() + i);
-            return PTMI_OK;
-        }
+    for (Resident *r : g.residents) {
+        if (r->blob != (const char *)blob) continue;
+        if (r->model_holds > 0)
+            return set_error(PTMI_ERR_STATE, "blob %p is still used by %d model(s): destroy them first", blob,
+                             r->model_holds);
+        if (r->explicit_holds == 0)
+            return set_error(PTMI_ERR_STATE, "blob %p has no ptmi_register_weights registration", blob);
+        if (--r->explicit_holds == 0) free_resident(r);
+        return PTMI_OK;
     }
     return set_error(PTMI_ERR_ARG, "blob %p is not registered", blob);
 }
@@ -350,6 +391,16 @@ int ptmi_matvec_dev(const float *dW, long ld, const float *dx, float *dy, int ou
     p.W = dW; p.ld = ld; p.rows = out_dim; p.n = in_dim; p.x = dx; p.y = dy;
     p.pro = PRO_NONE; p.epi = EPI_STORE;
     return launch_matvec(p, stream ? (hipStream_t)stream : g.stream);
+}
+
+int ptmi_matvec_dev_xreread(const float *dW, long ld, const float *dx, float *dy, int out_dim, int in_dim,
+                            void *stream) {
+    int st = ensure_init();
+    if (st) return st;
+    MatvecParams p = {};
+    p.W = dW; p.ld = ld; p.rows = out_dim; p.n = in_dim; p.x = dx; p.y = dy;
+    p.pro = PRO_NONE; p.epi = EPI_STORE;
+    return launch_matvec(p, stream ? (hipStream_t)stream : g.stream, nullptr, nullptr, true);
 }
 
 int ptmi_matvec_checked(const float *W, const float *x, float *y, int out_dim, int in_dim) {

@@ -475,14 +475,23 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
     if (!out) return set_error(PTMI_ERR_ARG, "ptmi_model_create: out is NULL");
     *out = nullptr;
     int st = PTMI_OK;
-    Resident *r = register_blob(blob, bytes, &st);
+    // The model holds the blob's registration until ptmi_model_destroy;
+    // every failure below releases it again.
+    Resident *r = register_blob(blob, bytes, false, &st);
     if (!r) return st;
     const Config &c = r->c;
     if (c.dim % 4 || c.hidden % 4 || c.head_dim % 4 || c.head_dim > kMaxHeadDim || c.seq_len > kMaxSeqLen ||
-        c.dim > kMaxCombineDim)
-        return set_error(PTMI_ERR_ARG, "unsupported shape: dim=%d hidden=%d head_dim=%d", c.dim, c.hidden,
-                         c.head_dim);
-    if (max_T < 0 || max_T > c.seq_len) return set_error(PTMI_ERR_ARG, "max_T=%d outside [0, seq_len]", max_T);
+        c.dim > kMaxCombineDim) {
+        st = set_error(PTMI_ERR_ARG, "unsupported shape: dim=%d hidden=%d head_dim=%d", c.dim, c.hidden,
+                       c.head_dim);
+        release_blob(r);
+        return st;
+    }
+    if (max_T < 0 || max_T > c.seq_len) {
+        st = set_error(PTMI_ERR_ARG, "max_T=%d outside [0, seq_len]", max_T);
+        release_blob(r);
+        return st;
+    }
     ptmi_model *m = new ptmi_model();
     m->res = r;
     m->c = c;
@@ -502,7 +511,12 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
     const size_t ints = align_up(sizeof(DecodeCtl) / 4, 64) + 2 * align_up(S, 64) + 64;
     total += ints;
     hipError_t e = hipMalloc(&m->mem, total * sizeof(float));
-    if (e != hipSuccess) { delete m; return hip_check(e, "hipMalloc(decode state)"); }
+    if (e != hipSuccess) {
+        st = hip_check(e, "hipMalloc(decode state)");
+        delete m;
+        release_blob(r);
+        return st;
+    }
     size_t o = 0;
     for (int i = 0; i < 9; i++) { *dst[i] = m->mem + o; o += align_up(sizes[i], 64); }
     m->ctl = (DecodeCtl *)(m->mem + o); o += align_up(sizeof(DecodeCtl) / 4, 64);
@@ -512,17 +526,24 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
     hipStream_t s = lib_stream();
     e = hipMemsetAsync(m->mem, 0, total * sizeof(float), s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e != hipSuccess) { (void)hipFree(m->mem); delete m; return hip_check(e, "zero decode state"); }
+    if (e != hipSuccess) {
+        st = hip_check(e, "zero decode state");
+        (void)hipFree(m->mem);
+        delete m;
+        release_blob(r);
+        return st;
+    }
     const char *eager = getenv("PTMI_DECODE_EAGER");
     m->eager = eager && eager[0] == '1';
     const char *nopf = getenv("PTMI_NO_PREFETCH");
     m->prefetch = !(nopf && nopf[0] == '1');
-    if (!m->eager && (st = build_graph(m))) { (void)hipFree(m->mem); delete m; return st; }
-    if (max_T > 0 && (st = train_create(m))) {
+    if ((!m->eager && (st = build_graph(m))) || (max_T > 0 && (st = train_create(m)))) {
+        train_destroy(m);
         if (m->exec) (void)hipGraphExecDestroy(m->exec);
         if (m->graph) (void)hipGraphDestroy(m->graph);
         (void)hipFree(m->mem);
         delete m;
+        release_blob(r);
         return st;
     }
     *out = m;
@@ -536,6 +557,7 @@ void ptmi_model_destroy(ptmi_model_t *m) {
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
     if (m->graph) (void)hipGraphDestroy(m->graph);
     (void)hipFree(m->mem);
+    release_blob(m->res);
     delete m;
 }
 

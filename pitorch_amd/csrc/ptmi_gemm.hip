@@ -20,6 +20,8 @@
 #include "ptmi_internal.h"
 
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 
 namespace ptmi {
 
@@ -333,12 +335,15 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 
 // Grouped TN GEMMs (32x32 tiles, whole K): block b runs tile
 // t = xcd_tile(b) - d.tile0 of the descriptor d whose tile range holds it;
-// tiles run along N first, so neighbours share the A^T tile.
+// tiles run along N first, so neighbours share the A^T tile.  The launch
+// covers entries [i0, i1) of the table, whose tiles start at d[i0].tile0 (a
+// tile's result does not depend on the block that computes it, so a launch
+// of a sub-range gives the same bits as the whole table).
 template <int TM, int TN, bool VEC>
-__global__ __launch_bounds__(256) void k_gemm_tn_group(const GemmGroupDesc *d, int n) {
-    const int b = xcd_tile(blockIdx.x, gridDim.x);
-    int i = 0;
-    while (i + 1 < n && d[i + 1].tile0 <= b) i++;
+__global__ __launch_bounds__(256) void k_gemm_tn_group(const GemmGroupDesc *d, int i0, int i1) {
+    const int b = d[i0].tile0 + xcd_tile(blockIdx.x, gridDim.x);
+    int i = i0;
+    while (i + 1 < i1 && d[i + 1].tile0 <= b) i++;
     const GemmGroupDesc &e = d[i];
     const int t = b - e.tile0;
     gemm_tile<true, false, TM, TN, kRing32, VEC>(e.g, (t / e.tiles_n) * TM, (t % e.tiles_n) * TN, 0);
@@ -357,7 +362,33 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *partial, int
 
 inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+bool gemm_big_tiles(int op, int M, int N, int K) { return K >= 4096 || (op == 2 && (long)M * N >= (4L << 20)); }
+
+// How launch_gemm splits K: `chosen` splits fit the workspace, then K is
+// cut into whole K steps per split, which gives `splits` (<= chosen).
+struct SplitPlan { int chosen, splits, k_per_split; };
+SplitPlan split_plan(int op, int M, int N, int K, size_t ws_floats, int ek) {
+    if (ek != GEMM_EPI_NONE) return SplitPlan{1, 1, K};          // the epilogue needs whole-K sums
+    const bool big = gemm_big_tiles(op, M, N, K);
+    const int T = big ? 64 : 32;
+    const long blocks = (long)((N + T - 1) / T) * ((M + T - 1) / T);
+    const int nk = (K + BK - 1) / BK;
+    int splits = 1;
+    if (big && K >= 4096 && blocks < 512) splits = (int)std::min<long>((1024 + blocks - 1) / blocks, nk / 8);
+    else if (!big && blocks < 128 && nk > 9) splits = std::min(8, nk / 6);
+    while (splits > 1 && (size_t)splits * M * N > ws_floats) splits--;
+    const int chosen = std::max(1, splits);
+    const int kps = ((K + chosen - 1) / chosen + BK - 1) / BK * BK;
+    return SplitPlan{chosen, (K + kps - 1) / kps, kps};
+}
+
 }  // namespace
+
+size_t gemm_workspace_floats(int op, int M, int N, int K, size_t ws_floats) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    const SplitPlan p = split_plan(op, M, N, K, ws_floats, GEMM_EPI_NONE);
+    return p.chosen > 1 ? (size_t)p.chosen * M * N : 0;
+}
 
 // Launch op(A).op(B) with shapes validated; `ws` (optional) is a split-K
 // workspace of ws_floats floats.
@@ -392,18 +423,12 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
     // elements: 64x64).  Every small GEMM is bound by the latency of its K
     // steps, so K is split when a 32x32 grid is small and K long: about six
     // K steps per split (K=768: 4 splits, 9.3 vs 14.6 us; K=1536: 8 splits).
-    const bool big = K >= 4096 || (op == 2 && (long)M * N >= (4L << 20));
+    const bool big = gemm_big_tiles(op, M, N, K);
     const int TM = big ? 64 : 32, TN = TM;
     const int gx = (N + TN - 1) / TN, gy = (M + TM - 1) / TM;
-    const long blocks = (long)gx * gy;
-    const int nk = (K + BK - 1) / BK;
-    int splits = 1;
-    if (big && K >= 4096 && blocks < 512) splits = (int)std::min<long>((1024 + blocks - 1) / blocks, nk / 8);
-    else if (!big && blocks < 128 && nk > 9) splits = std::min(8, nk / 6);
-    while (splits > 1 && (size_t)splits * M * N > ws_floats) splits--;
-    g.k_per_split = ((K + splits - 1) / splits + BK - 1) / BK * BK;
-    splits = (K + g.k_per_split - 1) / g.k_per_split;
-    if (ek != GEMM_EPI_NONE) splits = 1, g.k_per_split = K;      // the epilogue needs whole-K sums
+    const SplitPlan plan = split_plan(op, M, N, K, ws_floats, ek);
+    int splits = plan.splits;
+    g.k_per_split = plan.k_per_split;
     g.partial = splits > 1 ? ws : nullptr;
     g.epi = epi ? *epi : GemmEpi{};
     if (gy > 65535) return set_error(PTMI_ERR_ARG, "gemm: M too large");
@@ -471,10 +496,10 @@ int gemm_tn_group_prepare(const TnGemm *list, int n, const float *lr, void *host
     return PTMI_OK;
 }
 
-int launch_gemm_tn_group(const void *dev_desc, int n, int tiles_total, int vec, hipStream_t s) {
-    if (n <= 0 || tiles_total <= 0) return PTMI_OK;
-    void (*fn)(const GemmGroupDesc *, int) = vec ? k_gemm_tn_group<32, 32, true> : k_gemm_tn_group<32, 32, false>;
-    hipLaunchKernelGGL(fn, dim3((unsigned)tiles_total), dim3(256), 0, s, static_cast<const GemmGroupDesc *>(dev_desc), n);
+int launch_gemm_tn_group(const void *dev_desc, int i0, int i1, int tiles, int vec, hipStream_t s) {
+    if (i1 <= i0 || tiles <= 0) return PTMI_OK;
+    void (*fn)(const GemmGroupDesc *, int, int) = vec ? k_gemm_tn_group<32, 32, true> : k_gemm_tn_group<32, 32, false>;
+    hipLaunchKernelGGL(fn, dim3((unsigned)tiles), dim3(256), 0, s, static_cast<const GemmGroupDesc *>(dev_desc), i0, i1);
     PTMI_HIP(hipGetLastError());
     return PTMI_OK;
 }
@@ -509,13 +534,24 @@ int host_gemm(int op, const float *A, size_t a_n, long lda, const float *B, size
 
 }  // namespace
 
+namespace ptmi {
+
+// Split-K workspace of ptmi_gemm_dev: up to 64 partial products, at most
+// 256 MiB.
+size_t gemm_dev_ws_floats(int M, int N) {
+    if (M <= 0 || N <= 0) return 0;
+    return std::min<size_t>((size_t)M * N * 64, (size_t)64 << 20);
+}
+
+}  // namespace ptmi
+
 extern "C" {
 
 int ptmi_gemm_dev(int op, const float *dA, long lda, const float *dB, long ldb, float *dC, long ldc, int M, int N,
                   int K, int accumulate, void *stream) {
     int st = ensure_init();
     if (st) return st;
-    const size_t ws_n = std::min<size_t>((size_t)M * N * 64, (size_t)64 << 20);
+    const size_t ws_n = gemm_dev_ws_floats(M, N);
     float *ws = scratch_buf(3, ws_n);
     if (!ws) return ptmi_last_status();
     return launch_gemm(op, dA, lda, dB, ldb, dC, ldc, M, N, K, accumulate, ws, ws_n,
@@ -528,8 +564,8 @@ int ptmi_sgemm_rect(const float *A, const float *B, float *C, int M, int K, int 
     return host_gemm(0, A, (size_t)M * K, K, B, (size_t)K * N, N, C, M, N, K, accumulate);
 }
 
-int ptmi_matmul_backward_weight_batched(float *d_W, const float *d_y_all, const float *x_all, int out_dim, int in_dim,
-                                        int T) {
+int ptmi_matmul_backward_weight_batched_checked(float *d_W, const float *d_y_all, const float *x_all, int out_dim,
+                                                int in_dim, int T) {
     if (!d_W || !d_y_all || !x_all || out_dim <= 0 || in_dim <= 0 || T < 0)
         return set_error(PTMI_ERR_ARG, "ptmi_matmul_backward_weight_batched: bad arguments");
     if (T == 0) return PTMI_OK;
@@ -546,6 +582,33 @@ int ptmi_matmul_backward_input_batched(float *d_x_all, const float *W, const flo
     // dX[T,in] (+)= dY[T,out] . W[out,in]   (NN)
     return host_gemm(0, d_y_all, (size_t)T * out_dim, out_dim, W, (size_t)out_dim * in_dim, in_dim, d_x_all, T, in_dim,
                      out_dim, accumulate);
+}
+
+// The reference's void entries report failure by panicking
+// (libpi/libc/demand.h:20-60): message on stderr, then abort().
+static void panic_on(int st, const char *what) {
+    if (st == PTMI_OK) return;
+    fprintf(stderr, "%s: %s\n", what, ptmi_last_error());
+    abort();
+}
+
+void ptmi_sgemm_rect_tmu(const float *A, const float *B, float *C, int M, int K, int N, int num_qpus,
+                         int accumulate) {
+    // num_qpus selects no resource here, but keeps the reference's range
+    // check (gemm_rect.c:34: 1..12); N needs no multiple of 16 (:33).
+    if (num_qpus < 1 || num_qpus > 12)
+        panic_on(set_error(PTMI_ERR_ARG, "num_qpus %d outside 1..12", num_qpus), "ptmi_sgemm_rect_tmu");
+    panic_on(ptmi_sgemm_rect(A, B, C, M, K, N, accumulate), "ptmi_sgemm_rect_tmu");
+}
+
+void ptmi_sgemm_cpu(const float *A, const float *B, float *C, int M, int K, int N) {
+    panic_on(ptmi_sgemm_rect(A, B, C, M, K, N, 0), "ptmi_sgemm_cpu");
+}
+
+void ptmi_matmul_backward_weight_batched(float *d_W, const float *d_y_all, const float *x_all, int out_dim,
+                                         int in_dim, int T) {
+    panic_on(ptmi_matmul_backward_weight_batched_checked(d_W, d_y_all, x_all, out_dim, in_dim, T),
+             "ptmi_matmul_backward_weight_batched");
 }
 
 }  // extern "C"

@@ -285,7 +285,9 @@ inline void launch_k(F f, dim3 g, dim3 b, size_t shmem, hipStream_t s, hipEvent_
 }
 
 // Launch y = epilogue(W . prologue(x)); validates shapes, picks a kernel.
-int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
+// x_reread: the ablation kernel that re-reads x for every row pass.
+int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr,
+                  bool x_reread = false);
 
 // Split-K partial sums left in the workspace for the next kernel to add up
 // (dense [splits][M][N]; C = (Cin +) sum over z ascending of parts[z]).
@@ -340,6 +342,10 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
                 int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s, const float *Cin = nullptr,
                 SplitK *defer = nullptr, const GemmEpi *epi = nullptr);
 
+// Workspace floats launch_gemm needs to split this GEMM's K the way it does
+// with a workspace of ws_floats floats (0: no split).
+size_t gemm_workspace_floats(int op, int M, int N, int K, size_t ws_floats);
+
 // Grouped C[M,N] = A^T.B GEMMs (TN; A stored [K][M]; C written, not
 // accumulated), one launch of 32x32 tiles over all of them.  prepare fills host_desc (gemm_group_desc_bytes(n)
 // bytes); the caller copies it to device memory for the launch.
@@ -357,7 +363,8 @@ struct TnGemm {
 };
 size_t gemm_group_desc_bytes(int n);
 int gemm_tn_group_prepare(const TnGemm *list, int n, const float *lr, void *host_desc, int *tiles_total, int *vec);
-int launch_gemm_tn_group(const void *dev_desc, int n, int tiles_total, int vec, hipStream_t s);
+// Entries [i0, i1) of a prepared table, whose tiles number `tiles`.
+int launch_gemm_tn_group(const void *dev_desc, int i0, int i1, int tiles, int vec, hipStream_t s);
 
 // ── library state ───────────────────────────────────────────────────────
 struct Config {
@@ -369,6 +376,9 @@ struct Config {
 struct Resident {
     const char *blob;          // host blob (header included)
     size_t bytes;
+    int32_t header[7];         // the 28-byte header as registered
+    int explicit_holds;        // ptmi_register_weights calls not yet unregistered
+    int model_holds;           // live models created over this blob
     Config c;
     float *mem;                // one allocation for all tensors
     size_t mem_floats;
@@ -381,9 +391,14 @@ struct Resident {
 int  set_error(int status, const char *fmt, ...);
 int  ensure_init();
 hipStream_t lib_stream();
+
 int  hip_check(hipError_t e, const char *what);
 Resident *find_resident(const void *p);
-Resident *register_blob(const void *blob, size_t bytes, int *status);
+// Registration holds: register_blob takes one (explicit = ptmi_register_weights,
+// else a model's), release_blob drops a model's; the device copy is freed
+// when no hold is left.
+Resident *register_blob(const void *blob, size_t bytes, bool explicit_hold, int *status);
+void release_blob(Resident *r);
 int  upload_resident(Resident *r, hipStream_t s);   // host blob -> device layout
 int  download_resident(Resident *r, void *blob, hipStream_t s);
 int  parse_config(const void *blob, size_t bytes, Config *c);

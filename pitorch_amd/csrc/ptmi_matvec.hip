@@ -88,8 +88,14 @@ __device__ __forceinline__ void run_epilogue(const MatvecParams &p, const float 
 // NP passes of 64/LPR rows loaded together.  IT = ceil(n/4 / LPR), so only
 // the last chunk can run past the row: its address is clamped into the row
 // and its value replaced by 0, which keeps every load unconditional.
-template <int LPR, int IT, int NP, int PRO, int EPI>
+//
+// XR (ablation, plain y = Wx only): x is re-read from memory for every row
+// pass instead of once per wave — the MI355X counterpart of the reference's
+// smatvec_tmu_no_packing baseline (pitorch/ops/matvec/matvec_no_packing.c:
+// 1-10), which re-packs x for every dispatch.
+template <int LPR, int IT, int NP, int PRO, int EPI, bool XR = false>
 __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
+    static_assert(!XR || (PRO == PRO_NONE && EPI == EPI_STORE), "the x re-read ablation is a plain matvec");
     constexpr int RPP = 64 / LPR;                  // rows per pass
     constexpr bool kNorm = PRO == PRO_RMSNORM || PRO == PRO_EMBED_RMSNORM;
     __shared__ float ybuf[kWaves][kMaxRowsPerWave];
@@ -205,7 +211,7 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
     load_rows(0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (PRO == PRO_EMBED_RMSNORM) load_x(p.x + (long)(*p.token) * p.n);
-    if constexpr (PRO == PRO_NONE && !kXFirst) load_x(p.x);
+    if constexpr (PRO == PRO_NONE && !kXFirst && !XR) load_x(p.x);
     // The residual this wave's epilogue adds to (its rows only).
     float res = 0.0f;
     if constexpr (EPI == EPI_RESIDUAL) {
@@ -266,7 +272,7 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
     // The last chunk past the row contributes 0 (x and w both zeroed, so
     // a non-finite weight read through the clamped address cannot leak in).
     const bool tail_in = sub + (IT - 1) * LPR < n4;
-    xr[IT - 1] = sel4(tail_in, xr[IT - 1]);
+    if constexpr (!XR) xr[IT - 1] = sel4(tail_in, xr[IT - 1]);
     if (PRO == PRO_EMBED_RMSNORM && blockIdx.x == 0 && wave == 0 && slot == 0) {
 #pragma unroll
         for (int it = 0; it < IT; it++) {
@@ -292,6 +298,13 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
 
     for (int base = 0; base < nrows; base += kIterRows) {
         if (base > 0) load_rows(base);
+        if constexpr (XR) {
+            // a fresh read of x for this pass's rows; the barrier keeps the
+            // compiler from hoisting the loop-invariant loads out of the loop
+            asm volatile("" ::: "memory");
+            load_x(p.x);
+            xr[IT - 1] = sel4(tail_in, xr[IT - 1]);
+        }
 #pragma unroll
         for (int q = 0; q < NP; q++) {
             float acc = 0.0f;
@@ -391,6 +404,27 @@ KernelFn pick_role(int it, int pro, int epi) {
 template <int LPR>
 KernelFn pick(int it, int np, int pro, int epi) {
     return np == 2 ? pick_role<LPR, 2>(it, pro, epi) : pick_role<LPR, 1>(it, pro, epi);
+}
+
+template <int LPR, int NP>
+KernelFn pick_xr_np(int it) {
+    switch (it) {
+    case 1: return k_matvec<LPR, 1, NP, PRO_NONE, EPI_STORE, true>;
+    case 2: return k_matvec<LPR, 2, NP, PRO_NONE, EPI_STORE, true>;
+    case 3: return k_matvec<LPR, 3, NP, PRO_NONE, EPI_STORE, true>;
+    case 4: return k_matvec<LPR, 4, NP, PRO_NONE, EPI_STORE, true>;
+    case 5: return k_matvec<LPR, 5, NP, PRO_NONE, EPI_STORE, true>;
+    case 6: return k_matvec<LPR, 6, NP, PRO_NONE, EPI_STORE, true>;
+    case 7: return k_matvec<LPR, 7, NP, PRO_NONE, EPI_STORE, true>;
+    case 8: return k_matvec<LPR, 8, NP, PRO_NONE, EPI_STORE, true>;
+    case 9: return k_matvec<LPR, 9, NP, PRO_NONE, EPI_STORE, true>;
+    default: return nullptr;
+    }
+}
+
+template <int LPR>
+KernelFn pick_xr(int it, int np) {
+    return np == 2 ? pick_xr_np<LPR, 2>(it) : pick_xr_np<LPR, 1>(it);
 }
 
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
@@ -521,7 +555,7 @@ PrefetchDesc prefetch_for(const float *W, long ld, int rows, int n, int pro, int
 }
 
 // Host-side launcher: validates shapes and picks the kernel.
-int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0, hipEvent_t e1, bool x_reread) {
     if (p.rows <= 0 || p.n <= 0) return set_error(PTMI_ERR_ARG, "matvec: rows=%d n=%d", p.rows, p.n);
     if (!p.W || !p.x || !p.y) return set_error(PTMI_ERR_ARG, "matvec: null pointer");
     if (p.ld < p.n) return set_error(PTMI_ERR_ARG, "matvec: ld=%ld < n=%d", p.ld, p.n);
@@ -547,12 +581,23 @@ int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     KernelFn fn = nullptr;
     int rpp = 1;
     MatvecGeom geo;
+    if (x_reread && (p.pro != PRO_NONE || p.epi != EPI_STORE || p.pf.blocks))
+        return set_error(PTMI_ERR_ARG, "matvec: the x re-read variant is a plain y = Wx");
     if (vec_ok && matvec_geometry(p.rows, p.n, p.pro, p.epi, &geo)) {
-        switch (geo.lpr) {
-        case 8: fn = pick<8>(geo.it, geo.np, p.pro, p.epi); break;
-        case 16: fn = pick<16>(geo.it, geo.np, p.pro, p.epi); break;
-        case 32: fn = pick<32>(geo.it, geo.np, p.pro, p.epi); break;
-        default: fn = pick<64>(geo.it, geo.np, p.pro, p.epi); break;
+        if (x_reread) {
+            switch (geo.lpr) {
+            case 8: fn = pick_xr<8>(geo.it, geo.np); break;
+            case 16: fn = pick_xr<16>(geo.it, geo.np); break;
+            case 32: fn = pick_xr<32>(geo.it, geo.np); break;
+            default: fn = pick_xr<64>(geo.it, geo.np); break;
+            }
+        } else {
+            switch (geo.lpr) {
+            case 8: fn = pick<8>(geo.it, geo.np, p.pro, p.epi); break;
+            case 16: fn = pick<16>(geo.it, geo.np, p.pro, p.epi); break;
+            case 32: fn = pick<32>(geo.it, geo.np, p.pro, p.epi); break;
+            default: fn = pick<64>(geo.it, geo.np, p.pro, p.epi); break;
+            }
         }
         if (!fn) return set_error(PTMI_ERR_ARG, "matvec: unsupported prologue/epilogue pair %d/%d", p.pro, p.epi);
         p.stripe = geo.stripe;
@@ -565,6 +610,8 @@ int launch_matvec(MatvecParams p, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
         launch_k(fn, dim3((unsigned)(compute_blocks + p.pf.blocks)), dim3(geo.wpb * 64), 0, s, e0, e1, p);
         PTMI_HIP(hipGetLastError());
         return PTMI_OK;
+    } else if (x_reread) {
+        return set_error(PTMI_ERR_ARG, "matvec: the x re-read variant needs 16-byte rows of n <= %d", 64 * 9 * 4);
     } else if (vec_ok) {
         if (p.pf.blocks) return set_error(PTMI_ERR_ARG, "matvec: prefetch needs the register-resident kernel");
         if (p.pro != PRO_NONE || p.epi != EPI_STORE)

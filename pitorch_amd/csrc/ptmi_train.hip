@@ -38,7 +38,7 @@ struct TrainState {
     // Descriptor tables of the two grouped launches (device; built per T).
     void *dw_desc;
     float *nd_desc;
-    int desc_T = 0, dw_tiles = 0, n_dw = 0, dw_vec = 0;
+    int desc_T = 0, dw_tiles = 0, n_dw = 0, dw_vec = 0, dw_cls_tiles = 0;   // entry 0: the classifier
     float *ws;
     size_t ws_floats = 0;
     float *lr;                  // device copy of the step's learning rate
@@ -1246,6 +1246,7 @@ int train_descriptors(ptmi_model *m, int T) {
     PTMI_HIP(hipMemcpy(ts->nd_desc, nd.data(), nd.size() * sizeof(NormDw), hipMemcpyHostToDevice));
     ts->n_dw = (int)g.size();
     ts->dw_tiles = tiles;
+    ts->dw_cls_tiles = ((V + 31) / 32) * ((D + 31) / 32);
     ts->dw_vec = vec;
     ts->desc_T = T;
     return PTMI_OK;
@@ -1394,9 +1395,8 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr
         else
             hipLaunchKernelGGL(attn_fwd, dim3(T, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ao, T, D, QS, KV, hd,
                                kv_mul, scale);
-        SPAN_END();
-        // residual: rmid = rin + att_out . Wo^T
-        SPAN("wo", "fwd", l);
+        // residual: rmid = rin + att_out . Wo^T (inside the attention span,
+        // as pt_train.c:222-258 keeps the Wo matvecs)
         if ((st = gemm(s, ts, 2, ao, D, r->wo + (long)l * D * D, D, rmid, D, T, D, D, 1, rin))) return st;
         SPAN_END();
         SPAN("ffn", "fwd", l);
@@ -1453,9 +1453,23 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr
         v++;
     };
     SPAN("backward", "bwd", -1);                          // pt_backward, pt_train.c:549-866
-    SPAN("classifier", "bwd", -1);
+    SPAN("classifier", "bwd", -1);                        // pt_train.c:585-653
+    // The reference transposes Wcls on the host here (:590-594); the NN
+    // GEMM reads Wcls as stored, so the span is empty.
+    SPAN("cls_transpose", "bwd", -1);
+    SPAN_END();
     if ((st = gemm(s, ts, 0, ts->logits, V, r->wcls, D, dxb(0), D, R, D, V, 0, nullptr, &pk))) return st;
     norm_bwd(ts->res + L * TD, r->rms_final);
+    // Traced, the classifier's weight gradient (entry 0 of the grouped
+    // table, with its fused SGD step) runs here as its own launch, under
+    // cls_weight_grad (:644-652).  No later kernel of the step reads Wcls,
+    // and the tied embedding rows are still left to the embedding backward,
+    // so every value is the same as in the grouped launch.
+    if (tr) {
+        SPAN("cls_weight_grad", "bwd", -1);
+        if ((st = launch_gemm_tn_group(ts->dw_desc, 0, 1, ts->dw_cls_tiles, ts->dw_vec, s))) return st;
+        SPAN_END();
+    }
     SPAN_END();
     for (int l = L - 1; l >= 0; l--) {
         const float *rin = ts->res + l * TD, *rmid = ts->res_att + l * TD;
@@ -1469,6 +1483,9 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr
         // d_sh = d_res . W2, consumed in the GEMM's epilogue by the swiglu
         // backward: d_h13 (interleaved d_h1, d_h3) and shb = silu(h1)*h3
         SPAN("layer", "bwd", l);
+        // the reference's per-layer host transposes (:669-680): none here
+        SPAN("transpose", "bwd", l);
+        SPAN_END();
         SPAN("ffn", "bwd", l);
         GemmEpi sgb = {GEMM_EPI_SWIGLU_BWD, dh13, 2 * H, 0, 0, shb, H, h13, 2 * H};
         if ((st = gemm(s, ts, 0, dres(v), D, w2, H, ts->d_sh, H, R, H, D, 0, nullptr, nullptr, &sgb))) return st;
@@ -1506,10 +1523,17 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr
         SPAN_END();
     }
     PTMI_HIP(hipGetLastError());
-    // weight gradients: every TN GEMM in one launch, every RMSNorm dW in one
-    SPAN("weight_grads", "bwd", -1);
-    if ((st = launch_gemm_tn_group(ts->dw_desc, ts->n_dw, ts->dw_tiles, ts->dw_vec, s))) return st;
-    SPAN_END();
+    // weight gradients: every TN GEMM in one launch (traced: the layers'
+    // ones, under a span the reference does not have, since it computes
+    // each layer's dW inside that layer's spans), every RMSNorm dW in one
+    if (tr) {
+        SPAN("weight_grads", "bwd", -1);
+        if ((st = launch_gemm_tn_group(ts->dw_desc, 1, ts->n_dw, ts->dw_tiles - ts->dw_cls_tiles, ts->dw_vec, s)))
+            return st;
+        SPAN_END();
+    } else if ((st = launch_gemm_tn_group(ts->dw_desc, 0, ts->n_dw, ts->dw_tiles, ts->dw_vec, s))) {
+        return st;
+    }
     SPAN("embedding", "bwd", -1);
     // every RMSNorm dW, the embedding backward and the mean loss in one
     {

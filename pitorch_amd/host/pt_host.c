@@ -38,9 +38,9 @@ void pt_gpu_init(pt_context_t *ctx, void *weight_data, size_t bytes, int max_T) 
 }
 
 void pt_free(pt_context_t *ctx) {
+    /* the model's hold on the blob's device copy ends with it */
     if (ctx->dev) ptmi_model_destroy(ctx->dev);
     ctx->dev = NULL;
-    if (ctx->weight_data) ptmi_unregister_weights(ctx->weight_data);
     free(ctx->logits);
     ctx->logits = NULL;
     if (ctx->trace_owned) free(ctx->trace);

@@ -83,12 +83,40 @@ def ref():
         "ref_ctx_new": (vp, [vp, i]), "ref_ctx_free": (None, [vp]), "ref_set_matvec": (None, [vp, vp]),
         "ref_forward_step": (i, [vp, i]), "ref_reset_kv": (None, [vp]), "ref_logits": (fp, [vp]),
         "ref_train_step": (f, [vp, ip, i, f]), "ref_grads": (fp, [vp, ip]), "ref_train_logits": (fp, [vp]),
+        "ref_train_step_then": (f, [vp, ip, i, f, vp, vp, ctypes.c_size_t]),
+        "ref_enable_trace": (None, [vp]), "ref_trace": (vp, [vp]), "ref_trace_size": (ctypes.c_size_t, []),
+        "pt_trace_write_json": (None, [vp, ctypes.c_char_p]),
+        "pt_trace_write_meta": (None, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, i, i, i, ctypes.c_char_p,
+                                       i, i, f, f, f, ctypes.c_char_p]),
     }
     for n, (r, a) in sigs.items():
         getattr(L, n).restype = r
         getattr(L, n).argtypes = a
     _r = L
     return L
+
+
+class TraceEvent(ctypes.Structure):
+    """pt_trace_event_t (pitorch/profiler/trace.h:24-33)."""
+    _fields_ = [("name", ctypes.c_char_p), ("cat", ctypes.c_char_p), ("ts_us", ctypes.c_uint32),
+                ("dur_us", ctypes.c_uint32), ("layer", ctypes.c_int8), ("depth", ctypes.c_int8),
+                ("hw_cycles", ctypes.c_uint32), ("hw_stall", ctypes.c_uint32)]
+
+
+class TraceFrame(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("cat", ctypes.c_char_p), ("ts_us", ctypes.c_uint32),
+                ("layer", ctypes.c_int8)]
+
+
+class Trace(ctypes.Structure):
+    """pt_trace_t (pitorch/profiler/trace.h:35-48): 4096 events, a stack of 32."""
+    _fields_ = [("events", TraceEvent * 4096), ("count", ctypes.c_int), ("enabled", ctypes.c_int),
+                ("stack", TraceFrame * 32), ("depth", ctypes.c_int)]
+
+
+def trace_spans(tr):
+    """(name, cat, layer, depth) of every recorded event, in record order."""
+    return [(e.name.decode(), e.cat.decode(), int(e.layer), int(e.depth)) for e in tr.events[:tr.count]]
 
 
 def arr(ptr, n):

@@ -49,9 +49,58 @@ def test_backward_weight_batched_exact(out_dim, in_dim):
     dW = ints((out_dim, in_dim), 3)
     ref = dW.copy()
     L = pa.load_ptmi()
-    assert L.ptmi_matmul_backward_weight_batched(P(dW), P(dY), P(X), out_dim, in_dim, R) == 0
+    assert L.ptmi_matmul_backward_weight_batched_checked(P(dW), P(dY), P(X), out_dim, in_dim, R) == 0
     oracle().po_matmul_backward_weight_batched(P(ref), P(dY), P(X), out_dim, in_dim, R)
     assert np.array_equal(dW, ref)
+    # the void entry with the reference's exact signature (pt_train.c:475-477)
+    L.ptmi_matmul_backward_weight_batched(P(dW), P(dY), P(X), out_dim, in_dim, R)
+    oracle().po_matmul_backward_weight_batched(P(ref), P(dY), P(X), out_dim, in_dim, R)
+    assert np.array_equal(dW, ref)
+
+
+# T = 1: the rank-1 matmul_backward_weight (pitorch/train/pt_backward_ops.c:
+# 43-49), unit-tested by the reference at 32x16 (dev/tests/train/
+# test_backward_ops.c:86-105); also the config-5 projection shapes.
+@pytest.mark.parametrize("out_dim,in_dim", [(32, 16), (288, 288), (768, 288), (288, 768), (32000, 288), (5, 3)])
+def test_backward_weight_rank1_exact(out_dim, in_dim):
+    dy, x = ints(out_dim, 11), ints(in_dim, 12)
+    dW = ints((out_dim, in_dim), 13)
+    ref = dW.copy()
+    L = pa.load_ptmi()
+    L.ptmi_matmul_backward_weight_batched(P(dW), P(dy), P(x), out_dim, in_dim, 1)
+    oracle().po_matmul_backward_weight(P(ref), P(dy), P(x), out_dim, in_dim)
+    assert np.array_equal(dW, ref)
+
+
+# sgemm_rect_tmu's own call site (matmul_backward_weight_gpu,
+# pitorch/train/pt_train.c:536-543): C[V,D] += A[V,R] . X[R,D] with
+# M = 32000, K = R = 255, N = D = 288, accumulate = 1, num_qpus = 12; and
+# the rect shapes below, all integer-exact against the oracle's
+# sgemm_rect_tmu restatement.
+@pytest.mark.parametrize("M,K,N,acc", [(32000, 255, 288, 1), (255, 288, 288, 0), (255, 32000, 288, 1),
+                                       (300, 77, 130, 1), (1, 5, 3, 0), (100, 3001, 70, 1), (1000, 301, 900, 0)])
+def test_sgemm_rect_tmu_exact(M, K, N, acc):
+    A, B = ints((M, K), M + 1), ints((K, N), K + 2)
+    C = ints((M, N), N + 3) if acc else np.zeros((M, N), np.float32)
+    ref = C.copy()
+    L = pa.load_ptmi()
+    L.ptmi_sgemm_rect_tmu(P(A), P(B), P(C), M, K, N, 12, acc)
+    oracle().po_sgemm_rect(P(A), P(B), P(ref), M, K, N, acc)
+    assert np.array_equal(C, ref)
+
+
+@pytest.mark.parametrize("n", [16, 32])
+def test_sgemm_cpu_signature_exact(n):
+    """ptmi_sgemm_cpu: sgemm_cpu's signature (pitorch/ops/gemm/gemm.h:19-20),
+    at the reference's test sizes (dev/tests/gemm/test_gemm.c:82-83)."""
+    A = lcg_ints(n * n, 7, 16).reshape(n, n)
+    B = lcg_ints(n * n, 9, 16).reshape(n, n)
+    C = np.full((n, n), np.nan, np.float32)
+    L = pa.load_ptmi()
+    L.ptmi_sgemm_cpu(P(A), P(B), P(C), n, n, n)
+    ref = np.zeros((n, n), np.float32)
+    oracle().po_sgemm(P(A), P(B), P(ref), n, n, n)
+    assert np.array_equal(C, ref)
 
 
 @pytest.mark.parametrize("out_dim,in_dim", DX)

@@ -132,3 +132,43 @@ def test_device_pointer_entry_with_row_stride():
     check_close(dy.download(), oracle_mv(Wc, x), Wc, x)
     for a in (dW, dx, dy):
         a.free()
+
+
+def dev_matvec(entry, W, x):
+    """y = W x through a device-pointer entry (ptmi_matvec_dev or its x
+    re-read ablation), on the library stream."""
+    from pitorch_amd._hip import DeviceArray
+    L = pa.load_ptmi()
+    dW, dx = DeviceArray.from_host(np.ascontiguousarray(W)), DeviceArray.from_host(x)
+    dy = DeviceArray.from_host(np.full(W.shape[0], np.nan, np.float32))
+    assert getattr(L, entry)(dW.ptr, W.shape[1], dx.ptr, dy.ptr, W.shape[0], W.shape[1], None) == 0
+    assert L.ptmi_sync() == 0
+    y = dy.download()
+    for a in (dW, dx, dy):
+        a.free()
+    return y
+
+
+@pytest.mark.parametrize("d,n", SWEEP + [(48, 48), (37, 44), (16, 2304)])
+def test_x_reread_ablation_matches(d, n):
+    """The ablation kernel (x re-read per row pass, the counterpart of
+    smatvec_tmu_no_packing, pitorch/ops/matvec/matvec_no_packing.c:25-85)
+    is parity-held like the default: bit-exact on integer inputs, within
+    the tolerance on U(-1,1), and equal to the default kernel bit for bit
+    (same geometry, same per-row order)."""
+    Wi = np.random.default_rng(d + n).integers(1, 9, (d, n)).astype(np.float32)
+    xi = lcg_ints(n, 137)
+    assert np.array_equal(dev_matvec("ptmi_matvec_dev_xreread", Wi, xi), oracle_mv(Wi, xi))
+    W = pa.seed_uniform(1000 + d, d * n).reshape(d, n)
+    x = pa.seed_uniform(2000 + n, n)
+    y = dev_matvec("ptmi_matvec_dev_xreread", W, x)
+    check_close(y, oracle_mv(W, x), W, x)
+    assert np.array_equal(y, dev_matvec("ptmi_matvec_dev", W, x))
+
+
+def test_x_reread_ablation_rejects_long_rows():
+    from pitorch_amd._hip import DeviceArray
+    L = pa.load_ptmi()
+    a = DeviceArray(4 * 2400)
+    assert L.ptmi_matvec_dev_xreread(a.ptr, 2400, a.ptr, a.ptr, 2, 2400, None) == 1
+    a.free()

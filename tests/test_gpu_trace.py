@@ -4,9 +4,12 @@ pitorch/profiler/trace.c).
 
 * The traced step runs the same kernels (eagerly, behind a busy kernel): its loss and
   updated weights equal the untraced step's exactly.
-* Its spans carry the reference's names (pt.c:339-364, pt_train.c:171-866)
-  and nest: every span lies inside its parent, in the order trace.c
-  records them (children end first).
+* Its span sequence (name, cat, layer, depth, in the order trace.c records
+  them) is the reference's own traced pt_train_step's
+  (tests/golden/trace_spans.json, written from oracle/_ref), plus one span
+  the reference does not have: "weight_grads", the grouped launch of the
+  layers' weight gradients, which the reference computes inside each
+  layer's spans.  Every span lies inside its parent.
 * pt_demo (a C caller of pt.h) writes trace.json / meta.json as the
   reference's dev/host/test_train_profiled.c does.
 """
@@ -20,14 +23,22 @@ import pytest
 import pitorch_amd as pa
 
 pytestmark = pytest.mark.gpu
-CFG = (64, 160, 2, 4, 4, 512, 32)
-PER_LAYER = ["layer", "qkv", "attention", "wo", "ffn"]
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FX = json.load(open(os.path.join(ROOT, "tests", "golden", "trace_spans.json")))
+CFG = tuple(FX["config"])
+PER_LAYER = ["layer", "qkv", "attention", "wo", "ffn", "transpose"]
+EXTRA = ("weight_grads", "bwd", -1, 2)          # ours only, just before the backward "embedding"
+
+
+def expected_spans():
+    spans = [tuple(sp) for sp in FX["spans"]]
+    i = spans.index(("embedding", "bwd", -1, 2))
+    return spans[:i] + [EXTRA] + spans[i:]
 
 
 def expected_names(L):
-    top = ["train_step", "zero_grads", "forward", "embedding", "classifier", "loss", "backward", "classifier",
-           "weight_grads", "embedding", "sgd"]
-    return sorted(top + PER_LAYER * (2 * L))
+    assert L == CFG[2]
+    return sorted(sp[0] for sp in expected_spans())
 
 
 def check_nesting(spans, slack):
@@ -42,26 +53,25 @@ def check_nesting(spans, slack):
 
 
 def test_traced_step_equals_untraced_and_spans_nest():
-    blob = pa.synth_model(CFG, 31, 0.05)
-    tokens = pa.seed_tokens(32, 16, CFG[5])
-    a, b = pa.Model(blob.copy(), max_T=16), pa.Model(blob.copy(), max_T=16)
+    blob = pa.synth_model(CFG, FX["model_seed"], 0.05)
+    tokens = pa.seed_tokens(FX["token_seed"], FX["T"], CFG[5])
+    a, b = pa.Model(blob.copy(), max_T=FX["T"]), pa.Model(blob.copy(), max_T=FX["T"])
     for _ in range(2):
-        la, spans = a.train_step_trace(tokens, 0.05)
-        lb = b.train_step(tokens, 0.05)
+        la, spans = a.train_step_trace(tokens, FX["lr"])
+        lb = b.train_step(tokens, FX["lr"])
         assert la == lb
     assert np.array_equal(a.read_weights(), b.read_weights())
-    assert sorted(s["name"] for s in spans) == expected_names(CFG[2])
+    assert [(s["name"], s["cat"], s["layer"], s["depth"]) for s in spans] == expected_spans()
     assert spans[-1]["name"] == "train_step" and spans[-1]["depth"] == 0 and spans[-1]["start_us"] == 0.0
     check_nesting([dict(depth=s["depth"], start=s["start_us"], dur=s["dur_us"]) for s in spans], 1e-3)
     for s in spans:
         assert s["dur_us"] >= 0.0
-        if s["name"] in ("qkv", "attention", "wo", "ffn", "weight_grads", "loss"):
+        if s["name"] in ("qkv", "attention", "ffn", "weight_grads", "loss", "cls_weight_grad"):
             assert s["dur_us"] > 0.0, s
-        assert (s["layer"] >= 0) == (s["name"] in PER_LAYER)
     depth1 = sum(s["dur_us"] for s in spans if s["depth"] == 1)
     assert depth1 <= spans[-1]["dur_us"] + 1e-3
     with pytest.raises(pa.PtmiError):
-        a.train_step_trace(tokens, 0.05, max_spans=3)             # buffer smaller than the step's spans
+        a.train_step_trace(tokens, FX["lr"], max_spans=3)         # buffer smaller than the step's spans
     a.close()
     b.close()
 
@@ -80,7 +90,7 @@ def test_c_caller_writes_trace_json(tmp_path):
     assert bad.returncode != 0 and "could not write" in bad.stderr
     ev = json.load(open(out / "trace.json"))
     L = CFG[2]
-    assert len(ev) == 2 * (11 + 10 * L)
+    assert len(ev) == 2 * len(expected_spans())
     names = sorted(e["name"].split("_", 1)[1] if e["name"][0] == "L" and e["name"][1].isdigit() else e["name"]
                    for e in ev[: len(ev) // 2])
     assert names == expected_names(L)

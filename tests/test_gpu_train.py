@@ -168,3 +168,38 @@ def test_train_errors():
         m0.train_step(np.array([1, 2], np.int32), 0.1)
     assert "max_T" in str(e.value)
     m0.close()
+
+
+def test_reference_train_step_with_ptmi_matvec_dropin():
+    """The reference's own pt_train_step (pitorch/pt.c:339-364) with
+    ctx->matvec = ptmi_matvec and, after every step, ptmi_invalidate over
+    the blob (the reference-side binding: pt_sgd_update rewrites the host
+    weights in place, pt_train.c:870-896).  Every matvec of the forward and
+    of the backward's dX (incl. the host-transposed w_transpose views,
+    uploaded per call) runs on the GPU; losses track the all-CPU reference
+    within 1e-4 over 3 steps, and the updated weights within 1e-5."""
+    from tests._oracle import P, ref, ref_available
+    if not ref_available():
+        pytest.skip("oracle/_ref not built")
+    cfg, T, lr = (64, 160, 2, 4, 4, 1024, 32), 16, 0.05        # V >= 4*D + 3*H (pt_train.c:405-407)
+    blob = pa.synth_model(cfg, 41, 0.05)
+    cpu_blob, gpu_blob = blob.copy(), blob.copy()
+    tokens = pa.seed_tokens(42, T, cfg[5])
+    R, L = ref(), pa.load_ptmi()
+    assert L.ptmi_register_weights(P(gpu_blob), gpu_blob.nbytes) == 0
+    cpu, gpu = R.ref_ctx_new(P(cpu_blob), T), R.ref_ctx_new(P(gpu_blob), T)
+    R.ref_set_matvec(gpu, ctypes.cast(L.ptmi_matvec, ctypes.c_void_p))
+    inval = ctypes.cast(L.ptmi_invalidate, ctypes.c_void_p)
+    ip = ctypes.POINTER(ctypes.c_int)
+    try:
+        for _ in range(3):
+            la = R.ref_train_step(cpu, tokens.ctypes.data_as(ip), T, lr)
+            lb = R.ref_train_step_then(gpu, tokens.ctypes.data_as(ip), T, lr, inval, P(gpu_blob), gpu_blob.nbytes)
+            assert abs(la - lb) <= 1e-4, (la, lb)
+        w_cpu = np.frombuffer(cpu_blob.tobytes(), np.float32, offset=28)
+        w_gpu = np.frombuffer(gpu_blob.tobytes(), np.float32, offset=28)
+        assert np.max(np.abs(w_cpu - w_gpu)) <= 1e-5 * np.max(np.abs(w_cpu))
+    finally:
+        R.ref_ctx_free(cpu)
+        R.ref_ctx_free(gpu)
+        assert L.ptmi_unregister_weights(P(gpu_blob)) == 0

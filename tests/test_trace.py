@@ -67,3 +67,60 @@ def test_trace_layout_nesting_and_json(tmp_path):
     meta = json.load(open(tmp_path / "meta.json"))
     assert meta["dim"] == 288 and meta["layers"] == 6 and meta["steps"] == 18 and meta["device"] == "mi355x"
     assert abs(meta["final_loss"] - 10.25) < 1e-6 and meta["notes"] == "note"
+
+
+def _filled_trace():
+    """One event array covering every branch of trace.c's writer: layer -1
+    and >= 0 names, zero and non-zero V3D counters (the "args" object),
+    timestamps near the uint32 range."""
+    t = Trace()
+    rows = [(b"train_step", b"train", -1, 0, 10, 900, 0, 0), (b"qkv", b"fwd", 0, 2, 20, 35, 0, 0),
+            (b"attention", b"fwd", 11, 2, 55, 70, 1234, 0), (b"ffn", b"bwd", 3, 2, 4000000000, 5, 0, 77),
+            (b"cls_weight_grad", b"bwd", -1, 2, 4294967295, 0, 4294967295, 4294967295),
+            (b"sgd", b"train", -1, 1, 0, 0, 1, 1)]
+    for i, (n, c, layer, depth, ts, dur, cyc, stall) in enumerate(rows):
+        e = t.events[i]
+        e.name, e.cat, e.layer, e.depth, e.ts_us, e.dur_us, e.hw_cycles, e.hw_stall = n, c, layer, depth, ts, dur, cyc, stall
+    t.count = len(rows)
+    t.enabled = 1
+    return t
+
+
+def test_trace_writers_byte_identical_to_reference(tmp_path):
+    """pt_trace_write_json / pt_trace_write_meta of libpthost against the
+    reference's own trace.c (oracle/_ref), fed the same event array: the
+    files must be byte-identical (pitorch/profiler/trace.c:73-120)."""
+    import pytest
+    from tests._oracle import ref, ref_available
+    if not ref_available():
+        pytest.skip("oracle/_ref not built")
+    R, H = ref(), pa._ffi.load_host()
+    assert R.ref_trace_size() == H.pt_trace_size() == ctypes.sizeof(Trace)
+    t = _filled_trace()
+    a, b = tmp_path / "ours.json", tmp_path / "ref.json"
+    H.pt_trace_write_json(ctypes.byref(t), str(a).encode())
+    R.pt_trace_write_json(ctypes.byref(t), str(b).encode())
+    assert a.read_bytes() == b.read_bytes()
+    assert len(json.loads(a.read_text())) == t.count
+    for notes in (b"a note", None):
+        args = (b"run", b"stories110M", 768, 12, 32000, b"mi355x", 0, 18, 1e-3, 10.310569, 1.25, notes)
+        H.pt_trace_write_meta(str(a).encode(), *args)
+        R.pt_trace_write_meta(str(b).encode(), *args)
+        assert a.read_bytes() == b.read_bytes()
+
+
+def test_span_fixture_is_the_reference_traced_step():
+    """tests/golden/trace_spans.json is what the reference's own traced
+    pt_train_step records (regenerated here from oracle/_ref)."""
+    import os
+    import sys
+
+    import pytest
+    from tests._oracle import ref_available
+    if not ref_available():
+        pytest.skip("oracle/_ref not built")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, os.path.join(root, "tests", "golden"))
+    import make_golden
+    fx = json.load(open(os.path.join(root, "tests", "golden", "trace_spans.json")))
+    assert make_golden.trace() == fx
