@@ -132,6 +132,21 @@ int ptmi_matmul_backward_input_batched(float *d_x_all, const float *W,
 int ptmi_gemm_dev(int op, const float *dA, long lda, const float *dB, long ldb,
                   float *dC, long ldc, int M, int N, int K, int accumulate,
                   void *stream);
+/* ptmi_gemm_dev without any allocation.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, same kernels and the same bits as ptmi_gemm_dev; its
+ * split-K partial sums go to a fixed 16 MiB device scratch array that the
+ * library holds on each GPU for the life of the process, located once by
+ * ptmi_init (which must have been called: PTMI_ERR_STATE otherwise).  A
+ * GEMM whose K split needs more than 4 Mi floats of partials (splits*M*N)
+ * is rejected with PTMI_ERR_ARG before anything is enqueued.  Every call
+ * on a GPU shares that GPU's scratch: calls that can overlap on one GPU
+ * (other streams, other threads) race.  Nothing needs clearing between
+ * calls: each launch writes every partial it later reads.              */
+int ptmi_gemm_dev_noalloc(int op, const float *dA, long lda, const float *dB, long ldb,
+                          float *dC, long ldc, int M, int N, int K, int accumulate,
+                          void *stream);
 
 /* ── device-resident model (decode + training) ────────────────────────
  * One registered blob plus device state: KV cache, activations and, when

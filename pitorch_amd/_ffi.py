@@ -68,6 +68,8 @@ def load_ptmi():
     _sig(L, "ptmi_matmul_backward_input_batched", i, [_vp, _vp, _vp, i, i, i, i])
     _sig(L, "ptmi_gemm_dev", i, [i, _vp, ctypes.c_long, _vp, ctypes.c_long, _vp, ctypes.c_long,
                                  i, i, i, i, _vp])
+    _sig(L, "ptmi_gemm_dev_noalloc", i, [i, _vp, ctypes.c_long, _vp, ctypes.c_long, _vp, ctypes.c_long,
+                                         i, i, i, i, _vp])
     _sig(L, "ptmi_model_create", i, [_vp, sz, i, ctypes.POINTER(_vp)])
     _sig(L, "ptmi_model_destroy", None, [_vp])
     _sig(L, "ptmi_model_config", i, [_vp, _c_int_p])

@@ -55,6 +55,8 @@ static int init_device(int device) {
     if (e != hipSuccess || count == 0) return set_error(PTMI_ERR_NODEV, "no HIP device visible");
     if (device < 0 || device >= count) return set_error(PTMI_ERR_ARG, "device %d out of range (%d)", device, count);
     PTMI_HIP(hipSetDevice(device));
+    int st = gemm_scratch_setup(device);
+    if (st) return st;
     PTMI_HIP(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
     g.device = device;
     g.inited = true;
@@ -64,7 +66,8 @@ static int init_device(int device) {
 int ensure_init() { return g.inited ? PTMI_OK : init_device(0); }
 
 hipStream_t lib_stream() { return g.stream; }
-
+bool lib_initialised() { return g.inited; }
+int lib_device() { return g.device; }
 
 float *scratch_buf(int slot, size_t floats) {
     if (slot < 0 || slot >= 4) return nullptr;

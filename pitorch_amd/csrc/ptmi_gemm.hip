@@ -543,9 +543,50 @@ size_t gemm_dev_ws_floats(int M, int N) {
     return std::min<size_t>((size_t)M * N * 64, (size_t)64 << 20);
 }
 
+// ── the entry point that allocates nothing ───────────────────────────────
+// ptmi_gemm_dev_noalloc keeps its split-K partials in this file-scope
+// device array (16 MiB; each GPU the library runs on holds it until the
+// process ends).  In host code `scratch` names a host-side stand-in, not
+// device memory: the device address comes from hipGetSymbolAddress, once
+// per device at ptmi_init, and only that address is handed to kernels.
+constexpr size_t kNoAllocScratchFloats = (size_t)4 << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+static float *g_scratch_dev[kMaxDevices] = {};
+
+int gemm_scratch_setup(int device) {
+    if (device < 0 || device >= kMaxDevices)
+        return set_error(PTMI_ERR_ARG, "device %d: no GEMM scratch slot", device);
+    if (g_scratch_dev[device]) return PTMI_OK;
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_check(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return set_error(PTMI_ERR_HIP, "hipGetSymbolAddress(scratch) gave no address");
+    g_scratch_dev[device] = static_cast<float *>(p);
+    return PTMI_OK;
+}
+
 }  // namespace ptmi
 
 extern "C" {
+
+int ptmi_gemm_dev_noalloc(int op, const float *dA, long lda, const float *dB, long ldb, float *dC, long ldc, int M,
+                          int N, int K, int accumulate, void *stream) {
+    if (!lib_initialised())
+        return set_error(PTMI_ERR_STATE, "ptmi_gemm_dev_noalloc: call ptmi_init first (it locates the scratch)");
+    float *ws = g_scratch_dev[lib_device()];
+    if (!ws) return set_error(PTMI_ERR_STATE, "ptmi_gemm_dev_noalloc: no scratch on device %d", lib_device());
+    // The K split ptmi_gemm_dev would take must fit the fixed scratch, so
+    // both entries sum in the same order and give the same bits.
+    const size_t need = gemm_workspace_floats(op, M, N, K, gemm_dev_ws_floats(M, N));
+    if (need > kNoAllocScratchFloats)
+        return set_error(PTMI_ERR_ARG,
+                         "ptmi_gemm_dev_noalloc: %dx%dx%d needs %zu floats of split-K partials; the fixed scratch "
+                         "holds %zu",
+                         M, N, K, need, kNoAllocScratchFloats);
+    return launch_gemm(op, dA, lda, dB, ldb, dC, ldc, M, N, K, accumulate, ws, kNoAllocScratchFloats,
+                       stream ? (hipStream_t)stream : lib_stream());
+}
 
 int ptmi_gemm_dev(int op, const float *dA, long lda, const float *dB, long ldb, float *dC, long ldc, int M, int N,
                   int K, int accumulate, void *stream) {

@@ -391,7 +391,11 @@ struct Resident {
 int  set_error(int status, const char *fmt, ...);
 int  ensure_init();
 hipStream_t lib_stream();
-
+bool lib_initialised();
+int  lib_device();
+// Locates ptmi_gemm_dev_noalloc's fixed device scratch on `device` (the
+// current device); called once per device by ptmi_init.
+int  gemm_scratch_setup(int device);
 int  hip_check(hipError_t e, const char *what);
 Resident *find_resident(const void *p);
 // Registration holds: register_blob takes one (explicit = ptmi_register_weights,
