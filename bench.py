@@ -65,6 +65,7 @@ def role_bytes(cfg, positions):
         "w2": matvec_bytes(D, H),
         "classifier": matvec_bytes(V, D),
         "argmax": 4 * V,
+        "step": int(decode_bytes_per_token(cfg, positions)),
     }
 
 

@@ -178,10 +178,19 @@ int  ptmi_model_decode_async(ptmi_model_t *m, int first_token, int n_steps);
  * events around every launch, from the current position.  role_ms[i] is
  * the summed kernel time and role_launches[i] the launch count of role i:
  * 0 QKV matvec, 1 attention, 2 Wo matvec, 3 w1|w3 matvec, 4 w2 matvec,
- * 5 classifier matvec, 6 argmax.  Takes the place of the reference's
+ * 5 classifier matvec, 6 argmax; 7 the whole step when it runs as one
+ * kernel (then the only role).  Takes the place of the reference's
  * per-matvec V3D counters (pitorch/profiler/profiler.h:6-28).           */
 int  ptmi_model_profile(ptmi_model_t *m, int first_token, int n_steps,
-                        float role_ms[7], int role_launches[7]);
+                        float role_ms[8], int role_launches[8]);
+/* Stage timing of the one-kernel decode step, for a model created with
+ * PTMI_STEP_STAMPS=1 in the environment: for each of *n_wg workgroups,
+ * *n_stamps = 1 + 10*n_layers + 4 readings of the GPU's 100 MHz real-time
+ * counter taken by the LAST step: kernel start; per layer, the end of the
+ * wait and the end of the work of QKV, attention, Wo, w1|w3, w2; then the
+ * classifier's and the final argmax's.  0 where the workgroup had no
+ * part in a stage.  out holds n_wg * n_stamps words, workgroup-major.   */
+int  ptmi_model_step_stamps(ptmi_model_t *m, uint64_t *out, size_t n, int *n_stamps, int *n_wg);
 /* pt_train_step (pitorch/pt.c:339-364): zero grads, forward (loss),
  * backward, SGD on the device copy of the weights.                     */
 int  ptmi_model_train_step(ptmi_model_t *m, const int *tokens, int T, float lr,

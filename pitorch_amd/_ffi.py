@@ -80,6 +80,7 @@ def load_ptmi():
     _sig(L, "ptmi_model_generate", i, [_vp, _c_int_p, i, i, i, _c_int_p, _c_int_p])
     _sig(L, "ptmi_model_decode_async", i, [_vp, i, i])
     _sig(L, "ptmi_model_profile", i, [_vp, i, i, _c_float_p, _c_int_p])
+    _sig(L, "ptmi_model_step_stamps", i, [_vp, ctypes.POINTER(ctypes.c_uint64), sz, _c_int_p, _c_int_p])
     _sig(L, "ptmi_model_train_step", i, [_vp, _c_int_p, i, f, _c_float_p])
     _sig(L, "ptmi_model_train_step_trace", i,
          [_vp, _c_int_p, i, f, _c_float_p, ctypes.POINTER(Span), i, ctypes.POINTER(i)])
@@ -231,14 +232,25 @@ class Model:
     def decode_async(self, first_token, n_steps):
         check(self.L.ptmi_model_decode_async(self.h, int(first_token), int(n_steps)))
 
-    ROLES = ("qkv", "attention", "wo", "w13", "w2", "classifier", "argmax")
+    ROLES = ("qkv", "attention", "wo", "w13", "w2", "classifier", "argmax", "step")
 
     def profile(self, first_token, n_steps):
-        """Per-role (total ms, launches) over n_steps eager decode steps."""
-        ms = (ctypes.c_float * 7)()
-        cnt = (ctypes.c_int * 7)()
+        """Per-role (total ms, launches) over n_steps eager decode steps
+        ("step": the whole step as one kernel, when it runs that way)."""
+        ms = (ctypes.c_float * 8)()
+        cnt = (ctypes.c_int * 8)()
         check(self.L.ptmi_model_profile(self.h, int(first_token), int(n_steps), ms, cnt))
         return {r: (ms[i], cnt[i]) for i, r in enumerate(self.ROLES)}
+
+    def step_stamps(self):
+        """Stage stamps of the last one-kernel decode step (model created
+        with PTMI_STEP_STAMPS=1): uint64 array [workgroups][stamps]."""
+        ns, nw = ctypes.c_int(), ctypes.c_int()
+        self.L.ptmi_model_step_stamps(self.h, None, 0, ctypes.byref(ns), ctypes.byref(nw))
+        out = np.zeros((nw.value, ns.value), dtype=np.uint64)
+        check(self.L.ptmi_model_step_stamps(self.h, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)), out.size,
+                                            ctypes.byref(ns), ctypes.byref(nw)))
+        return out
 
     def train_step(self, tokens, lr):
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)

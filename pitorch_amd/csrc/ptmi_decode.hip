@@ -23,6 +23,19 @@
 
 namespace ptmi {
 
+// att_scale = 1/pt_sqrtf(head_dim) (llama2.c:137), evaluated on the host
+// with the reference's seed + 3 Newton steps (pt_math.c:92-102).
+float host_att_scale(int head_dim) {
+    const float x = (float)head_dim;
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    u = 0x1fbd1df5u + (u >> 1);
+    float y;
+    memcpy(&y, &u, 4);
+    for (int i = 0; i < 3; i++) y = 0.5f * (y + x / y);
+    return 1.0f / y;
+}
+
 namespace {
 
 struct AttnParams {
@@ -290,19 +303,6 @@ __global__ __launch_bounds__(1024) void k_argmax_step(const float *logits, int n
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// att_scale = 1/pt_sqrtf(head_dim) (llama2.c:137), evaluated on the host
-// with the reference's seed + 3 Newton steps (pt_math.c:92-102).
-float host_att_scale(int head_dim) {
-    const float x = (float)head_dim;
-    uint32_t u;
-    memcpy(&u, &x, 4);
-    u = 0x1fbd1df5u + (u >> 1);
-    float y;
-    memcpy(&y, &u, 4);
-    for (int i = 0; i < 3; i++) y = 0.5f * (y + x / y);
-    return 1.0f / y;
-}
-
 // Optional per-launch HIP events (eager profiling runs only): each launch
 // gets a start/stop pair timestamped by the command processor around the
 // kernel itself (hipExtLaunchKernelGGL), i.e. the kernel's own duration.
@@ -356,6 +356,10 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
     const long D = c.dim, H = c.hidden, KV = c.kv_dim, S = c.seq_len;
     const int QR = (int)(D + 2 * KV);
     int st = PTMI_OK;
+    if (m->step_mem) {                                    // the one-kernel step
+        TIMED(7, st = launch_decode_step(m, s, e0, e1));
+        return st;
+    }
     for (int l = 0; l < c.n_layers; l++) {
         float *kc = m->kc + (long)l * S * KV, *vc = m->vc + (long)l * S * KV;
         MatvecParams p = {};
@@ -450,10 +454,23 @@ int launch_step(ptmi_model *m, hipStream_t s) {
     return PTMI_OK;
 }
 
+// The host's four fields of the control block (the step sequence number
+// and the error word stay as the device left them).
 int set_ctl(ptmi_model *m, int tok, int pos, int n_prompt) {
-    DecodeCtl h = {tok, pos, n_prompt, 0};
-    PTMI_HIP(hipMemcpyAsync(m->ctl, &h, sizeof(h), hipMemcpyHostToDevice, lib_stream()));
+    const int h[4] = {tok, pos, n_prompt, 0};
+    PTMI_HIP(hipMemcpyAsync(m->ctl, h, sizeof(h), hipMemcpyHostToDevice, lib_stream()));
     return PTMI_OK;
+}
+
+// After a synchronised step: a wait of the one-kernel step that timed out
+// is an error (the step's results are void).  The error word is cleared and
+// the step sequence number moved past the failed step's, whose partly
+// written exchange words carry its tag and must never match a later step.
+int check_step_error(ptmi_model *m, const DecodeCtl &h) {
+    if (!h.err) return PTMI_OK;
+    const int fix[2] = {h.seq + 1, 0};                   // seq, err
+    PTMI_HIP(hipMemcpy(&m->ctl->seq, fix, sizeof(fix), hipMemcpyHostToDevice));
+    return set_error(PTMI_ERR_STATE, "decode step: a workgroup timed out waiting for another's results");
 }
 
 int zero_kv(ptmi_model *m) {
@@ -537,8 +554,10 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
     m->eager = eager && eager[0] == '1';
     const char *nopf = getenv("PTMI_NO_PREFETCH");
     m->prefetch = !(nopf && nopf[0] == '1');
-    if ((!m->eager && (st = build_graph(m))) || (max_T > 0 && (st = train_create(m)))) {
+    if ((st = decode_step_create(m)) || (!m->eager && (st = build_graph(m))) ||
+        (max_T > 0 && (st = train_create(m)))) {
         train_destroy(m);
+        decode_step_destroy(m);
         if (m->exec) (void)hipGraphExecDestroy(m->exec);
         if (m->graph) (void)hipGraphDestroy(m->graph);
         (void)hipFree(m->mem);
@@ -556,6 +575,7 @@ void ptmi_model_destroy(ptmi_model_t *m) {
     train_destroy(m);
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
     if (m->graph) (void)hipGraphDestroy(m->graph);
+    decode_step_destroy(m);
     (void)hipFree(m->mem);
     release_blob(m->res);
     delete m;
@@ -591,6 +611,7 @@ int ptmi_model_forward_step(ptmi_model_t *m, int token, int *next) {
     DecodeCtl h;
     PTMI_HIP(hipMemcpyAsync(&h, m->ctl, sizeof(h), hipMemcpyDeviceToHost, s));
     PTMI_HIP(hipStreamSynchronize(s));
+    if ((st = check_step_error(m, h))) return st;
     m->host_pos++;
     if (next) *next = h.next;
     return PTMI_OK;
@@ -623,7 +644,10 @@ int ptmi_model_generate(ptmi_model_t *m, const int *prompt, int n_prompt, int ma
     for (int i = 0; i < max_tokens; i++)
         if ((st = launch_step(m, s))) return st;
     PTMI_HIP(hipMemcpyAsync(out, m->out_tokens, (size_t)max_tokens * sizeof(int), hipMemcpyDeviceToHost, s));
+    DecodeCtl h;
+    PTMI_HIP(hipMemcpyAsync(&h, m->ctl, sizeof(h), hipMemcpyDeviceToHost, s));
     PTMI_HIP(hipStreamSynchronize(s));
+    if ((st = check_step_error(m, h))) return st;
     m->host_pos = max_tokens;
     int n = max_tokens;
     if (stop_on_eos)                                               // pt_text.c:354
@@ -647,12 +671,12 @@ int ptmi_model_decode_async(ptmi_model_t *m, int first_token, int n_steps) {
     return PTMI_OK;
 }
 
-int ptmi_model_profile(ptmi_model_t *m, int first_token, int n_steps, float role_ms[7], int role_launches[7]) {
+int ptmi_model_profile(ptmi_model_t *m, int first_token, int n_steps, float role_ms[8], int role_launches[8]) {
     if (!m || !role_ms || !role_launches) return set_error(PTMI_ERR_ARG, "NULL argument");
     if (first_token < 0 || first_token >= m->c.vocab) return set_error(PTMI_ERR_ARG, "token out of range");
     if (n_steps < 0 || m->host_pos + n_steps > m->c.seq_len)
         return set_error(PTMI_ERR_STATE, "pos %d + %d steps exceeds seq_len %d", m->host_pos, n_steps, m->c.seq_len);
-    for (int i = 0; i < 7; i++) { role_ms[i] = 0.0f; role_launches[i] = 0; }
+    for (int i = 0; i < 8; i++) { role_ms[i] = 0.0f; role_launches[i] = 0; }
     hipStream_t s = lib_stream();
     int st;
     if ((st = set_ctl(m, first_token, m->host_pos, 0))) return st;
@@ -661,6 +685,9 @@ int ptmi_model_profile(ptmi_model_t *m, int first_token, int n_steps, float role
         tm.used = 0;
         if ((st = enqueue_step(m, s, &tm))) return st;
         PTMI_HIP(hipStreamSynchronize(s));
+        DecodeCtl h;
+        PTMI_HIP(hipMemcpy(&h, m->ctl, sizeof(h), hipMemcpyDeviceToHost));
+        if ((st = check_step_error(m, h))) return st;
         for (size_t i = 0; i < tm.used / 2; i++) {
             float ms = 0.0f;
             PTMI_HIP(hipEventElapsedTime(&ms, tm.ev[2 * i], tm.ev[2 * i + 1]));

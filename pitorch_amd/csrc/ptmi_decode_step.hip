@@ -1,0 +1,986 @@
+// The decode step (pt_forward_step over pt_forward, pitorch/model/llama2.c:
+// 127-206, plus the argmax of pitorch/pt.c:267-271) as ONE persistent
+// kernel launch per token.
+//
+// A kernel boundary on this part costs ~4 us per dependent stage (launch,
+// L2 invalidate, then the first weight round trip); the step has 5L+2 such
+// stages.  Here every workgroup walks all stages of the token:
+//  * each stage's weights are loaded into registers BEFORE the workgroup
+//    waits for the stage's input, so the weight stream overlaps the
+//    dependency latency instead of following it;
+//  * every value handed between workgroups within the token is one 64-bit
+//    word (float bits | 32-bit tag), written and read with agent-scope
+//    relaxed atomics (they bypass the per-XCD L2s, which are not coherent
+//    with each other).  The tag is the step's sequence number, so a reader
+//    never accepts a value of an earlier token, and every (layer, stage)
+//    has its own buffer, so nothing is overwritten while it can still be
+//    read.  A consumer polls exactly the words it needs — no barrier
+//    flags, no fences.
+//  * data that only later tokens read (the KV cache rows of this position)
+//    and the logits the host reads are plain stores: the kernel boundary
+//    between tokens makes them visible.
+// Every wait is bounded (20 ms of the 100 MHz real-time counter) and
+// checks a shared error word, so on any failure every wave leaves within
+// one bound and the host reports the error.
+//
+// Stages per layer (workgroup b takes row blocks b, b+NB, ...):
+//   QKV  : RMSNorm(x) . [Wq;Wk;Wv], RoPE, q|k|v published, K/V cache row
+//   ATT  : (head, chunk of positions) units: scores, chunk softmax, e.v
+//   WO   : combine the chunks of every head, . Wo, + residual  -> x_a
+//   W13  : RMSNorm(x_a) . [w1|w3] rows interleaved, SwiGLU     -> hb
+//   W2   : hb . w2 + x_a                                         -> x_b
+// then the classifier (RMSNorm . Wcls, per-workgroup argmax candidates)
+// and workgroup 0's final argmax, prompt forcing and position advance.
+// Arithmetic per element follows the multi-kernel step (and through it
+// the reference's ops); reductions run in a different order.
+#include "ptmi_model.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <type_traits>
+
+namespace ptmi {
+
+namespace {
+
+constexpr int kT = 512;                      // threads per workgroup
+constexpr int kW = kT / 64;                  // waves per workgroup
+constexpr int kRowsD = 2 * kW;               // rows per block, D-length rows (32 lanes per row)
+constexpr int kRowsH = kW;                   // rows per block, H-length rows (64 lanes per row)
+constexpr int kMaxChunk = 128;               // attention positions per unit
+constexpr int kMaxChunks = 8;                // units per head
+constexpr int kWriter = kW - 1;              // the wave that issues the workgroup's global stores
+constexpr int kPollT = kWriter * 64;         // threads that poll (all other waves)
+constexpr int kPartLds = 16 * kPollT;        // floats of chunk partials a workgroup combines
+constexpr uint64_t kWaitTicks = 2000000;     // default wait bound: 20 ms at 100 MHz
+
+typedef float fx4 __attribute__((ext_vector_type(4)));
+
+struct StepArgs {
+    // weights (device layout of the registered blob)
+    const float *emb, *rms_att, *wqkv, *wo, *rms_ffn, *w13, *w2, *rms_final, *wcls;
+    int D, H, L, NH, KV, hd, kv_mul, V, S;
+    int chunk, n_chunks;                     // attention unit = chunk positions of one head
+    float att_scale;
+    float *kc, *vc;                          // [L][S][KV]
+    float *logits;                           // [V]
+    DecodeCtl *ctl;
+    const int *prompt;
+    int *out_tokens;
+    // tagged exchange buffers: word = tag << 32 | float bits
+    uint64_t *t_qkv;                         // [L][D + 2KV]
+    uint64_t *t_part;                        // [L][n_chunks][NH][hd + 2]  (o[hd], max, sum)
+    uint64_t *t_xa, *t_xb;                   // [L][D]
+    uint64_t *t_hb;                          // [L][H]
+    uint64_t *t_cand;                        // [nb][2]  (best logit, its index)
+    // optional stage stamps (PTMI_STEP_STAMPS=1): per workgroup, the 100 MHz
+    // real-time counter at kernel start, then for every stage the end of
+    // its wait and the end of its work; 0 where the workgroup had no part
+    uint64_t *stamps;                        // [nb][n_stamps]
+    int n_stamps;                            // 1 + 10 L + 4
+    uint64_t wait_ticks;                     // bound of every wait (100 MHz ticks)
+};
+
+
+// Every pointer of the argument block points to global memory; accesses
+// go through the global address space explicitly (pointers read from
+// memory are otherwise generic, and flat instructions also count against
+// the LDS counter, so an LDS read would wait for every flat load in flight).
+#define PTMI_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ PTMI_GLOBAL T *gl(T *p) {
+    return (PTMI_GLOBAL T *)p;
+}
+
+// The argument block is read through the constant address space: its
+// fields come in with scalar loads.
+#define PTMI_CONST __attribute__((address_space(4)))
+
+// Stamp slot `i` of this workgroup (thread 0 only; no-op without stamps).
+__device__ __forceinline__ void stamp(const PTMI_CONST StepArgs *a, int i) {
+    if (a->stamps && threadIdx.x == kPollT)
+        gl(a->stamps)[(long)blockIdx.x * a->n_stamps + i] = __builtin_amdgcn_s_memrealtime();
+}
+
+__device__ __forceinline__ uint64_t tload(const uint64_t *p) {
+    return __hip_atomic_load(gl(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void tstore(uint64_t *p, float v, uint32_t tag) {
+    __hip_atomic_store(gl(p), ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int err_seen(const DecodeCtl *c) {
+    return __hip_atomic_load(gl(&c->err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A value the compiler cannot see through: per-thread addresses derived
+// from it are recomputed where they are used (a few ALU operations)
+// instead of being hoisted out of the layer loop and held in registers
+// for the whole kernel.
+__device__ __forceinline__ int opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+__device__ __forceinline__ float4 sel4(bool keep, float4 v) {
+    return make_float4(keep ? v.x : 0.0f, keep ? v.y : 0.0f, keep ? v.z : 0.0f, keep ? v.w : 0.0f);
+}
+__device__ __forceinline__ float dot4(float4 a, float4 b, float acc) {
+    acc = fmaf(a.x, b.x, acc);
+    acc = fmaf(a.y, b.y, acc);
+    acc = fmaf(a.z, b.z, acc);
+    return fmaf(a.w, b.w, acc);
+}
+__device__ __forceinline__ float4 load4(const float *p) {
+    const fx4 t = *gl(reinterpret_cast<const fx4 *>(p));
+    return make_float4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ float4 ntload4(const float *p) {
+    const fx4 t = __builtin_nontemporal_load(gl(reinterpret_cast<const fx4 *>(p)));
+    return make_float4(t.x, t.y, t.z, t.w);
+}
+
+// Wait until the n tagged words of src carry `tag`; their values go to
+// dst (LDS).  The calling thread takes words t, t + kPollT, ... (t = its
+// index among the callers), at most K of them, and re-reads only those
+// still missing.  Returns false on a timeout or when another workgroup has
+// already failed.
+// Only waves other than the writer wave poll: on this GPU a wave's loads
+// and stores share one in-order counter, so a wave that has just stored
+// would see its poll wait for the acknowledgement of its stores.
+template <int K>
+__device__ bool poll_words(const uint64_t *src, int n, uint32_t tag, float *dst, const DecodeCtl *ctl, int t,
+                           uint64_t wait_ticks) {
+    t = opaque(t);
+    bool ok[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) ok[k] = t + k * kPollT >= n;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+        uint64_t v[K];
+#pragma unroll
+        for (int k = 0; k < K; k++)
+            if (!ok[k]) v[k] = tload(src + t + k * kPollT);
+        bool all = true;
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            if (ok[k]) continue;
+            if ((uint32_t)(v[k] >> 32) == tag) {
+                dst[t + k * kPollT] = __uint_as_float((uint32_t)v[k]);
+                ok[k] = true;
+            } else {
+                all = false;
+            }
+        }
+        if (all) return true;
+        if (err_seen(ctl) || __builtin_amdgcn_s_memrealtime() - t0 > wait_ticks) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Block-uniform end of a wait: every thread reaches the barrier; true when
+// the whole block may go on.
+__device__ __forceinline__ bool block_ok(bool mine, int *s_fail, DecodeCtl *ctl) {
+    if (!mine) {
+        *s_fail = 1;
+        __hip_atomic_fetch_or(gl(&ctl->err), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return *s_fail == 0;
+}
+
+// argmax pair (value, index): larger value, ties to the smaller index
+// (pt_ops.c:65-70 returns the first index of the maximum).
+__device__ __forceinline__ void take_best(float &bv, int &bi, float ov, int oi) {
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+
+// The argument block lives in device memory; every stage re-reads the
+// fields it needs through a pointer the compiler cannot see through, so
+// uniform values are reloaded per stage (scalar-cache hits) instead of
+// being held in scalar registers across the whole layer loop.
+__device__ __forceinline__ const PTMI_CONST StepArgs *fresh(const StepArgs *p) {
+    asm volatile("" : "+s"(p));
+    return (const PTMI_CONST StepArgs *)p;
+}
+
+// Per-token values read once at kernel start.
+struct Tok {
+    int pos, token, nact;
+    uint32_t tag;
+};
+
+// Workgroup LDS.
+struct Smem {
+    float xs[2048];                    // the stage's input vector (<= max(D, H))
+    float part[kPartLds];              // WO: chunk partials of every head
+    float wts[64][kMaxChunks];         // WO: chunk weights per head
+    float xres[kRowsD];                // WO: residual rows of this block
+    float xres2[kRowsH];               // W2: residual rows of this block
+    float rope_c[64], rope_s[64];      // RoPE cos/sin of this position, pair i = 2*k (all layers)
+    float ybuf[kW][2];                 // argmax per wave
+    float qs[128], kp[128], vp[128];   // ATT: q, and k/v of this position
+    float sc[kMaxChunk];               // ATT: scores -> weights
+    float red[kW][128];
+    float wred[kW];
+    float cand[1024];                  // final argmax: (value, index) per workgroup
+    float yout[kRowsD];                // results the writer wave stores
+    int fail;
+};
+
+// Per-lane registers carried between stages: the weights of the next
+// stage (loaded before its wait) and the K/V rows of the attention unit.
+template <int ITD, int ITH, int GA>
+struct Regs {
+    static constexpr int kRPW = 64 / GA;                 // K/V rows per wave load
+    static constexpr int kU = kMaxChunk / (kW * kRPW);   // loads per thread per chunk
+    float4 wD[ITD], nw[ITD], wH[ITH];
+    float4 kk[kU], vv[kU];
+};
+
+__device__ __forceinline__ int slot_d() { return opaque(((int)threadIdx.x >> 6) * 2 + (((int)threadIdx.x & 63) >> 5)); }
+__device__ __forceinline__ int sub_d() { return opaque((int)threadIdx.x & 31); }
+
+// Weights of D-length row block rb of W (rows x D) and, when norm is set,
+// the RMSNorm weights of this lane's columns.  Rows past the matrix
+// re-read its last row; chunks past the row re-read its last chunk (both
+// dropped at use).
+template <int ITD, int ITH, int GA>
+__device__ __forceinline__ void load_wD(const PTMI_CONST StepArgs *a, Regs<ITD, ITH, GA> &R, const float *W, int rows, int rb,
+                                        const float *norm) {
+    const int nD4 = a->D >> 2, slot = slot_d(), sub = sub_d();
+    const int r = min(rb * kRowsD + slot, rows - 1);
+    const float *row = W + (long)r * a->D;
+#pragma unroll
+    for (int it = 0; it < ITD; it++) R.wD[it] = ntload4(row + 4 * min(sub + it * 32, nD4 - 1));
+    if (norm) {
+#pragma unroll
+        for (int it = 0; it < ITD; it++) R.nw[it] = load4(norm + 4 * min(sub + it * 32, nD4 - 1));
+    }
+}
+
+template <int ITD, int ITH, int GA>
+__device__ __forceinline__ void load_wH(const PTMI_CONST StepArgs *a, Regs<ITD, ITH, GA> &R, const float *W, int rows, int rb) {
+    const int nH4 = a->H >> 2, slot = opaque((int)threadIdx.x >> 6), sub = opaque((int)threadIdx.x & 63);
+    const int r = min(rb * kRowsH + slot, rows - 1);
+    const float *row = W + (long)r * a->H;
+#pragma unroll
+    for (int it = 0; it < ITH; it++) R.wH[it] = ntload4(row + 4 * min(sub + it * 64, nH4 - 1));
+}
+
+// The lane's D-row weights against xs (RMSNorm'd when norm): the row's sum
+// in every lane of its 32-lane group.
+template <int ITD, int ITH, int GA>
+__device__ __forceinline__ float dot_d(const PTMI_CONST StepArgs *a, const Regs<ITD, ITH, GA> &R, const float *xs, bool norm) {
+    const int nD4 = a->D >> 2, sub = sub_d();
+    float4 xr[ITD];
+#pragma unroll
+    for (int it = 0; it < ITD; it++) {
+        const int c = sub + it * 32;
+        xr[it] = sel4(c < nD4, reinterpret_cast<const float4 *>(xs)[min(c, nD4 - 1)]);
+    }
+    if (norm) {                                       // rmsnorm, pt_ops.c:5-12
+        float ss = 0.0f;
+#pragma unroll
+        for (int it = 0; it < ITD; it++)
+            ss += xr[it].x * xr[it].x + xr[it].y * xr[it].y + xr[it].z * xr[it].z + xr[it].w * xr[it].w;
+        ss = group_sum<32>(ss);
+        const float inv = 1.0f / d_sqrtf(ss / (float)a->D + 1e-5f);
+#pragma unroll
+        for (int it = 0; it < ITD; it++) {
+            xr[it].x = xr[it].x * inv * R.nw[it].x;
+            xr[it].y = xr[it].y * inv * R.nw[it].y;
+            xr[it].z = xr[it].z * inv * R.nw[it].z;
+            xr[it].w = xr[it].w * inv * R.nw[it].w;
+        }
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int it = 0; it < ITD; it++) acc = dot4(sel4(sub + it * 32 < nD4, R.wD[it]), xr[it], acc);
+    return group_sum<32>(acc);
+}
+
+template <int ITD, int ITH, int GA>
+__device__ __forceinline__ float dot_h(const PTMI_CONST StepArgs *a, const Regs<ITD, ITH, GA> &R, const float *xs) {
+    const int nH4 = a->H >> 2, sub = opaque((int)threadIdx.x & 63);
+    float acc = 0.0f;
+#pragma unroll
+    for (int it = 0; it < ITH; it++) {
+        const int c = sub + it * 64;
+        const bool in = c < nH4;
+        acc = dot4(sel4(in, R.wH[it]), sel4(in, reinterpret_cast<const float4 *>(xs)[min(c, nH4 - 1)]), acc);
+    }
+    return group_sum<64>(acc);
+}
+
+// K/V rows of attention unit u (head u % NH, chunk u / NH) at positions
+// below pos (written by earlier tokens' kernels), clamped into the chunk.
+template <int ITD, int ITH, int GA>
+__device__ __forceinline__ void load_kv(const PTMI_CONST StepArgs *a, Regs<ITD, ITH, GA> &R, const Tok &t, int l, int u) {
+    using Rg = Regs<ITD, ITH, GA>;
+    const int lane = (int)threadIdx.x & 63, wave = opaque((int)threadIdx.x >> 6);
+    const int h = u % a->NH, c = u / a->NH;
+    const int t0 = c * a->chunk, t_end = min(t0 + a->chunk, t.pos + 1);
+    const int slot = opaque(lane / GA), sub = opaque(lane % GA);
+    const int sub_c = min(sub, (a->hd >> 2) - 1);
+    const long base = (long)l * a->S * a->KV + (long)(h / a->kv_mul) * a->hd + 4 * sub_c;
+    const int top = max(t0, min(t_end, t.pos) - 1);
+#pragma unroll
+    for (int q = 0; q < Rg::kU; q++) {
+        const int row = t0 + q * (kW * Rg::kRPW) + wave * Rg::kRPW + slot;
+        const long o = base + (long)max(t0, min(row, top)) * a->KV;
+        R.kk[q] = ntload4(a->kc + o);
+        R.vv[q] = ntload4(a->vc + o);
+    }
+}
+
+// L2 prefetch by a workgroup that has no work in the current window: row
+// blocks rb (rows [rb*R, rb*R + R) of W, n floats per row) that workgroups
+// on this XCD (rb % 8 == blockIdx.x % 8) will load into registers later,
+// shared among the idle workgroups of this XCD whose blockIdx is at least
+// first_idle.  Plain loads allocate the lines in this XCD's L2, which no
+// kernel boundary invalidates before the owners read them.
+__device__ __forceinline__ float prefetch_rows(const float *W, int rows, int n, int R, int nblocks, int first_idle,
+                                               int nb, float acc) {
+    const int b = blockIdx.x, x = b & 7;
+    if (b < first_idle) return acc;
+    const int m0 = first_idle > x ? (first_idle - x + 7) / 8 : 0;
+    const int m_end = (nb - 1 - x) / 8 + 1;
+    const int rank = b / 8 - m0, nranks = m_end - m0;
+    if (nranks <= 0) return acc;
+    const int t = opaque((int)threadIdx.x);
+    for (int j = rank; x + 8 * j < nblocks; j += nranks) {
+        const int rb = x + 8 * j;
+        const int r0 = rb * R, r1 = min(r0 + R, rows);
+        const long n4 = (long)(r1 - r0) * n / 4;
+        const float *base = W + (long)r0 * n;
+        for (long i = t; i < n4; i += 8L * kT) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = load4(base + 4 * min(i + (long)u * kT, n4 - 1));
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc += v[u].x;
+        }
+    }
+    return acc;
+}
+
+template <int ITD, int ITH, int GA>
+__global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
+    using Rg = Regs<ITD, ITH, GA>;
+    __shared__ Smem sm;
+    Rg R;
+    float pf_acc = 0.0f;                              // keeps prefetch loads alive
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int b = blockIdx.x, nb = gridDim.x;
+    Tok tk;
+    int L;
+    {
+        const PTMI_CONST StepArgs *a = fresh(ap);
+        tk.pos = gl(a->ctl)->pos;
+        tk.tag = (uint32_t)gl(a->ctl)->seq + 1u;
+        tk.token = gl(a->ctl)->tok_in;
+        tk.nact = tk.pos / a->chunk + 1;
+        L = a->L;
+        if (tid == 0) sm.fail = 0;
+        // RoPE angle of pair (i, i+1) depends on i % head_dim and pos only
+        // (pt_ops.c:33-40): one table per token serves q and k of every layer
+        if (tid < (a->hd >> 1)) {
+            float c, sn;
+            d_rope_cs(2 * tid, a->hd, tk.pos, &c, &sn);
+            sm.rope_c[tid] = c;
+            sm.rope_s[tid] = sn;
+        }
+        if (b < (a->D + 2 * a->KV + kRowsD - 1) / kRowsD) load_wD(a, R, a->wqkv, a->D + 2 * a->KV, b, a->rms_att);
+        stamp(a, 0);
+    }
+    __syncthreads();
+
+    for (int l = 0; l < L; l++) {
+        // ── QKV: y = [Wq;Wk;Wv] . rmsnorm(x), RoPE on q and k (llama2.c:
+        //    143-151); k and v also into the cache row of pos ──
+        {
+            const PTMI_CONST StepArgs *a = fresh(ap);
+            const int D = a->D, KV = a->KV, QR = D + 2 * KV;
+            const int blocks_qkv = (QR + kRowsD - 1) / kRowsD, blocks_wo = (D + kRowsD - 1) / kRowsD;
+            const int n_units = a->NH * a->n_chunks;
+            const bool unit = b < n_units && b / a->NH < tk.nact;
+            if (b < blocks_qkv) {
+                __syncthreads();                              // xs is free again
+                bool ok = true;
+                if (l == 0) {
+                    const float *x = a->emb + (long)tk.token * D;
+                    for (int i = tid; i < D; i += kT) sm.xs[i] = gl(x)[i];
+                } else {
+                    ok = tid >= kPollT || poll_words<5>(a->t_xb + (long)(l - 1) * D, D, tk.tag, sm.xs, a->ctl, tid, a->wait_ticks);
+                }
+                if (!block_ok(ok, &sm.fail, a->ctl)) return;
+                stamp(a, 1 + 10 * l);
+                // the WO residual rows are rows of this same input
+                if (b < blocks_wo && tid < kRowsD) sm.xres[tid] = sm.xs[min(b * kRowsD + tid, D - 1)];
+                uint64_t *t_qkv = a->t_qkv + (long)l * QR;
+                for (int rb = b; rb < blocks_qkv; rb += nb) {
+                    if (rb != b) {
+                        __syncthreads();                      // the writer wave is done with yout
+                        load_wD(a, R, a->wqkv + (long)l * QR * D, QR, rb, a->rms_att + (long)l * D);
+                    }
+                    const float acc = dot_d(a, R, sm.xs, true);
+                    if (rb + nb >= blocks_qkv) {              // this block's last rows: next stages' loads
+                        if (unit) load_kv(a, R, tk, l, b);
+                        if (b < blocks_wo) load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
+                    }
+                    // RoPE pairs: rows 2k (lanes 0-31) and 2k+1 (lanes 32-63) of a wave
+                    const LanePair pr = pl32(acc);
+                    const int r = rb * kRowsD + slot_d();
+                    if ((lane & 31) == 0 && r < QR) {
+                        const int r0 = r & ~1;
+                        float out;
+                        if (r0 < D + KV) {
+                            const int k = ((r0 < D ? r0 : r0 - D) % a->hd) >> 1;
+                            const float c = sm.rope_c[k], sn = sm.rope_s[k];
+                            out = (r & 1) ? pr.lo * sn + pr.hi * c : pr.lo * c - pr.hi * sn;
+                        } else {
+                            out = (r & 1) ? pr.hi : pr.lo;
+                        }
+                        sm.yout[slot_d()] = out;
+                    }
+                    __syncthreads();
+                    if (wave == kWriter && lane < kRowsD) {
+                        const int rw = rb * kRowsD + lane;
+                        if (rw < QR) {
+                            const float out = sm.yout[lane];
+                            tstore(t_qkv + rw, out, tk.tag);
+                            const long crow = ((long)l * a->S + tk.pos) * KV;
+                            if (rw >= D + KV) gl(a->vc)[crow + (rw - D - KV)] = out;
+                            else if (rw >= D) gl(a->kc)[crow + (rw - D)] = out;
+                        }
+                    }
+                }
+                stamp(a, 2 + 10 * l);
+            } else {
+                if (unit) load_kv(a, R, tk, l, b);
+                if (b < blocks_wo) load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
+            }
+            // Workgroups with no QKV, attention or Wo work wait until the
+            // w1|w3 stage: meanwhile they stage this layer's w1|w3 and w2
+            // rows in their XCD's L2.
+            const int H = a->H;
+            const int first_idle = max(max(blocks_qkv, blocks_wo), n_units);
+            if (b >= first_idle) {
+                pf_acc = prefetch_rows(a->w13 + (long)l * 2 * H * D, 2 * H, D, kRowsD, (2 * H + kRowsD - 1) / kRowsD,
+                                       first_idle, nb, pf_acc);
+                pf_acc = prefetch_rows(a->w2 + (long)l * D * H, D, H, kRowsH, (D + kRowsH - 1) / kRowsH, first_idle, nb,
+                                       pf_acc);
+            }
+        }
+
+        // ── ATT: unit (head h, chunk c) over positions [t0, t_end) (llama2.c:
+        //    153-177): scores, the chunk's softmax statistics and e.v ──
+        {
+            const PTMI_CONST StepArgs *a = fresh(ap);
+            const int D = a->D, KV = a->KV, hd = a->hd, NH = a->NH, QR = D + 2 * KV;
+            const int n_units = NH * a->n_chunks;
+            for (int u = b; u < n_units; u += nb) {
+                const int h = u % NH, c = u / NH;
+                if (c >= tk.nact) continue;                   // uniform: chunk past pos
+                if (u != b) load_kv(a, R, tk, l, u);
+                const int t0 = c * a->chunk, t_end = min(t0 + a->chunk, tk.pos + 1), cnt = t_end - t0;
+                const bool has_pos = tk.pos < t_end;
+                const int kvh = h / a->kv_mul;
+                const uint64_t *t_qkv = a->t_qkv + (long)l * QR;
+                __syncthreads();
+                bool ok = true;
+                if (tid < hd) {
+                    ok = poll_words<1>(t_qkv + h * hd, hd, tk.tag, sm.qs, a->ctl, tid, a->wait_ticks);
+                } else if (has_pos && tid >= 128 && tid < 128 + hd) {
+                    ok = poll_words<1>(t_qkv + D + kvh * hd, hd, tk.tag, sm.kp, a->ctl, tid - 128, a->wait_ticks);
+                } else if (has_pos && tid >= 256 && tid < 256 + hd) {
+                    ok = poll_words<1>(t_qkv + D + KV + kvh * hd, hd, tk.tag, sm.vp, a->ctl, tid - 256, a->wait_ticks);
+                }
+                if (!block_ok(ok, &sm.fail, a->ctl)) return;
+                stamp(a, 3 + 10 * l);
+                const int slot = lane / GA, sub = lane % GA;
+                const bool has = sub < (hd >> 2);
+                const int sub_c = has ? sub : 0;
+                const float4 q4 = sel4(has, reinterpret_cast<const float4 *>(sm.qs)[sub_c]);
+                const float4 kp4 = reinterpret_cast<const float4 *>(sm.kp)[sub_c];
+                const float4 vp4 = reinterpret_cast<const float4 *>(sm.vp)[sub_c];
+#pragma unroll
+                for (int q = 0; q < Rg::kU; q++) {
+                    const int t = t0 + q * (kW * Rg::kRPW) + wave * Rg::kRPW + slot;
+                    const float4 k4 = sel4(t < t_end, t == tk.pos ? kp4 : R.kk[q]);
+                    float sv = has ? dot4(k4, q4, 0.0f) : 0.0f;
+                    sv = group_sum<GA>(sv);
+                    if (sub == 0 && t < t_end) sm.sc[t - t0] = sv * a->att_scale;
+                }
+                __syncthreads();
+                // chunk softmax statistics: max, then e^(s - max) and their sum
+                float mx = -INFINITY;
+                for (int i = tid; i < cnt; i += kT) mx = fmaxf(mx, sm.sc[i]);
+                mx = group_max<64>(mx);
+                if (lane == 0) sm.wred[wave] = mx;
+                __syncthreads();
+                mx = sm.wred[0];
+#pragma unroll
+                for (int w = 1; w < kW; w++) mx = fmaxf(mx, sm.wred[w]);
+                __syncthreads();
+                float sum = 0.0f;
+                for (int i = tid; i < cnt; i += kT) {
+                    const float e = d_expf(sm.sc[i] - mx);
+                    sm.sc[i] = e;
+                    sum += e;
+                }
+                sum = group_sum<64>(sum);
+                if (lane == 0) sm.wred[wave] = sum;
+                __syncthreads();
+                float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int q = 0; q < Rg::kU; q++) {
+                    const int t = t0 + q * (kW * Rg::kRPW) + wave * Rg::kRPW + slot;
+                    const float e = t < t_end ? sm.sc[t - t0] : 0.0f;
+                    const float4 v4 = sel4(t < t_end, t == tk.pos ? vp4 : R.vv[q]);
+                    acc.x = fmaf(e, v4.x, acc.x);
+                    acc.y = fmaf(e, v4.y, acc.y);
+                    acc.z = fmaf(e, v4.z, acc.z);
+                    acc.w = fmaf(e, v4.w, acc.w);
+                }
+                // sum over the wave's row slots (lanes with equal lane % GA)
+                auto slot_sum = [](float v) {
+                    if constexpr (GA <= 16) v = xsum16(v);
+                    return xsum32(v);
+                };
+                acc.x = slot_sum(acc.x);
+                acc.y = slot_sum(acc.y);
+                acc.z = slot_sum(acc.z);
+                acc.w = slot_sum(acc.w);
+                if (slot == 0 && has) {
+                    sm.red[wave][4 * sub + 0] = acc.x;
+                    sm.red[wave][4 * sub + 1] = acc.y;
+                    sm.red[wave][4 * sub + 2] = acc.z;
+                    sm.red[wave][4 * sub + 3] = acc.w;
+                }
+                __syncthreads();
+                uint64_t *dst = a->t_part + (((long)l * a->n_chunks + c) * NH + h) * (hd + 2);
+                if (wave == kWriter) {
+                    if (lane < hd) {
+                        float o = 0.0f;
+#pragma unroll
+                        for (int w = 0; w < kW; w++) o += sm.red[w][lane];
+                        tstore(dst + lane, o, tk.tag);
+                    }
+                    if (lane == 0) tstore(dst + hd, mx, tk.tag);
+                    if (lane == 1) {
+                        float lsum = 0.0f;
+#pragma unroll
+                        for (int w = 0; w < kW; w++) lsum += sm.wred[w];
+                        tstore(dst + hd + 1, lsum, tk.tag);
+                    }
+                }
+                stamp(a, 4 + 10 * l);
+            }
+        }
+
+        // ── WO: x_a = x + Wo . combine(chunks) (llama2.c:179-180) ──
+        {
+            const PTMI_CONST StepArgs *a = fresh(ap);
+            const int D = a->D, H = a->H, hd = a->hd, NH = a->NH;
+            const int blocks_wo = (D + kRowsD - 1) / kRowsD, blocks_w13 = (2 * H + kRowsD - 1) / kRowsD;
+            const float *x_emb = a->emb + (long)tk.token * D;
+            const uint64_t *t_xin = a->t_xb + (long)(l - 1) * D;      // used for l > 0 only
+            uint64_t *t_xa = a->t_xa + (long)l * D;
+            if (b < blocks_wo) {
+                const int nwords = tk.nact * NH * (hd + 2);
+                __syncthreads();
+                // (the first block's residual rows came with the QKV input)
+                bool ok = tid >= kPollT || poll_words<kPartLds / kPollT>(a->t_part + (long)l * a->n_chunks * NH * (hd + 2),
+                                                                         nwords, tk.tag, sm.part, a->ctl, tid, a->wait_ticks);
+                if (!block_ok(ok, &sm.fail, a->ctl)) return;
+                stamp(a, 5 + 10 * l);
+                // chunk weights w[h][c] = e^(m_c - M) / sum_c' l_c' e^(m_c' - M)
+                if (tid < NH) {
+                    const int nact = tk.nact;
+                    float M = -INFINITY;
+                    for (int c = 0; c < nact; c++) M = fmaxf(M, sm.part[(c * NH + tid) * (hd + 2) + hd]);
+                    float f[kMaxChunks], Ls = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < kMaxChunks; c++) {
+                        const float *pc = sm.part + (min(c, nact - 1) * NH + tid) * (hd + 2);
+                        f[c] = c < nact ? d_expf(pc[hd] - M) : 0.0f;
+                        Ls = c < nact ? fmaf(pc[hd + 1], f[c], Ls) : Ls;
+                    }
+                    const float inv = 1.0f / Ls;
+#pragma unroll
+                    for (int c = 0; c < kMaxChunks; c++) sm.wts[tid][c] = f[c] * inv;
+                }
+                __syncthreads();
+                for (int i = tid; i < D; i += kT) {
+                    const int h = i / hd, d = i - h * hd;
+                    float v = 0.0f;
+                    for (int c = 0; c < tk.nact; c++) v = fmaf(sm.part[(c * NH + h) * (hd + 2) + d], sm.wts[h][c], v);
+                    sm.xs[i] = v;
+                }
+                __syncthreads();
+                for (int rb = b; rb < blocks_wo; rb += nb) {
+                    if (rb != b) {
+                        __syncthreads();                      // the writer wave is done with yout
+                        load_wD(a, R, a->wo + (long)l * D * D, D, rb, nullptr);
+                        bool ok2 = true;
+                        if (tid < kRowsD) {
+                            if (l == 0) sm.xres[tid] = gl(x_emb)[min(rb * kRowsD + tid, D - 1)];
+                            else ok2 = poll_words<1>(t_xin + rb * kRowsD, min(kRowsD, D - rb * kRowsD), tk.tag, sm.xres,
+                                                     a->ctl, tid, a->wait_ticks);
+                        }
+                        if (!block_ok(ok2, &sm.fail, a->ctl)) return;
+                    }
+                    const float acc = dot_d(a, R, sm.xs, false);
+                    if (rb + nb >= blocks_wo && b < blocks_w13)
+                        load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, b, a->rms_ffn + (long)l * D);
+                    const int slot = slot_d();
+                    if ((lane & 31) == 0) sm.yout[slot] = sm.xres[slot] + acc;
+                    __syncthreads();
+                    if (wave == kWriter && lane < kRowsD && rb * kRowsD + lane < D)
+                        tstore(t_xa + rb * kRowsD + lane, sm.yout[lane], tk.tag);
+                }
+                stamp(a, 6 + 10 * l);
+            } else if (b < blocks_w13) {
+                load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, b, a->rms_ffn + (long)l * D);
+            }
+        }
+
+        // ── W13: hb = silu(w1 . xn) * (w3 . xn), xn = rmsnorm(x_a)
+        //    (llama2.c:184-188; w1/w3 rows interleaved) ──
+        {
+            const PTMI_CONST StepArgs *a = fresh(ap);
+            const int D = a->D, H = a->H;
+            const int blocks_w13 = (2 * H + kRowsD - 1) / kRowsD, blocks_w2 = (D + kRowsH - 1) / kRowsH;
+            if (b < blocks_w13) {
+                __syncthreads();                              // xs and xres2 are free again
+                bool ok = tid >= kPollT || poll_words<5>(a->t_xa + (long)l * D, D, tk.tag, sm.xs, a->ctl, tid, a->wait_ticks);
+                if (!block_ok(ok, &sm.fail, a->ctl)) return;
+                stamp(a, 7 + 10 * l);
+                // the W2 residual rows are rows of this same input
+                if (b < blocks_w2 && tid < kRowsH) sm.xres2[tid] = sm.xs[min(b * kRowsH + tid, D - 1)];
+                uint64_t *t_hb = a->t_hb + (long)l * H;
+                for (int rb = b; rb < blocks_w13; rb += nb) {
+                    if (rb != b) {
+                        __syncthreads();                      // the writer wave is done with yout
+                        load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, rb, a->rms_ffn + (long)l * D);
+                    }
+                    const float acc = dot_d(a, R, sm.xs, true);
+                    if (rb + nb >= blocks_w13 && b < blocks_w2) load_wH(a, R, a->w2 + (long)l * D * H, D, b);
+                    const LanePair pr = pl32(acc);
+                    if (lane == 0) {
+                        const float h1 = pr.lo, h3 = pr.hi;
+                        const float sg = h1 / (1.0f + d_expf(-h1));
+                        sm.yout[wave] = sg * h3;
+                    }
+                    __syncthreads();
+                    const int i = rb * (kRowsD / 2) + lane;       // hb index of row pair `lane`
+                    if (wave == kWriter && lane < kRowsD / 2 && 2 * i < 2 * H) tstore(t_hb + i, sm.yout[lane], tk.tag);
+                }
+                stamp(a, 8 + 10 * l);
+            } else if (b < blocks_w2) {
+                load_wH(a, R, a->w2 + (long)l * D * H, D, b);
+            }
+        }
+
+        // ── W2: x_b = x_a + w2 . hb (llama2.c:189-190) ──
+        {
+            const PTMI_CONST StepArgs *a = fresh(ap);
+            const int D = a->D, H = a->H, QR = D + 2 * a->KV;
+            const int blocks_w2 = (D + kRowsH - 1) / kRowsH, blocks_w13 = (2 * H + kRowsD - 1) / kRowsD;
+            const bool last_layer = l + 1 == a->L;
+            const int next_blocks = last_layer ? (a->V + kRowsD - 1) / kRowsD : (QR + kRowsD - 1) / kRowsD;
+            auto preload_next = [&]() {
+                if (b >= next_blocks) return;
+                if (last_layer) load_wD(a, R, a->wcls, a->V, b, a->rms_final);
+                else load_wD(a, R, a->wqkv + (long)(l + 1) * QR * D, QR, b, a->rms_att + (long)(l + 1) * D);
+            };
+            if (b < blocks_w2) {
+                const uint64_t *t_xa = a->t_xa + (long)l * D;
+                uint64_t *t_xb = a->t_xb + (long)l * D;
+                __syncthreads();
+                bool ok = tid >= kPollT || poll_words<5>(a->t_hb + (long)l * H, H, tk.tag, sm.xs, a->ctl, tid, a->wait_ticks);
+                if (ok && tid < kRowsH && b >= blocks_w13)   // residual rows not taken in W13
+                    ok = poll_words<1>(t_xa + b * kRowsH, min(kRowsH, D - b * kRowsH), tk.tag, sm.xres2, a->ctl, tid, a->wait_ticks);
+                if (!block_ok(ok, &sm.fail, a->ctl)) return;
+                stamp(a, 9 + 10 * l);
+                for (int rb = b; rb < blocks_w2; rb += nb) {
+                    if (rb != b) {
+                        __syncthreads();                      // the writer wave is done with yout
+                        load_wH(a, R, a->w2 + (long)l * D * H, D, rb);
+                        bool ok2 = true;
+                        if (tid < kRowsH)
+                            ok2 = poll_words<1>(t_xa + rb * kRowsH, min(kRowsH, D - rb * kRowsH), tk.tag, sm.xres2,
+                                                a->ctl, tid, a->wait_ticks);
+                        if (!block_ok(ok2, &sm.fail, a->ctl)) return;
+                    }
+                    const float acc = dot_h(a, R, sm.xs);
+                    if (rb + nb >= blocks_w2) preload_next();
+                    if (lane == 0) sm.yout[wave] = sm.xres2[wave] + acc;
+                    __syncthreads();
+                    if (wave == kWriter && lane < kRowsH && rb * kRowsH + lane < D)
+                        tstore(t_xb + rb * kRowsH + lane, sm.yout[lane], tk.tag);
+                }
+                stamp(a, 10 + 10 * l);
+            } else {
+                preload_next();
+                // idle until the next layer's QKV input: stage its QKV and Wo
+                // rows in this XCD's L2
+                if (!last_layer) {
+                    pf_acc = prefetch_rows(a->wqkv + (long)(l + 1) * QR * D, QR, D, kRowsD, (QR + kRowsD - 1) / kRowsD,
+                                           blocks_w2, nb, pf_acc);
+                    pf_acc = prefetch_rows(a->wo + (long)(l + 1) * D * D, D, D, kRowsD, (D + kRowsD - 1) / kRowsD,
+                                           blocks_w2, nb, pf_acc);
+                }
+            }
+        }
+    }
+    if (pf_acc == 1.2345e-37f) sm.fail = 2;            // never true: keeps the prefetch loads
+
+    // ── classifier: logits = Wcls . rmsnorm(x) (llama2.c:195-197), and this
+    //    workgroup's argmax candidate ──
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    {
+        const PTMI_CONST StepArgs *a = fresh(ap);
+        const int blocks_cls = (a->V + kRowsD - 1) / kRowsD;
+        if (b < blocks_cls) {
+            __syncthreads();
+            bool ok = tid >= kPollT || poll_words<5>(a->t_xb + (long)(a->L - 1) * a->D, a->D, tk.tag, sm.xs, a->ctl, tid, a->wait_ticks);
+            if (!block_ok(ok, &sm.fail, a->ctl)) return;
+            stamp(a, 1 + 10 * a->L);
+            for (int rb = b; rb < blocks_cls; rb += nb) {
+                if (rb != b) {
+                    __syncthreads();                          // the writer wave is done with yout
+                    load_wD(a, R, a->wcls, a->V, rb, a->rms_final);
+                }
+                const float acc = dot_d(a, R, sm.xs, true);
+                const int r = rb * kRowsD + slot_d();
+                if (r < a->V) {
+                    if ((lane & 31) == 0) sm.yout[slot_d()] = acc;
+                    take_best(bv, bi, acc, r);
+                }
+                __syncthreads();
+                if (wave == kWriter && lane < kRowsD && rb * kRowsD + lane < a->V)
+                    gl(a->logits)[rb * kRowsD + lane] = sm.yout[lane];
+            }
+            stamp(a, 2 + 10 * a->L);
+        }
+    }
+    // workgroup argmax: DPP within rows of 16, the permlane swaps, then
+    // across waves
+    auto dpp_pair = [&](auto ctrl) {
+        constexpr int C = decltype(ctrl)::value;
+        take_best(bv, bi, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(bv), C, 0xF, 0xF, true)),
+                  __builtin_amdgcn_mov_dpp(bi, C, 0xF, 0xF, true));
+    };
+    dpp_pair(std::integral_constant<int, 0xB1>{});
+    dpp_pair(std::integral_constant<int, 0x4E>{});
+    dpp_pair(std::integral_constant<int, 0x141>{});
+    dpp_pair(std::integral_constant<int, 0x140>{});
+    {
+        int ih;
+        const int il = pl16i(bi, ih);
+        const LanePair p = pl16(bv);
+        bv = p.lo; bi = il;
+        take_best(bv, bi, p.hi, ih);
+    }
+    {
+        int ih;
+        const int il = pl32i(bi, ih);
+        const LanePair p = pl32(bv);
+        bv = p.lo; bi = il;
+        take_best(bv, bi, p.hi, ih);
+    }
+    __syncthreads();
+    if (lane == 0) { sm.ybuf[wave][0] = bv; sm.ybuf[wave][1] = __int_as_float(bi); }
+    __syncthreads();
+    const PTMI_CONST StepArgs *a = fresh(ap);
+    if (tid == kPollT) {                              // the writer wave
+        float v = sm.ybuf[0][0];
+        int i = __float_as_int(sm.ybuf[0][1]);
+        for (int w = 1; w < kW; w++) take_best(v, i, sm.ybuf[w][0], __float_as_int(sm.ybuf[w][1]));
+        tstore(a->t_cand + 2 * b, v, tk.tag);
+        tstore(a->t_cand + 2 * b + 1, __int_as_float(i), tk.tag);
+    }
+    if (b != 0) return;
+
+    // ── workgroup 0: the step's argmax, prompt forcing and position
+    //    advance (pt.c:267-271, pt_text.c:344-350) ──
+    __syncthreads();
+    bool ok = tid >= kPollT || poll_words<3>(a->t_cand, 2 * nb, tk.tag, sm.cand, a->ctl, tid, a->wait_ticks);
+    if (!block_ok(ok, &sm.fail, a->ctl)) return;
+    stamp(a, 3 + 10 * a->L);
+    bv = -INFINITY;
+    bi = 0x7fffffff;
+    for (int w = tid; w < nb; w += kT) take_best(bv, bi, sm.cand[2 * w], __float_as_int(sm.cand[2 * w + 1]));
+    dpp_pair(std::integral_constant<int, 0xB1>{});
+    dpp_pair(std::integral_constant<int, 0x4E>{});
+    dpp_pair(std::integral_constant<int, 0x141>{});
+    dpp_pair(std::integral_constant<int, 0x140>{});
+    {
+        int ih;
+        const int il = pl16i(bi, ih);
+        const LanePair p = pl16(bv);
+        bv = p.lo; bi = il;
+        take_best(bv, bi, p.hi, ih);
+    }
+    {
+        int ih;
+        const int il = pl32i(bi, ih);
+        const LanePair p = pl32(bv);
+        bv = p.lo; bi = il;
+        take_best(bv, bi, p.hi, ih);
+    }
+    __syncthreads();
+    if (lane == 0) { sm.ybuf[wave][0] = bv; sm.ybuf[wave][1] = __int_as_float(bi); }
+    __syncthreads();
+    if (tid == 0) {
+        float v = bv;
+        int i = bi;
+        for (int w = 1; w < kW; w++) take_best(v, i, sm.ybuf[w][0], __float_as_int(sm.ybuf[w][1]));
+        if (i == 0x7fffffff) i = 0;              // all NaN: the reference returns 0
+        const int pos = tk.pos;
+        PTMI_GLOBAL DecodeCtl *ctl = gl(a->ctl);
+        const int next = (pos < ctl->n_prompt - 1) ? gl(a->prompt)[pos + 1] : i;
+        ctl->next = i;
+        ctl->tok_in = next;
+        ctl->pos = pos + 1;
+        ctl->seq = (int)tk.tag;
+        if (a->out_tokens) gl(a->out_tokens)[pos] = next;
+    }
+    stamp(a, 4 + 10 * a->L);
+}
+
+using StepFn = void (*)(const StepArgs *);
+
+// Instantiated shapes: (float4 per lane of a D-row, of an H-row, lanes per
+// K/V row).  Other shapes keep the multi-kernel step.
+struct StepKernel { int itd, ith, ga; StepFn fn; };
+const StepKernel kStepKernels[] = {
+    {1, 1, 16, k_decode_step<1, 1, 16>}, {2, 2, 16, k_decode_step<2, 2, 16>},
+    {3, 3, 16, k_decode_step<3, 3, 16>}, {4, 6, 16, k_decode_step<4, 6, 16>},
+    {6, 8, 16, k_decode_step<6, 8, 16>},
+};
+
+}  // namespace
+
+// The persistent step for this model's shape, or null.
+static const StepKernel *pick_step(const Config &c, int *chunk, int *n_chunks) {
+    if (c.dim % 4 || c.hidden % 4 || c.head_dim % 4 || (c.dim & 1) || (c.kv_dim & 1)) return nullptr;
+    if (c.dim > 2048 || c.hidden > 2048 || c.head_dim > 128 || c.n_heads > 64) return nullptr;
+    const int itd = (c.dim / 4 + 31) / 32, ith = (c.hidden / 4 + 63) / 64;
+    const int ga = 16;                                     // lanes per K/V row: head_dim <= 64
+    if (c.head_dim > 4 * ga) return nullptr;
+    // chunk: a multiple of the K/V rows one pass of the block covers, at
+    // most kMaxChunk positions, at most kMaxChunks per head
+    const int gran = kW * (64 / ga);
+    int ch = (c.seq_len + kMaxChunks - 1) / kMaxChunks;
+    ch = (ch + gran - 1) / gran * gran;
+    if (ch > kMaxChunk) return nullptr;
+    const int nc = (c.seq_len + ch - 1) / ch;
+    if ((long)nc * c.n_heads * (c.head_dim + 2) > kPartLds) return nullptr;
+    for (const StepKernel &k : kStepKernels)
+        if (k.ga == ga && k.itd >= itd && k.ith >= ith && k.itd <= itd + 1 && k.ith <= ith + 2) {
+            *chunk = ch;
+            *n_chunks = nc;
+            return &k;
+        }
+    return nullptr;
+}
+
+int decode_step_create(ptmi_model *m) {
+    // Opt-in (PTMI_DECODE_STEP=1): measured slower than the captured
+    // multi-kernel step on stories110M (3145 vs 3640 tok/s).
+    const char *env = getenv("PTMI_DECODE_STEP");
+    if (!env || env[0] != '1') return PTMI_OK;
+    int chunk = 0, nc = 0;
+    if (!pick_step(m->c, &chunk, &nc)) return PTMI_OK;       // multi-kernel step
+    int dev = 0, cus = 0;
+    PTMI_HIP(hipGetDevice(&dev));
+    PTMI_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    if (cus <= 0) return PTMI_OK;
+    const Config &c = m->c;
+    const long L = c.n_layers, D = c.dim, H = c.hidden, KV = c.kv_dim, NH = c.n_heads, hd = c.head_dim;
+    const int nb = std::min(cus, 512);
+    // tagged words, then the argument block (32-byte aligned)
+    const size_t words = L * (D + 2 * KV) + L * nc * NH * (hd + 2) + 2 * L * D + L * H + 2 * (size_t)nb;
+    const char *st_env = getenv("PTMI_STEP_STAMPS");
+    const int n_stamps = (st_env && st_env[0] == '1') ? (int)(1 + 10 * L + 4) : 0;
+    const size_t args_off = (words * sizeof(uint64_t) + 255) / 256 * 256;
+    const size_t stamps_off = (args_off + sizeof(StepArgs) + 255) / 256 * 256;
+    const size_t total = stamps_off + (size_t)nb * n_stamps * sizeof(uint64_t);
+    char *mem = nullptr;
+    PTMI_HIP(hipMalloc(&mem, total));
+    const Resident *r = m->res;
+    StepArgs a = {};
+    a.emb = r->emb; a.rms_att = r->rms_att; a.wqkv = r->wqkv; a.wo = r->wo; a.rms_ffn = r->rms_ffn;
+    a.w13 = r->w13; a.w2 = r->w2; a.rms_final = r->rms_final; a.wcls = r->wcls;
+    a.D = c.dim; a.H = c.hidden; a.L = c.n_layers; a.NH = c.n_heads; a.KV = c.kv_dim; a.hd = c.head_dim;
+    a.kv_mul = c.n_heads / c.n_kv_heads; a.V = c.vocab; a.S = c.seq_len;
+    a.chunk = chunk; a.n_chunks = nc;
+    a.att_scale = host_att_scale(c.head_dim);
+    a.kc = m->kc; a.vc = m->vc; a.logits = m->logits; a.ctl = m->ctl;
+    a.prompt = m->prompt; a.out_tokens = m->out_tokens;
+    uint64_t *p = reinterpret_cast<uint64_t *>(mem);
+    a.t_qkv = p;  p += L * (D + 2 * KV);
+    a.t_part = p; p += L * nc * NH * (hd + 2);
+    a.t_xa = p;   p += L * D;
+    a.t_xb = p;   p += L * D;
+    a.t_hb = p;   p += L * H;
+    a.t_cand = p;
+    a.stamps = n_stamps ? reinterpret_cast<uint64_t *>(mem + stamps_off) : nullptr;
+    a.n_stamps = n_stamps;
+    // PTMI_STEP_WAIT_TICKS shortens the bound of every wait (tests of the
+    // timeout path: the step then fails and reports, and every wave exits)
+    const char *wt = getenv("PTMI_STEP_WAIT_TICKS");
+    a.wait_ticks = wt ? strtoull(wt, nullptr, 10) : kWaitTicks;
+    hipError_t e = hipMemsetAsync(mem, 0, total, lib_stream());
+    if (e == hipSuccess) e = hipMemcpyAsync(mem + args_off, &a, sizeof(a), hipMemcpyHostToDevice, lib_stream());
+    if (e == hipSuccess) e = hipStreamSynchronize(lib_stream());
+    if (e != hipSuccess) { (void)hipFree(mem); return hip_check(e, "set up the decode step"); }
+    m->step_mem = reinterpret_cast<uint64_t *>(mem);
+    m->step_args = mem + args_off;
+    m->step_nb = nb;
+    m->step_chunk = chunk;
+    m->step_chunks = nc;
+    m->step_stamps = a.stamps;
+    m->step_n_stamps = n_stamps;
+    return PTMI_OK;
+}
+
+void decode_step_destroy(ptmi_model *m) {
+    if (m->step_mem) (void)hipFree(m->step_mem);
+    m->step_mem = nullptr;
+    m->step_args = nullptr;
+}
+
+int launch_decode_step(ptmi_model *m, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+    int chunk = 0, nc = 0;
+    const StepKernel *k = pick_step(m->c, &chunk, &nc);
+    if (!k || !m->step_args || chunk != m->step_chunk || nc != m->step_chunks)
+        return set_error(PTMI_ERR_STATE, "decode step kernel not set up for this model");
+    const StepArgs *args = reinterpret_cast<const StepArgs *>(m->step_args);
+    launch_k(k->fn, dim3(m->step_nb), dim3(kT), 0, s, e0, e1, args);
+    PTMI_HIP(hipGetLastError());
+    return PTMI_OK;
+}
+
+}  // namespace ptmi
+
+using namespace ptmi;
+
+extern "C" int ptmi_model_step_stamps(ptmi_model_t *m, uint64_t *out, size_t n, int *n_stamps, int *n_wg) {
+    if (!m || !n_stamps || !n_wg) return set_error(PTMI_ERR_ARG, "NULL argument");
+    *n_stamps = m->step_n_stamps;
+    *n_wg = m->step_nb;
+    if (!m->step_stamps) return set_error(PTMI_ERR_STATE, "no stage stamps: create the model with PTMI_STEP_STAMPS=1");
+    const size_t need = (size_t)m->step_nb * m->step_n_stamps;
+    if (!out || n < need) return set_error(PTMI_ERR_ARG, "stamp buffer holds %zu of %zu words", n, need);
+    PTMI_HIP(hipStreamSynchronize(lib_stream()));
+    PTMI_HIP(hipMemcpy(out, m->step_stamps, need * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    return PTMI_OK;
+}

@@ -13,6 +13,9 @@ struct DecodeCtl {
     int pos;         // current position
     int n_prompt;    // generate: positions < n_prompt-1 force prompt[pos+1]
     int next;        // argmax of the last step's logits
+    // The host writes only the four fields above.
+    int seq;         // steps run by the one-kernel decode step (its tags are seq + 1)
+    int err;         // nonzero: a wait of the one-kernel step timed out
 };
 
 struct TrainState;   // defined by the training unit
@@ -40,10 +43,24 @@ struct ptmi_model {
     bool eager = false;                  // PTMI_DECODE_EAGER=1: no graph
     bool prefetch = true;                // PTMI_NO_PREFETCH=1: no L2 prefetch blocks
     float *sink = nullptr;               // prefetch load sink
+    // one-kernel decode step (null step_mem: the multi-kernel step)
+    uint64_t *step_mem = nullptr;        // its tagged exchange buffers
+    void *step_args = nullptr;           // its argument block (device memory)
+    int step_nb = 0;                     // its workgroups
+    int step_chunk = 0, step_chunks = 0; // attention positions per unit, units per head
+    uint64_t *step_stamps = nullptr;     // stage stamps (PTMI_STEP_STAMPS=1)
+    int step_n_stamps = 0;
     ptmi::TrainState *train = nullptr;
 };
 
 namespace ptmi {
 int  train_create(ptmi_model *m);
 void train_destroy(ptmi_model *m);
+// 1/pt_sqrtf(head_dim) evaluated on the host (llama2.c:137)
+float host_att_scale(int head_dim);
+// The one-kernel decode step: set up (when PTMI_DECODE_STEP=1 and the shape
+// has an instantiated kernel), tear down, enqueue one step.
+int  decode_step_create(ptmi_model *m);
+void decode_step_destroy(ptmi_model *m);
+int  launch_decode_step(ptmi_model *m, hipStream_t s, hipEvent_t e0, hipEvent_t e1);
 }

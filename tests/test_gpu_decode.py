@@ -4,6 +4,10 @@ Golden tokens come from the reference's own host build (tests/golden/
 make_golden.py).  Greedy tokens must be IDENTICAL over the full runs
 (256 positions for 15M, 1024 for 42M/110M); logits are compared with the
 oracle at a relative tolerance (matvec reduction order differs).
+
+Both decode paths are held to this: the captured multi-kernel step (the
+default) and the one-kernel step (PTMI_DECODE_STEP=1, read when a model is
+created).
 """
 import ctypes
 import hashlib
@@ -20,6 +24,21 @@ pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
+@pytest.fixture(params=["multi_kernel", "one_kernel"])
+def decode_path(request, monkeypatch):
+    monkeypatch.setenv("PTMI_DECODE_STEP", "1" if request.param == "one_kernel" else "0")
+    return request.param
+
+
+def check_path(m, decode_path):
+    """The model ran the decode path the test was parametrized for (one
+    profiled step from position 0: a "step" launch only on the one-kernel
+    path)."""
+    m.reset_kv()
+    prof = m.profile(1, 1)
+    assert prof["step"][1] == (1 if decode_path == "one_kernel" else 0), prof["step"]
+
+
 def fixture(name):
     return json.load(open(os.path.join(ROOT, "tests", "golden", f"decode_{name}.json")))
 
@@ -31,7 +50,7 @@ def model_for(name):
     return blob
 
 
-def test_logits_track_oracle_15M():
+def test_logits_track_oracle_15M(decode_path):
     """Every one of the 256 positions (4 attention chunks of 64 positions,
     so the multi-chunk softmax combine runs from position 64 on): logits
     within 1e-5 of max |logit| of the oracle's, same argmax."""
@@ -51,12 +70,13 @@ def test_logits_track_oracle_15M():
         assert a == b == int(np.argmax(ref_lg))
         tok = prompt[pos + 1] if pos + 1 < len(prompt) else a
     assert m.pos() == 256
+    check_path(m, decode_path)
     m.close()
     om.close()
 
 
 @pytest.mark.parametrize("name", ["stories15M", "stories42M", "stories110M"])
-def test_long_context_logits_match_reference(name):
+def test_long_context_logits_match_reference(name, decode_path):
     """Logits at positions across the attention chunks (128 positions per
     chunk at seq_len 1024: 127 | 128 on either side of a chunk boundary,
     511/512, the full cache at 1023), teacher-forced on the golden tokens,
@@ -85,11 +105,12 @@ def test_long_context_logits_match_reference(name):
         norm, ref_norm = np.sqrt((lg64 * lg64).sum()), np.sqrt(r["sumsq"])
         assert abs(norm - ref_norm) <= 1e-5 * ref_norm, pos
         assert abs(lg64.sum() - r["sum"]) <= 1e-5 * np.sqrt(len(lg)) * ref_norm, pos
+    check_path(m, decode_path)
     m.close()
 
 
 @pytest.mark.parametrize("name", ["stories15M", "stories42M", "stories110M"])
-def test_greedy_tokens_identical_to_reference(name):
+def test_greedy_tokens_identical_to_reference(name, decode_path):
     fx = fixture(name)
     blob = model_for(name)
     m = pa.Model(blob)
@@ -97,10 +118,11 @@ def test_greedy_tokens_identical_to_reference(name):
     assert len(toks) == len(fx["tokens"])
     first_diff = next((i for i, (a, b) in enumerate(zip(toks, fx["tokens"])) if a != b), None)
     assert first_diff is None, f"first divergence at position {first_diff}"
+    check_path(m, decode_path)
     m.close()
 
 
-def test_forward_step_matches_generate_and_reset():
+def test_forward_step_matches_generate_and_reset(decode_path):
     fx = fixture("stories15M")
     blob = model_for("stories15M")
     m = pa.Model(blob)
@@ -109,10 +131,11 @@ def test_forward_step_matches_generate_and_reset():
     m.reset_kv()
     assert m.pos() == 0
     assert greedy_tokens(m.forward_step, fx["prompt"], 16) == fx["tokens"][:16]
+    check_path(m, decode_path)
     m.close()
 
 
-def test_generate_stop_and_clamp_semantics():
+def test_generate_stop_and_clamp_semantics(decode_path):
     """pt_text.c:321-322 clamp, :344-347 forced prefill, :354 stop on 1/2."""
     cfg = (64, 160, 2, 4, 4, 512, 24)
     blob = pa.synth_model(cfg, 5, 0.3)
@@ -124,6 +147,7 @@ def test_generate_stop_and_clamp_semantics():
     m = pa.Model(blob)
     got = m.generate(prompt, 100, stop_on_eos=True)
     assert list(got) == list(out[:n])
+    check_path(m, decode_path)
     m.close()
     om.close()
 
@@ -164,13 +188,72 @@ def test_reference_forward_with_ptmi_matvec_dropin():
         L.ptmi_unregister_weights(P(blob))
 
 
-def test_profile_roles_cover_every_launch():
+@pytest.mark.parametrize("one_kernel", [True, False])
+def test_profile_roles_cover_every_launch(one_kernel, monkeypatch):
+    """The one-kernel step is one launch per token (role "step"); the
+    multi-kernel step (PTMI_DECODE_STEP=0) is 5 launches per layer plus the
+    classifier and the argmax."""
+    monkeypatch.setenv("PTMI_DECODE_STEP", "1" if one_kernel else "0")
     cfg = pa.STORIES["stories15M"]
     blob = model_for("stories15M")
     m = pa.Model(blob)
     prof = m.profile(1, 4)
     Lyr = cfg[2]
-    assert prof["qkv"][1] == prof["attention"][1] == prof["wo"][1] == prof["w13"][1] == prof["w2"][1] == 4 * Lyr
-    assert prof["classifier"][1] == prof["argmax"][1] == 4
-    assert all(ms > 0 for ms, _ in prof.values())
+    if one_kernel:
+        assert prof["step"][1] == 4 and prof["step"][0] > 0
+        assert all(cnt == 0 for r, (ms, cnt) in prof.items() if r != "step")
+    else:
+        assert prof["qkv"][1] == prof["attention"][1] == prof["wo"][1] == prof["w13"][1] == prof["w2"][1] == 4 * Lyr
+        assert prof["classifier"][1] == prof["argmax"][1] == 4 and prof["step"][1] == 0
+        assert all(ms > 0 for r, (ms, _) in prof.items() if r != "step")
+    m.close()
+
+
+def test_one_kernel_step_stage_stamps(monkeypatch):
+    """PTMI_STEP_STAMPS=1: per workgroup, kernel start, then for every stage
+    the end of its wait and the end of its work, in time order."""
+    monkeypatch.setenv("PTMI_DECODE_STEP", "1")
+    monkeypatch.setenv("PTMI_STEP_STAMPS", "1")
+    cfg = pa.STORIES["stories15M"]
+    m = pa.Model(model_for("stories15M"))
+    m.forward_step(1)
+    m.forward_step(5)
+    st = m.step_stamps().astype(np.int64)
+    L = cfg[2]
+    assert st.shape[1] == 1 + 10 * L + 4 and st.shape[0] >= 64
+    assert np.all(st[:, 0] > 0)
+    for row in st:
+        seen = row[row > 0]
+        assert np.all(np.diff(seen) >= 0)          # a workgroup's stamps are in time order
+    blocks_w13 = (2 * cfg[1] + 15) // 16            # 16 interleaved w1|w3 rows per workgroup pass
+    took_w13 = st[:, 7 + 10 * (L - 1)] > 0
+    assert took_w13.sum() == min(len(st), blocks_w13) and took_w13[:blocks_w13].all()
+    assert st[0, 4 + 10 * L] > 0                   # workgroup 0 finished the step
+    m.close()
+    monkeypatch.setenv("PTMI_STEP_STAMPS", "0")
+    m = pa.Model(model_for("stories15M"))
+    with pytest.raises(pa.PtmiError):
+        m.step_stamps()
+    m.close()
+
+
+def test_one_kernel_step_timeout_is_reported(monkeypatch):
+    """A wait of the one-kernel step that runs out is an error of the call,
+    forced here from the host with a one-tick wait bound: the kernel still
+    exits normally (every wait is bounded and checks the shared error word),
+    the call raises, and the model stays usable for the next call."""
+    monkeypatch.setenv("PTMI_DECODE_STEP", "1")
+    monkeypatch.setenv("PTMI_STEP_WAIT_TICKS", "1")
+    m = pa.Model(model_for("stories15M"))
+    for _ in range(2):
+        with pytest.raises(pa.PtmiError) as e:
+            m.forward_step(1)
+        assert "timed out" in str(e.value)
+    with pytest.raises(pa.PtmiError):
+        m.generate(np.array([1, 2, 3], np.int32), 8, stop_on_eos=False)
+    m.close()
+    monkeypatch.delenv("PTMI_STEP_WAIT_TICKS")
+    fx = fixture("stories15M")
+    m = pa.Model(model_for("stories15M"))
+    assert greedy_tokens(m.forward_step, fx["prompt"], 16) == fx["tokens"][:16]
     m.close()
