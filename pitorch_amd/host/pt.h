@@ -124,9 +124,11 @@ int  pt_generate_ids(pt_context_t *ctx, const int *prompt, int n_prompt,
                      int max_tokens, int *out);
 
 /* ── profiling (pt.c:322-335): with a trace enabled, pt_train_step runs
- * the device step without its graph and records the reference's spans
- * (train_step, zero_grads, forward, layer, qkv, attention, wo, ffn,
- * classifier, loss, backward, weight_grads, embedding, sgd) with HIP-event
+ * the device step without its graph and records the reference's span
+ * tree (train_step, zero_grads, forward, embedding, layer, qkv,
+ * attention, ffn, classifier, loss, backward, cls_transpose,
+ * cls_weight_grad, transpose, wo, sgd; pt_train.c:171-866), plus
+ * weight_grads (the layers' dW GEMMs in one launch), with HIP-event
  * times.  preallocated = NULL: the context allocates (and pt_free frees) it. */
 void pt_enable_trace(pt_context_t *ctx, pt_trace_t *preallocated);
 void pt_disable_trace(pt_context_t *ctx);
