@@ -221,24 +221,27 @@ MFMA_FP32_PEAK_TFLOPS = 157.3
 
 
 def train_gemm_shapes(cfg, T):
-    """Every GEMM of one pt_train_step at this config (op, M, N, K, count):
-    forward Y = X W^T (NT), backward dX = dY W (NN) and dW += dY^T X (TN),
-    R = T-1 backward rows; QKV and w1|w3 are fused as in the device layout."""
+    """Every GEMM of one pt_train_step at this config (op, M, N, K, count,
+    accumulate): forward Y = X W^T (NT), backward dX = dY W (NN) and
+    dW = dY^T X (TN), R = T-1 backward rows; QKV and w1|w3 are fused as in
+    the device layout.  `accumulate` is what the device step does: the Wo
+    and w2 forward GEMMs add the residual stream; every other GEMM writes
+    (gradients are written, not accumulated into zeroed buffers)."""
     D, H, L, _, _, V, _ = cfg
     R = T - 1
     QS = 3 * D
-    fwd = [(2, T, QS, D, L), (2, T, D, D, L), (2, T, 2 * H, D, L), (2, T, D, H, L), (2, T, V, D, 1)]
-    dx = [(0, R, D, V, 1), (0, R, H, D, L), (0, R, D, 2 * H, L), (0, R, D, D, L), (0, R, D, QS, L)]
-    dw = [(1, V, D, R, 1), (1, D, H, R, L), (1, 2 * H, D, R, L), (1, D, D, R, L), (1, QS, D, R, L)]
+    fwd = [(2, T, QS, D, L, 0), (2, T, D, D, L, 1), (2, T, 2 * H, D, L, 0), (2, T, D, H, L, 1), (2, T, V, D, 1, 0)]
+    dx = [(0, R, D, V, 1, 0), (0, R, H, D, L, 0), (0, R, D, 2 * H, L, 0), (0, R, D, D, L, 0), (0, R, D, QS, L, 0)]
+    dw = [(1, V, D, R, 1, 0), (1, D, H, R, L, 0), (1, 2 * H, D, R, L, 0), (1, D, D, R, L, 0), (1, QS, D, R, L, 0)]
     return fwd + dx + dw
 
 
 def bench_train(pa, reps=20):
     """stories15M training step (config 5): ms/step of the device pt_train_step
     (hipGraph per step) and fp32-MFMA utilisation of its GEMMs; each GEMM
-    shape is captured `reps` times back to back in a hipGraph on the library
-    stream and timed with HIP events around graph replays, so host launch
-    cost is not in the figure."""
+    shape (with the step's accumulate flag) is captured `reps` times back to
+    back in a hipGraph on the library stream and timed with HIP events
+    around graph replays, so host launch cost is not in the figure."""
     import numpy as np
     from pitorch_amd._hip import DeviceArray, Event, Graph
 
@@ -256,14 +259,14 @@ def bench_train(pa, reps=20):
     m.close()
     stream = L.ptmi_stream()
     shapes = train_gemm_shapes(cfg, T)
-    maxA = max(M * K for _, M, N, K, _ in shapes)
-    maxB = max(K * N for _, M, N, K, _ in shapes)
-    maxC = max(M * N for _, M, N, K, _ in shapes)
+    maxA = max(M * K for _, M, N, K, _, _ in shapes)
+    maxB = max(K * N for _, M, N, K, _, _ in shapes)
+    maxC = max(M * N for _, M, N, K, _, _ in shapes)
     A = DeviceArray.from_host(pa.seed_uniform(1, maxA))
     B = DeviceArray.from_host(pa.seed_uniform(2, maxB))
     C = DeviceArray(maxC)
     total_flop, total_ms, rows = 0.0, 0.0, []
-    for op, M, N, K, count in shapes:
+    for op, M, N, K, count, acc in shapes:
         lda = K if op != 1 else M
         ldb = N if op != 2 else K
         pa._ffi.check(L.ptmi_gemm_dev(op, A.ptr, lda, B.ptr, ldb, C.ptr, N, M, N, K, 0, None))
@@ -271,7 +274,7 @@ def bench_train(pa, reps=20):
 
         def enqueue():
             for _ in range(reps):
-                pa._ffi.check(L.ptmi_gemm_dev(op, A.ptr, lda, B.ptr, ldb, C.ptr, N, M, N, K, 1, stream))
+                pa._ffi.check(L.ptmi_gemm_dev(op, A.ptr, lda, B.ptr, ldb, C.ptr, N, M, N, K, acc, stream))
 
         g = Graph(stream, enqueue)
         g.launch()
@@ -285,7 +288,7 @@ def bench_train(pa, reps=20):
         flop = 2.0 * M * N * K
         total_flop += flop * count
         total_ms += ms * count
-        rows.append({"op": "NN TN NT".split()[op], "M": M, "N": N, "K": K, "count": count,
+        rows.append({"op": "NN TN NT".split()[op], "M": M, "N": N, "K": K, "count": count, "acc": acc,
                      "us": round(ms * 1e3, 2), "TFLOPs": round(flop / (ms * 1e-3) / 1e12, 2)})
     for a in (A, B, C):
         a.free()
@@ -337,14 +340,14 @@ def pmc_gemm(pa, reps):
 
     L = pa.load_ptmi()
     shapes = train_gemm_shapes(pa.STORIES["stories15M"], 256)
-    A = DeviceArray.from_host(pa.seed_uniform(1, max(M * K for _, M, N, K, _ in shapes)))
-    B = DeviceArray.from_host(pa.seed_uniform(2, max(K * N for _, M, N, K, _ in shapes)))
-    C = DeviceArray(max(M * N for _, M, N, K, _ in shapes))
-    for op, M, N, K, _ in shapes:
+    A = DeviceArray.from_host(pa.seed_uniform(1, max(M * K for _, M, N, K, _, _ in shapes)))
+    B = DeviceArray.from_host(pa.seed_uniform(2, max(K * N for _, M, N, K, _, _ in shapes)))
+    C = DeviceArray(max(M * N for _, M, N, K, _, _ in shapes))
+    for op, M, N, K, _, acc in shapes:
         lda = K if op != 1 else M
         ldb = N if op != 2 else K
         for _ in range(reps):
-            pa._ffi.check(L.ptmi_gemm_dev(op, A.ptr, lda, B.ptr, ldb, C.ptr, N, M, N, K, 0, None))
+            pa._ffi.check(L.ptmi_gemm_dev(op, A.ptr, lda, B.ptr, ldb, C.ptr, N, M, N, K, acc, None))
         pa._ffi.check(L.ptmi_sync())
     for a in (A, B, C):
         a.free()

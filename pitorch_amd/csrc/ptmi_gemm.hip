@@ -152,6 +152,75 @@ __device__ __forceinline__ void store_tile(float (*S)[R], int tid, const float (
     }
 }
 
+// Epilogue of one wave's FM x FN 16x16 blocks: block (i, j) of the wave
+// covers rows mb + 16i .. and columns nb + 16j ..; lane l holds rows
+// 4*(l/16) + r, column l%16 of it (the 16x16x4 MFMA result layout).
+template <int EPI, int FM, int FN>
+__device__ __forceinline__ void gemm_store(const GemmArgs &g, const floatx4 (&acc)[FM][FN], int mb, int nb, int z,
+                                           int li, int lk) {
+    const float lrv = g.upd ? *g.lr : 0.0f;
+    // C[4*(l/16)+r][l%16] of each 16x16 block; columns n and n^1 of a row sit
+    // in lanes l and l^1, which the fused epilogues pair with a DPP swap
+    // (every lane reaches it: bounds are checked after).
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int n = nb + j * 16 + li;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = mb + i * 16 + 4 * lk + r;
+                float v = acc[i][j][r];
+                if constexpr (EPI == GEMM_EPI_ROPE) {
+                    // RoPE of the q and k columns at position m (pt_ops.c:33-49;
+                    // training forward pt_train.c:217)
+                    const float pv = dpp_xor1(v);
+                    if (n < 2 * g.epi.rope_dim) {
+                        const int ip = (n < g.epi.rope_dim ? n : n - g.epi.rope_dim) & ~1;
+                        float c, sn;
+                        d_rope_cs(ip, g.epi.head_dim, m, &c, &sn);
+                        v = (n & 1) ? pv * sn + v * c : v * c - pv * sn;
+                    }
+                } else if constexpr (EPI == GEMM_EPI_SWIGLU) {
+                    // columns (2i, 2i+1) = (h1, h3): out[m][i] = (h1*sigmoid(h1))*h3,
+                    // the training form of silu (pt_train.c:280-284)
+                    const float pv = dpp_xor1(v);
+                    if (!(n & 1) && n < g.N && m < g.M) {
+                        const float sig = 1.0f / (1.0f + d_expf(-v));
+                        g.epi.out[(long)m * g.epi.ld + (n >> 1)] = (v * sig) * pv;
+                    }
+                }
+                if constexpr (EPI == GEMM_EPI_SWIGLU_BWD) {
+                    // silu*gate backward (pt_train.c:696-721) into the interleaved
+                    // (d_h1, d_h3) columns, plus silu(h1)*h3 for dW2
+                    if (n < g.N && m < g.M) {
+                        const float *hp = g.epi.aux + (long)m * g.epi.aux_ld + 2 * n;
+                        const float h1 = hp[0], h3 = hp[1];
+                        const float sig = 1.0f / (1.0f + d_expf(-h1));
+                        const float silu_val = h1 * sig;
+                        g.epi.out2[(long)m * g.epi.ld2 + n] = silu_val * h3;
+                        const float d_silu = v * h3;
+                        float *dp = g.epi.out + (long)m * g.epi.ld + 2 * n;
+                        dp[1] = v * silu_val;
+                        dp[0] = d_silu * sig * (1.0f + h1 * (1.0f - sig));
+                    }
+                    continue;                                   // d_sh itself is not kept
+                }
+                if (n >= g.N || m >= g.M) continue;
+                if (g.partial) {
+                    g.partial[((long)z * g.M + m) * g.N + n] = v;
+                } else {
+                    const long o = (long)m * g.ldc + n;
+                    const float cv = g.accumulate ? g.Cin[o] + v : v;
+                    g.C[o] = cv;
+                    // sgd_step (pt_train.c:870-873) on the weight this gradient belongs to
+                    if (g.upd && !(g.keep && ((g.keep[m >> 5] >> (m & 31)) & 1u))) g.upd[o] -= lrv * cv;
+                }
+            }
+        }
+    }
+}
+
 // One TMxTN output tile of g at (m0, n0) over K range split z.  The LDS
 // tiles use the swizzled layout of lds_col.
 template <bool AT, bool BT, int TM, int TN, int P, bool VEC, int EPI = GEMM_EPI_NONE>
@@ -243,67 +312,165 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
         }
     }
 
-    const float lrv = g.upd ? *g.lr : 0.0f;
-    // C[4*(l/16)+r][l%16] of each 16x16 block; columns n and n^1 of a row sit
-    // in lanes l and l^1, which the fused epilogues pair with a DPP swap
-    // (every lane reaches it: bounds are checked after).
+    gemm_store<EPI, FM, FN>(g, acc, m0 + wm * (TM / 2), n0 + wn * (TN / 2), z, li, lk);
+}
+
+// ── Direct-to-LDS tiles for the large training GEMMs ─────────────────────
+// gfx950's global_load_lds_dwordx4 moves a 16-byte chunk per lane from
+// global memory straight into LDS, at the wave's LDS base + 16*lane (lane
+// layout checked on the MI355X).  No staging registers and no LDS store
+// instructions, so 128- and 256-row tiles fit with two waves per SIMD.
+// Each operand tile keeps its global layout in LDS, permuted in whole
+// 16-byte chunks (the only granularity a DMA load can place):
+//  * k-contiguous operands ([i][k]: A of NN/NT, B^T of NT): rows of BK=32
+//    floats, chunk c of row i at slot c ^ (i & 7).  A lane reads the 4 k of
+//    its row for 4 MFMA steps as one b128 (lane group g takes k = 4g..4g+3 of
+//    each 16-k group): the 8 lanes of an access phase hit 8 distinct chunk
+//    slots, so there are no bank conflicts;
+//  * k-major operands ([k][i]: A^T of TN, B of NN/TN): rows of TI floats,
+//    the column XOR-ed with 16 in rows whose bit 2 of k is set; the two k
+//    rows a half-wave reads (g = 0, 1) then sit 16 banks apart.
+// Both operands use the same order of k inside a 16-k group (lane group g,
+// step s -> k = 4g + s), so every product pairs the same k.
+// Two LDS stages: the loads of tile s+1 are issued before the MFMAs of tile
+// s and waited for (vmcnt, in order) at the next step's barrier.
+// Measured on the MI355X against the register-ring kernel (launches back to
+// back, same inputs, same bits): NT 256x32000x288 with 256x128 tiles, 47.2
+// vs 51.3 us; TN 32000x288x255 with 64x96 tiles, 55.5 vs 58.7 us.  Deeper
+// stage rings, 64-k stages, and loads interleaved one per MFMA k step were
+// all slower; so were these tiles on the per-layer shapes (5-16 us against
+// 5-10 us) and on the long-K NN (split K, 68 vs 60 us).
+constexpr int kDlStages = 2;
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {                   // s_waitcnt vmcnt(N), other counters untouched
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// This thread's DMA loads of one operand tile (TI rows of the M or N side x
+// BK k, k0 = first k) into `lds`; 64-chunk regions are dealt to the NW
+// waves round-robin, and a wave with no region left loads zeros into `junk`
+// so that every wave issues the same number of loads.
+template <bool KMAJOR, int TI, int NW>
+__device__ __forceinline__ void dl_issue(const float *P, long ld, int ilim, int i0, int k0, int kend, float *lds,
+                                         float *junk, int wave, int lane) {
+    constexpr int CPI = BK / 4;                          // chunks per row, k-contiguous layout
+    constexpr int R = TI * CPI / 64;
 #pragma unroll
-    for (int i = 0; i < FM; i++) {
+    for (int j = 0; j < (R + NW - 1) / NW; j++) {
+        const int rgn = j * NW + wave;
+        const bool real = rgn < R;                       // wave-uniform
+        const int S = (real ? rgn : 0) * 64 + lane;      // chunk slot in the tile
+        const float *src = g_gemm_zero;
+        if constexpr (KMAJOR) {
+            constexpr int CPR = TI / 4;                  // chunks per LDS row
+            const int k = S / CPR, t = S % CPR;
+            const int i = i0 + 4 * (t ^ (((k >> 2) & 1) << 2)), kk = k0 + k;
+            if (real && kk < kend && i < ilim) src = P + (long)kk * ld + i;
+        } else {
+            const int i = S / CPI, t = S % CPI;
+            const int ii = i0 + i, kk = k0 + 4 * (t ^ (i & 7));
+            if (real && ii < ilim && kk < kend) src = P + (long)ii * ld + kk;
+        }
+        typedef const void __attribute__((address_space(1))) *gptr;
+        typedef void __attribute__((address_space(3))) *lptr;
+        __builtin_amdgcn_global_load_lds((gptr)src, (lptr)(real ? lds + rgn * 256 : junk), 16, 0, 0);
+    }
+}
+
+// One TMxTN output tile on WM x WN waves (each (TM/WM) x (TN/WN)).
+// AK: A stored [K][M] (TN); BKM: B stored [K][N] (NN, TN).
+template <bool AK, bool BKM, int TM, int TN, int WM, int WN, int EPI = GEMM_EPI_NONE>
+__device__ __forceinline__ void gemm_tile_dl(const GemmArgs &g, int m0, int n0, int z) {
+    constexpr int NW = WM * WN, NS = kDlStages, CPI = BK / 4;
+    constexpr int FM = TM / WM / 16, FN = TN / WN / 16;
+    static_assert(FM * WM * 16 == TM && FN * WN * 16 == TN, "tile");
+    constexpr int STAGE = (TM + TN) * BK;
+    constexpr int LPT = (TM * CPI / 64 + NW - 1) / NW + (TN * CPI / 64 + NW - 1) / NW;
+    static_assert((NS - 2) * LPT < 64, "vmcnt");
+    __shared__ __align__(16) float smem[NS * STAGE + 256];
+    float *junk = smem + NS * STAGE;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int li = lane & 15, lk = lane >> 4;
+    const int kb = z * g.k_per_split;
+    const int kend = min(g.K, kb + g.k_per_split);
+    const int nk = kb < kend ? (kend - kb + BK - 1) / BK : 0;
+
+    floatx4 acc[FM][FN];
 #pragma unroll
-        for (int j = 0; j < FN; j++) {
-            const int n = n0 + wn * (TN / 2) + j * 16 + li;
+    for (int i = 0; i < FM; i++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = m0 + wm * (TM / 2) + i * 16 + 4 * lk + r;
-                float v = acc[i][j][r];
-                if constexpr (EPI == GEMM_EPI_ROPE) {
-                    // RoPE of the q and k columns at position m (pt_ops.c:33-49;
-                    // training forward pt_train.c:217)
-                    const float pv = dpp_xor1(v);
-                    if (n < 2 * g.epi.rope_dim) {
-                        const int ip = (n < g.epi.rope_dim ? n : n - g.epi.rope_dim) & ~1;
-                        float c, sn;
-                        d_rope_cs(ip, g.epi.head_dim, m, &c, &sn);
-                        v = (n & 1) ? pv * sn + v * c : v * c - pv * sn;
-                    }
-                } else if constexpr (EPI == GEMM_EPI_SWIGLU) {
-                    // columns (2i, 2i+1) = (h1, h3): out[m][i] = (h1*sigmoid(h1))*h3,
-                    // the training form of silu (pt_train.c:280-284)
-                    const float pv = dpp_xor1(v);
-                    if (!(n & 1) && n < g.N && m < g.M) {
-                        const float sig = 1.0f / (1.0f + d_expf(-v));
-                        g.epi.out[(long)m * g.epi.ld + (n >> 1)] = (v * sig) * pv;
-                    }
+        for (int j = 0; j < FN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    auto issue = [&](int t) {
+        float *st = smem + (t % NS) * STAGE;
+        const int k0 = kb + t * BK;
+        dl_issue<AK, TM, NW>(g.A, g.lda, g.M, m0, k0, kend, st, junk, wave, lane);
+        dl_issue<BKM, TN, NW>(g.B, g.ldb, g.N, n0, k0, kend, st + TM * BK, junk, wave, lane);
+    };
+    // MFMA operands of 16-k group q: lane group lk takes k = 16q + 4lk + s
+    // in step s (a float4 per fragment, one k per component).
+    auto read_a = [&](const float *st, int q, floatx4 (&a)[FM]) {
+#pragma unroll
+        for (int f = 0; f < FM; f++) {
+            const int i = wm * (TM / WM) + f * 16 + li;
+            if constexpr (AK) {
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    const int k = 16 * q + 4 * lk + s;
+                    a[f][s] = st[k * TM + (i ^ (((k >> 2) & 1) << 4))];
                 }
-                if constexpr (EPI == GEMM_EPI_SWIGLU_BWD) {
-                    // silu*gate backward (pt_train.c:696-721) into the interleaved
-                    // (d_h1, d_h3) columns, plus silu(h1)*h3 for dW2
-                    if (n < g.N && m < g.M) {
-                        const float *hp = g.epi.aux + (long)m * g.epi.aux_ld + 2 * n;
-                        const float h1 = hp[0], h3 = hp[1];
-                        const float sig = 1.0f / (1.0f + d_expf(-h1));
-                        const float silu_val = h1 * sig;
-                        g.epi.out2[(long)m * g.epi.ld2 + n] = silu_val * h3;
-                        const float d_silu = v * h3;
-                        float *dp = g.epi.out + (long)m * g.epi.ld + 2 * n;
-                        dp[1] = v * silu_val;
-                        dp[0] = d_silu * sig * (1.0f + h1 * (1.0f - sig));
-                    }
-                    continue;                                   // d_sh itself is not kept
-                }
-                if (n >= g.N || m >= g.M) continue;
-                if (g.partial) {
-                    g.partial[((long)z * g.M + m) * g.N + n] = v;
-                } else {
-                    const long o = (long)m * g.ldc + n;
-                    const float cv = g.accumulate ? g.Cin[o] + v : v;
-                    g.C[o] = cv;
-                    // sgd_step (pt_train.c:870-873) on the weight this gradient belongs to
-                    if (g.upd && !(g.keep && ((g.keep[m >> 5] >> (m & 31)) & 1u))) g.upd[o] -= lrv * cv;
-                }
+            } else {
+                a[f] = *reinterpret_cast<const floatx4 *>(st + (i * CPI + ((4 * q + lk) ^ (i & 7))) * 4);
             }
         }
+    };
+    auto read_b = [&](const float *st, int q, floatx4 (&b)[FN]) {
+        const float *sb = st + TM * BK;
+#pragma unroll
+        for (int h = 0; h < FN; h++) {
+            const int i = wn * (TN / WN) + h * 16 + li;
+            if constexpr (BKM) {
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    const int k = 16 * q + 4 * lk + s;
+                    b[h][s] = sb[k * TN + (i ^ (((k >> 2) & 1) << 4))];
+                }
+            } else {
+                b[h] = *reinterpret_cast<const floatx4 *>(sb + (i * CPI + ((4 * q + lk) ^ (i & 7))) * 4);
+            }
+        }
+    };
+
+    if (nk > 0) issue(0);
+    for (int s = 0; s < nk; s++) {
+        // tile s has landed in every wave's share once each wave's own
+        // loads are done (vmcnt) and all waves passed the barrier; the
+        // barrier also ends every read of the stage tile s+1 overwrites
+        wait_vmcnt<0>();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (s + 1 < nk) issue(s + 1);
+        const float *st = smem + (s % NS) * STAGE;
+        floatx4 a[2][FM], b[2][FN];
+        read_a(st, 0, a[0]);
+        read_b(st, 0, b[0]);
+        read_a(st, 1, a[1]);
+        read_b(st, 1, b[1]);
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+#pragma unroll
+            for (int ss = 0; ss < 4; ss++)
+#pragma unroll
+                for (int f = 0; f < FM; f++)
+#pragma unroll
+                    for (int h = 0; h < FN; h++)
+                        acc[f][h] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[q][f][ss], b[q][h][ss], acc[f][h], 0, 0, 0);
     }
+    gemm_store<EPI, FM, FN>(g, acc, m0 + wm * (TM / WM), n0 + wn * (TN / WN), z, li, lk);
 }
 
 // Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its
@@ -331,6 +498,21 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
         else n = u / gy, m = u - n * gy;
     }
     gemm_tile<AT, BT, TM, TN, P, VEC, EPI>(g, m * TM, n * TN, z);
+}
+
+// The direct-to-LDS GEMM (grid and tile order as k_gemm).
+template <bool AK, bool BKM, int TM, int TN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void k_gemm_dl(GemmArgs g) {
+    const int gx = gridDim.x, gy = gridDim.y, per_z = gx * gy, total = per_z * gridDim.z;
+    int m = blockIdx.y, n = blockIdx.x, z = blockIdx.z;
+    if (total >= kXcdGrid) {                                        // uniform
+        const int t = xcd_tile(blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z), total);
+        z = t / per_z;
+        const int u = t - z * per_z;
+        if (g.M > g.N) m = u / gx, n = u - m * gx;
+        else n = u / gy, m = u - n * gy;
+    }
+    gemm_tile_dl<AK, BKM, TM, TN, WM, WN>(g, m * TM, n * TN, z);
 }
 
 // Grouped TN GEMMs (32x32 tiles, whole K): block b runs tile
@@ -457,7 +639,20 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
              k_gemm<false, false, 64, 64, kRing64, true, GEMM_EPI_SWIGLU_BWD>}};
         fn = ek == GEMM_EPI_SWIGLU_BWD ? fused_nn[big][vec] : fused[ek == GEMM_EPI_SWIGLU][big][vec];
     }
-    hipLaunchKernelGGL(fn, grid, dim3(256), 0, s, g);
+    int threads = 256;
+    // The large whole-K GEMMs without a fused epilogue (the classifier's
+    // forward and weight gradient) take the direct-to-LDS tiles.
+    if (vec && ek == GEMM_EPI_NONE && splits == 1 && (long)M * N >= (4L << 20)) {
+        if (op == 2 && M >= 192) {
+            grid = dim3((unsigned)((N + 127) / 128), (unsigned)((M + 255) / 256), 1);
+            fn = k_gemm_dl<false, false, 256, 128, 4, 2>;
+            threads = 512;
+        } else if (op == 1) {
+            grid = dim3((unsigned)((N + 95) / 96), (unsigned)((M + 63) / 64), 1);
+            fn = k_gemm_dl<true, true, 64, 96, 2, 2>;
+        }
+    }
+    hipLaunchKernelGGL(fn, grid, dim3(threads), 0, s, g);
     PTMI_HIP(hipGetLastError());
     if (splits > 1 && defer) {
         *defer = SplitK{ws, splits, (long)M * N};

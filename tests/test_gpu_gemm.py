@@ -192,6 +192,32 @@ def test_gemm_dev_large_grids(op, M, N, K):
         a.free()
 
 
+# The direct-to-LDS tiles (NT with M >= 192 on 256x128 tiles, TN on 64x96;
+# outputs of 4M elements and more, whole K, no fused epilogue):
+# integer-exact at the classifier shapes of config 5, with and without
+# accumulate, and on ragged M, N and K.
+@pytest.mark.parametrize("op,M,N,K,acc", [(2, 256, 32000, 288, 0), (2, 256, 32000, 288, 1), (2, 193, 21845, 36, 1),
+                                          (1, 32000, 288, 255, 0), (1, 32000, 288, 255, 1), (1, 16388, 260, 7, 0)])
+def test_gemm_dev_direct_lds_exact(op, M, N, K, acc):
+    if op == 1:
+        A, B = ints((K, M), 21), ints((K, N), 22)
+        ref = A.T.astype(np.float64) @ B.astype(np.float64)
+    else:
+        A, B = ints((M, K), 23), ints((N, K), 24)
+        ref = A.astype(np.float64) @ B.T.astype(np.float64)
+    C0 = ints((M, N), 25) if acc else np.full((M, N), np.nan, np.float32)
+    if acc:
+        ref = ref + C0
+    dA, dB, dC = DeviceArray.from_host(A), DeviceArray.from_host(B), DeviceArray.from_host(C0)
+    L = pa.load_ptmi()
+    assert L.ptmi_gemm_dev(op, dA.ptr, A.shape[1], dB.ptr, B.shape[1], dC.ptr, N, M, N, K, acc, None) == 0
+    assert L.ptmi_sync() == 0
+    got = dC.download().reshape(M, N)
+    assert np.array_equal(got, ref.astype(np.float32))
+    for a in (dA, dB, dC):
+        a.free()
+
+
 def test_gemm_errors():
     L = pa.load_ptmi()
     A = np.ones((4, 4), np.float32)
