@@ -59,11 +59,24 @@ int         ptmi_sync(void);            /* wait for the stream         */
  * held at that address fails with PTMI_ERR_STATE.                       */
 int ptmi_register_weights(const void *blob, size_t bytes);
 /* Re-upload [ptr, ptr+bytes) of a registered blob after host writes
- * (pitorch/train/pt_train.c:870-896 mutates W in place).               */
+ * (pitorch/train/pt_train.c:870-896 mutates W in place), or of a
+ * registered buffer (below).                                            */
 int ptmi_invalidate(const void *ptr, size_t bytes);
 /* End one ptmi_register_weights hold.  Refused (PTMI_ERR_STATE) while a
  * model created over the blob is alive: destroy the models first.       */
 int ptmi_unregister_weights(const void *blob);
+/* Register a plain host buffer of floats that ptmi_matvec reads as W many
+ * times between host writes, e.g. the backward's host-transposed weights
+ * (w_transpose, pitorch/train/pt_train.c:405-407, filled by transpose()
+ * at :588-594 and :662-679, then read by T-1 matvecs each).  It is copied
+ * to HBM once; a W that lies inside it is served from that copy instead of
+ * being uploaded per call (37 MB per call for the transposed classifier).
+ * After the host rewrites part of it, ptmi_invalidate(ptr, bytes) over
+ * that part re-uploads it; until then matvecs read the old contents.
+ * Must not overlap a registered blob or buffer.  No reference counterpart:
+ * the Pi reads host memory directly through the TMU.                    */
+int ptmi_register_buffer(const void *p, size_t bytes);
+int ptmi_unregister_buffer(const void *p);
 
 /* ── matvec: y[out_dim] = W[out_dim, in_dim] . x[in_dim] ──────────────
  * ptmi_matvec has exactly the pt_matvec_fn signature

@@ -56,6 +56,8 @@ def load_ptmi():
     _sig(L, "ptmi_register_weights", i, [_vp, sz])
     _sig(L, "ptmi_invalidate", i, [_vp, sz])
     _sig(L, "ptmi_unregister_weights", i, [_vp])
+    _sig(L, "ptmi_register_buffer", i, [_vp, sz])
+    _sig(L, "ptmi_unregister_buffer", i, [_vp])
     _sig(L, "ptmi_matvec", None, [_vp, _vp, _vp, i, i])
     _sig(L, "ptmi_matvec_checked", i, [_vp, _vp, _vp, i, i])
     _sig(L, "ptmi_matvec_dev", i, [_vp, ctypes.c_long, _vp, _vp, i, i, _vp])

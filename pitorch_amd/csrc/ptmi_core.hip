@@ -2,6 +2,7 @@
 // residency registry and the host-pointer pt_matvec_fn drop-in.
 #include "ptmi_internal.h"
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -12,11 +13,19 @@ namespace ptmi {
 
 namespace {
 
+// A registered plain host buffer and its device copy (same layout).
+struct HostBuffer {
+    const char *host;
+    size_t bytes;
+    char *dev;
+};
+
 struct LibState {
     bool inited = false;
     int device = 0;
     hipStream_t stream = nullptr;
     std::vector<Resident *> residents;
+    std::vector<HostBuffer> buffers;
     float *scratch[4] = {nullptr, nullptr, nullptr, nullptr};
     size_t scratch_cap[4] = {0, 0, 0, 0};
     int status = PTMI_OK;
@@ -128,6 +137,12 @@ static void host_offsets(Resident *r) {
     r->off_end = o;
 }
 
+static HostBuffer *find_buffer(const void *p) {
+    for (HostBuffer &b : g.buffers)
+        if ((const char *)p >= b.host && (const char *)p < b.host + b.bytes) return &b;
+    return nullptr;
+}
+
 Resident *find_resident(const void *p) {
     for (Resident *r : g.residents) {
         const char *lo = r->blob, *hi = r->blob + r->bytes;
@@ -215,6 +230,11 @@ Resident *register_blob(const void *blob, size_t bytes, bool explicit_hold, int 
         else r->model_holds++;
         return r;
     }
+    for (const HostBuffer &b : g.buffers)
+        if ((const char *)blob < b.host + b.bytes && b.host < (const char *)blob + bytes) {
+            *status = set_error(PTMI_ERR_ARG, "blob overlaps a registered buffer");
+            return nullptr;
+        }
     Resident *r = new Resident();
     r->blob = (const char *)blob;
     r->bytes = bytes;
@@ -330,6 +350,8 @@ void ptmi_shutdown(void) {
     (void)hipStreamSynchronize(g.stream);
     for (Resident *r : g.residents) { (void)hipFree(r->mem); delete r; }
     g.residents.clear();
+    for (HostBuffer &b : g.buffers) (void)hipFree(b.dev);
+    g.buffers.clear();
     for (int i = 0; i < 4; i++) {
         if (g.scratch[i]) (void)hipFree(g.scratch[i]);
         g.scratch[i] = nullptr;
@@ -361,9 +383,44 @@ int ptmi_register_weights(const void *blob, size_t bytes) {
     return st;
 }
 
+int ptmi_register_buffer(const void *p, size_t bytes) {
+    int st = ensure_init();
+    if (st) return st;
+    if (!p || bytes == 0) return set_error(PTMI_ERR_ARG, "ptmi_register_buffer: empty buffer");
+    const char *lo = (const char *)p, *hi = lo + bytes;
+    for (const HostBuffer &b : g.buffers)
+        if (lo < b.host + b.bytes && b.host < hi) return set_error(PTMI_ERR_ARG, "buffer %p overlaps a registered buffer", p);
+    for (const Resident *r : g.residents)
+        if (lo < r->blob + r->bytes && r->blob < hi) return set_error(PTMI_ERR_ARG, "buffer %p overlaps a registered blob", p);
+    char *dev = nullptr;
+    PTMI_HIP(hipMalloc(&dev, bytes));
+    hipError_t e = hipMemcpyAsync(dev, p, bytes, hipMemcpyHostToDevice, g.stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g.stream);
+    if (e != hipSuccess) { (void)hipFree(dev); return hip_check(e, "ptmi_register_buffer upload"); }
+    g.buffers.push_back(HostBuffer{lo, bytes, dev});
+    return PTMI_OK;
+}
+
+int ptmi_unregister_buffer(const void *p) {
+    for (size_t i = 0; i < g.buffers.size(); i++) {
+        if (g.buffers[i].host != (const char *)p) continue;
+        (void)hipStreamSynchronize(g.stream);
+        (void)hipFree(g.buffers[i].dev);
+        g.buffers.erase(g.buffers.begin() + (long)i);
+        return PTMI_OK;
+    }
+    return set_error(PTMI_ERR_ARG, "buffer %p is not registered", p);
+}
+
 int ptmi_invalidate(const void *ptr, size_t bytes) {
     int st = ensure_init();
     if (st) return st;
+    if (HostBuffer *b = find_buffer(ptr)) {      // re-upload the part written, clipped to the buffer
+        const size_t off = (size_t)((const char *)ptr - b->host), n = std::min(bytes, b->bytes - off);
+        PTMI_HIP(hipMemcpyAsync(b->dev + off, ptr, n, hipMemcpyHostToDevice, g.stream));
+        PTMI_HIP(hipStreamSynchronize(g.stream));
+        return PTMI_OK;
+    }
     Resident *r = find_resident(ptr);
     if (!r) return PTMI_OK;            // not resident: nothing cached
     (void)bytes;                       // whole-tensor granularity: re-upload all
@@ -415,9 +472,14 @@ int ptmi_matvec_checked(const float *W, const float *x, float *y, int out_dim, i
     const float *dW = nullptr;
     long ld = in_dim;
     Resident *r = find_resident(W);
-    if (!(r && resolve(r, W, out_dim, in_dim, &dW, &ld))) {
-        // Not a resident tensor view (e.g. a host-transposed scratch copy):
-        // upload for this call.
+    const HostBuffer *hb = r ? nullptr : find_buffer(W);
+    const size_t w_bytes = (size_t)out_dim * in_dim * sizeof(float);
+    if (hb && (size_t)((const char *)W - hb->host) + w_bytes <= hb->bytes) {
+        // inside a registered plain buffer: its device copy
+        dW = reinterpret_cast<const float *>(hb->dev + ((const char *)W - hb->host));
+    } else if (!(r && resolve(r, W, out_dim, in_dim, &dW, &ld))) {
+        // Not a resident tensor view (e.g. an unregistered host-transposed
+        // scratch copy): upload for this call.
         float *w = scratch_buf(0, (size_t)out_dim * in_dim);
         if (!w) return g.status;
         PTMI_HIP(hipMemcpyAsync(w, W, (size_t)out_dim * in_dim * sizeof(float), hipMemcpyHostToDevice, s));

@@ -172,3 +172,44 @@ def test_x_reread_ablation_rejects_long_rows():
     a = DeviceArray(4 * 2400)
     assert L.ptmi_matvec_dev_xreread(a.ptr, 2400, a.ptr, a.ptr, 2, 2400, None) == 1
     a.free()
+
+
+def test_registered_buffer_serves_w_until_invalidated():
+    """ptmi_register_buffer: a host scratch matrix (the backward's
+    host-transposed W, pitorch/train/pt_train.c:588-594, 662-679) is copied
+    to HBM once and every W inside it is read from that copy; a host write
+    is seen after ptmi_invalidate over the written part and not before;
+    overlapping registrations are refused.  Integer inputs: exact."""
+    L = pa.load_ptmi()
+    D, V = 288, 4096
+    buf = lcg_ints(D * V + 2 * D * D, 31, 16).astype(np.float32)     # [W_t (D x V) | two D x D blocks]
+    x = lcg_ints(V, 32, 16).astype(np.float32)
+    y = np.zeros(D, np.float32)
+    assert L.ptmi_register_buffer(P(buf), buf.nbytes) == 0
+    try:
+        wt = buf[:D * V].reshape(D, V)
+        for _ in range(3):                            # the T-1 calls of one backward
+            assert L.ptmi_matvec_checked(P(wt), P(x), P(y), D, V) == 0
+            assert np.array_equal(y, oracle_mv(wt, x))
+        # a sub-matrix view at an offset (a layer's block of the packed transposes)
+        blk = buf[D * V + D * D:].reshape(D, D)
+        y2 = np.zeros(D, np.float32)
+        assert L.ptmi_matvec_checked(P(blk), P(x[:D]), P(y2), D, D) == 0
+        assert np.array_equal(y2, oracle_mv(blk, x[:D]))
+        # host write without invalidate: the device copy still holds the old W
+        old = oracle_mv(blk, x[:D])
+        blk[:] = lcg_ints(D * D, 33, 16).astype(np.float32).reshape(D, D)
+        assert L.ptmi_matvec_checked(P(blk), P(x[:D]), P(y2), D, D) == 0
+        assert np.array_equal(y2, old)
+        # invalidate the written part only: now the new W
+        assert L.ptmi_invalidate(P(blk), blk.nbytes) == 0
+        assert L.ptmi_matvec_checked(P(blk), P(x[:D]), P(y2), D, D) == 0
+        assert np.array_equal(y2, oracle_mv(blk, x[:D]))
+        assert L.ptmi_matvec_checked(P(wt), P(x), P(y), D, V) == 0    # the rest untouched
+        assert np.array_equal(y, oracle_mv(wt, x))
+        # overlaps are refused
+        assert L.ptmi_register_buffer(P(blk), blk.nbytes) == 1
+        assert "overlaps" in L.ptmi_last_error().decode()
+    finally:
+        assert L.ptmi_unregister_buffer(P(buf)) == 0
+    assert L.ptmi_unregister_buffer(P(buf)) == 1
