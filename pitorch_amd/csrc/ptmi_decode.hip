@@ -339,17 +339,18 @@ struct StepTimer {
 
 // Producer-side prefetch of consumer matvec weights W[rows, n] (ld = n).
 // The producer's own grid is `first_block` blocks of `threads` threads.
-PrefetchDesc pf_matvec(const ptmi_model *m, const float *W, int rows, int n, int pro, int epi, int first_block,
-                       int threads) {
-    if (!m->prefetch) return PrefetchDesc{};
+PrefetchDesc pf_matvec(const ptmi_model *m, unsigned stage, const float *W, int rows, int n, int pro, int epi,
+                       int first_block, int threads) {
+    if (!m->prefetch || !(m->prefetch_mask & (1u << stage))) return PrefetchDesc{};
     return prefetch_for(W, n, rows, n, pro, epi, first_block, threads, m->sink);
 }
 
 // Enqueue one decode step on s (used both for capture and eager runs).
-// Each stage prefetches the weights of a later matvec into the L2 of the
-// XCDs that will read them:
-//   QKV_l -> Wo_l,  attention_l -> w13_l,  Wo_l -> w2_l,
-//   w13_l -> QKV_{l+1},  classifier -> QKV_0 (next token).
+// A stage can prefetch the weights of a later matvec into the L2 of the
+// XCDs that will read them (the consumer's loads then hit the MALL):
+//   QKV_l -> Wo_l,  attention_l -> w13_l,  Wo_l -> w2_l         (default on)
+//   w13_l -> QKV_{l+1},  classifier -> QKV_0 (next token)        (default off)
+// as selected by m->prefetch_mask.
 int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
     const Config &c = m->c;
     const Resident *r = m->res;
@@ -370,7 +371,7 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         p.norm_w = r->rms_att + l * D;
         p.y = m->q; p.epi = EPI_QKV_ROPE; p.pos = &m->ctl->pos;
         p.q_rows = (int)D; p.kv_rows = (int)KV; p.head_dim = c.head_dim; p.k_cache = kc; p.v_cache = vc;
-        p.pf = pf_matvec(m, r->wo + (long)l * D * D, (int)D, (int)D, PRO_ATTN_COMBINE, EPI_RESIDUAL,
+        p.pf = pf_matvec(m, 0, r->wo + (long)l * D * D, (int)D, (int)D, PRO_ATTN_COMBINE, EPI_RESIDUAL,
                          matvec_compute_blocks(QR, (int)D, p.pro, EPI_QKV_ROPE),
                          matvec_block_threads(QR, (int)D, p.pro, EPI_QKV_ROPE));
         TIMED(0, if ((st = launch_matvec(p, s, e0, e1))) return st);
@@ -383,7 +384,7 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         const int hd4 = c.head_dim / 4;
         auto attn = hd4 <= 8 ? k_attn_chunk<8> : hd4 <= 16 ? k_attn_chunk<16> : k_attn_chunk<32>;
         const int attn_blocks = c.n_heads * m->attn_chunks;
-        a.pf = pf_matvec(m, r->w13 + (long)l * 2 * H * D, (int)(2 * H), (int)D, PRO_RMSNORM, EPI_SWIGLU, attn_blocks,
+        a.pf = pf_matvec(m, 1, r->w13 + (long)l * 2 * H * D, (int)(2 * H), (int)D, PRO_RMSNORM, EPI_SWIGLU, attn_blocks,
                          kAttnWaves * 64);
         a.pf.first_block = attn_blocks;
         TIMED(1, launch_k(attn, dim3(attn_blocks + a.pf.blocks), dim3(kAttnWaves * 64), 0, s, e0, e1, a));
@@ -394,7 +395,7 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         p.x = m->xb; p.y = m->x; p.pro = PRO_ATTN_COMBINE; p.epi = EPI_RESIDUAL;
         p.pos = &m->ctl->pos; p.att_o = m->part_o; p.att_ml = m->part_ml;
         p.att_chunks = m->attn_chunks; p.att_chunk = m->attn_chunk; p.att_heads = c.n_heads;
-        p.pf = pf_matvec(m, r->w2 + (long)l * D * H, (int)D, (int)H, PRO_NONE, EPI_RESIDUAL,
+        p.pf = pf_matvec(m, 2, r->w2 + (long)l * D * H, (int)D, (int)H, PRO_NONE, EPI_RESIDUAL,
                          matvec_compute_blocks((int)D, (int)D, PRO_ATTN_COMBINE, EPI_RESIDUAL),
                          matvec_block_threads((int)D, (int)D, PRO_ATTN_COMBINE, EPI_RESIDUAL));
         TIMED(2, if ((st = launch_matvec(p, s, e0, e1))) return st);
@@ -404,7 +405,7 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         p.x = m->x; p.pro = PRO_RMSNORM; p.norm_w = r->rms_ffn + l * D;
         p.y = m->hb; p.epi = EPI_SWIGLU;
         if (l + 1 < c.n_layers)
-            p.pf = pf_matvec(m, r->wqkv + (long)(l + 1) * QR * D, QR, (int)D, PRO_RMSNORM, EPI_QKV_ROPE,
+            p.pf = pf_matvec(m, 3, r->wqkv + (long)(l + 1) * QR * D, QR, (int)D, PRO_RMSNORM, EPI_QKV_ROPE,
                              matvec_compute_blocks((int)(2 * H), (int)D, PRO_RMSNORM, EPI_SWIGLU),
                              matvec_block_threads((int)(2 * H), (int)D, PRO_RMSNORM, EPI_SWIGLU));
         TIMED(3, if ((st = launch_matvec(p, s, e0, e1))) return st);
@@ -417,7 +418,7 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
     MatvecParams p = {};
     p.W = r->wcls; p.ld = D; p.rows = c.vocab; p.n = (int)D;
     p.x = m->x; p.pro = PRO_RMSNORM; p.norm_w = r->rms_final; p.y = m->logits; p.epi = EPI_STORE;
-    p.pf = pf_matvec(m, r->wqkv, QR, (int)D, PRO_EMBED_RMSNORM, EPI_QKV_ROPE,
+    p.pf = pf_matvec(m, 4, r->wqkv, QR, (int)D, PRO_EMBED_RMSNORM, EPI_QKV_ROPE,
                      matvec_compute_blocks(c.vocab, (int)D, PRO_RMSNORM, EPI_STORE),
                      matvec_block_threads(c.vocab, (int)D, PRO_RMSNORM, EPI_STORE));
     TIMED(5, if ((st = launch_matvec(p, s, e0, e1))) return st);
@@ -554,6 +555,7 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
     m->eager = eager && eager[0] == '1';
     const char *nopf = getenv("PTMI_NO_PREFETCH");
     m->prefetch = !(nopf && nopf[0] == '1');
+    if (const char *pm = getenv("PTMI_PREFETCH_MASK")) m->prefetch_mask = (unsigned)strtoul(pm, nullptr, 0);
     if ((st = decode_step_create(m)) || (!m->eager && (st = build_graph(m))) ||
         (max_T > 0 && (st = train_create(m)))) {
         train_destroy(m);

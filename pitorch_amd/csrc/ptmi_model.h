@@ -42,6 +42,12 @@ struct ptmi_model {
     hipGraphExec_t exec = nullptr;
     bool eager = false;                  // PTMI_DECODE_EAGER=1: no graph
     bool prefetch = true;                // PTMI_NO_PREFETCH=1: no L2 prefetch blocks
+    // Producer stages that prefetch (bit 0 QKV->Wo, 1 attention->w1|w3,
+    // 2 Wo->w2, 3 w1|w3->next QKV, 4 classifier->next token's QKV).  The
+    // default, bits 0-2, measured best of all 16 subsets of bits 0-3 on
+    // stories110M (3775 tok/s; all five 3617; none 3637).
+    // PTMI_PREFETCH_MASK overrides it.
+    unsigned prefetch_mask = 7;
     float *sink = nullptr;               // prefetch load sink
     // one-kernel decode step (null step_mem: the multi-kernel step)
     uint64_t *step_mem = nullptr;        // its tagged exchange buffers
