@@ -339,18 +339,36 @@ struct StepTimer {
 
 // Producer-side prefetch of consumer matvec weights W[rows, n] (ld = n).
 // The producer's own grid is `first_block` blocks of `threads` threads.
-PrefetchDesc pf_matvec(const ptmi_model *m, unsigned stage, const float *W, int rows, int n, int pro, int epi,
-                       int first_block, int threads) {
-    if (!m->prefetch || !(m->prefetch_mask & (1u << stage))) return PrefetchDesc{};
+PrefetchDesc pf_matvec(const ptmi_model *m, const float *W, int rows, int n, int pro, int epi, int first_block,
+                       int threads) {
+    if (!m->prefetch) return PrefetchDesc{};
     return prefetch_for(W, n, rows, n, pro, epi, first_block, threads, m->sink);
 }
 
+// The prefetch of producer `stage` (0 QKV, 1 attention, 2 Wo, 3 w1|w3,
+// 4 w2, 5 classifier, 6 argmax) in layer l, per m->prefetch_plan; the
+// producer's own grid is `first_block` blocks of `threads` threads.
+PrefetchDesc pf_plan(const ptmi_model *m, int stage, int l, int first_block, int threads) {
+    const Config &c = m->c;
+    const Resident *r = m->res;
+    const int D = c.dim, H = c.hidden, QR = c.dim + 2 * c.kv_dim, L = c.n_layers;
+    const int ll = l < L ? l + 1 : 0;                 // the next layer (next token's first after the last)
+    switch (m->prefetch_plan[stage]) {
+    case 'o': return l < L ? pf_matvec(m, r->wo + (long)l * D * D, D, D, PRO_ATTN_COMBINE, EPI_RESIDUAL, first_block, threads) : PrefetchDesc{};
+    case 'f': return l < L ? pf_matvec(m, r->w13 + (long)l * 2 * H * D, 2 * H, D, PRO_RMSNORM, EPI_SWIGLU, first_block, threads) : PrefetchDesc{};
+    case 'd': return l < L ? pf_matvec(m, r->w2 + (long)l * D * H, D, H, PRO_NONE, EPI_RESIDUAL, first_block, threads) : PrefetchDesc{};
+    case 'q': return pf_matvec(m, r->wqkv + (long)(ll < L ? ll : 0) * QR * D, QR, D, ll == 0 ? PRO_EMBED_RMSNORM : PRO_RMSNORM,
+                               EPI_QKV_ROPE, first_block, threads);
+    case 'O': return ll < L && ll > 0 ? pf_matvec(m, r->wo + (long)ll * D * D, D, D, PRO_ATTN_COMBINE, EPI_RESIDUAL, first_block, threads) : PrefetchDesc{};
+    case 'F': return ll < L && ll > 0 ? pf_matvec(m, r->w13 + (long)ll * 2 * H * D, 2 * H, D, PRO_RMSNORM, EPI_SWIGLU, first_block, threads) : PrefetchDesc{};
+    default: return PrefetchDesc{};
+    }
+}
+
 // Enqueue one decode step on s (used both for capture and eager runs).
-// A stage can prefetch the weights of a later matvec into the L2 of the
-// XCDs that will read them (the consumer's loads then hit the MALL):
-//   QKV_l -> Wo_l,  attention_l -> w13_l,  Wo_l -> w2_l         (default on)
-//   w13_l -> QKV_{l+1},  classifier -> QKV_0 (next token)        (default off)
-// as selected by m->prefetch_mask.
+// A launch can carry extra blocks that read the weights of a later matvec
+// (m->prefetch_plan): each kernel starts with an L2 invalidate, so the
+// consumer then finds them in the memory-side MALL.
 int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
     const Config &c = m->c;
     const Resident *r = m->res;
@@ -371,9 +389,8 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         p.norm_w = r->rms_att + l * D;
         p.y = m->q; p.epi = EPI_QKV_ROPE; p.pos = &m->ctl->pos;
         p.q_rows = (int)D; p.kv_rows = (int)KV; p.head_dim = c.head_dim; p.k_cache = kc; p.v_cache = vc;
-        p.pf = pf_matvec(m, 0, r->wo + (long)l * D * D, (int)D, (int)D, PRO_ATTN_COMBINE, EPI_RESIDUAL,
-                         matvec_compute_blocks(QR, (int)D, p.pro, EPI_QKV_ROPE),
-                         matvec_block_threads(QR, (int)D, p.pro, EPI_QKV_ROPE));
+        p.pf = pf_plan(m, 0, l, matvec_compute_blocks(QR, (int)D, p.pro, EPI_QKV_ROPE),
+                       matvec_block_threads(QR, (int)D, p.pro, EPI_QKV_ROPE));
         TIMED(0, if ((st = launch_matvec(p, s, e0, e1))) return st);
 
         AttnParams a = {};
@@ -384,8 +401,7 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         const int hd4 = c.head_dim / 4;
         auto attn = hd4 <= 8 ? k_attn_chunk<8> : hd4 <= 16 ? k_attn_chunk<16> : k_attn_chunk<32>;
         const int attn_blocks = c.n_heads * m->attn_chunks;
-        a.pf = pf_matvec(m, 1, r->w13 + (long)l * 2 * H * D, (int)(2 * H), (int)D, PRO_RMSNORM, EPI_SWIGLU, attn_blocks,
-                         kAttnWaves * 64);
+        a.pf = pf_plan(m, 1, l, attn_blocks, kAttnWaves * 64);
         a.pf.first_block = attn_blocks;
         TIMED(1, launch_k(attn, dim3(attn_blocks + a.pf.blocks), dim3(kAttnWaves * 64), 0, s, e0, e1, a));
         PTMI_HIP(hipGetLastError());
@@ -395,36 +411,35 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
         p.x = m->xb; p.y = m->x; p.pro = PRO_ATTN_COMBINE; p.epi = EPI_RESIDUAL;
         p.pos = &m->ctl->pos; p.att_o = m->part_o; p.att_ml = m->part_ml;
         p.att_chunks = m->attn_chunks; p.att_chunk = m->attn_chunk; p.att_heads = c.n_heads;
-        p.pf = pf_matvec(m, 2, r->w2 + (long)l * D * H, (int)D, (int)H, PRO_NONE, EPI_RESIDUAL,
-                         matvec_compute_blocks((int)D, (int)D, PRO_ATTN_COMBINE, EPI_RESIDUAL),
-                         matvec_block_threads((int)D, (int)D, PRO_ATTN_COMBINE, EPI_RESIDUAL));
+        p.pf = pf_plan(m, 2, l, matvec_compute_blocks((int)D, (int)D, PRO_ATTN_COMBINE, EPI_RESIDUAL),
+                       matvec_block_threads((int)D, (int)D, PRO_ATTN_COMBINE, EPI_RESIDUAL));
         TIMED(2, if ((st = launch_matvec(p, s, e0, e1))) return st);
 
         p = MatvecParams{};
         p.W = r->w13 + (long)l * 2 * H * D; p.ld = D; p.rows = (int)(2 * H); p.n = (int)D;
         p.x = m->x; p.pro = PRO_RMSNORM; p.norm_w = r->rms_ffn + l * D;
         p.y = m->hb; p.epi = EPI_SWIGLU;
-        if (l + 1 < c.n_layers)
-            p.pf = pf_matvec(m, 3, r->wqkv + (long)(l + 1) * QR * D, QR, (int)D, PRO_RMSNORM, EPI_QKV_ROPE,
-                             matvec_compute_blocks((int)(2 * H), (int)D, PRO_RMSNORM, EPI_SWIGLU),
-                             matvec_block_threads((int)(2 * H), (int)D, PRO_RMSNORM, EPI_SWIGLU));
+        p.pf = pf_plan(m, 3, l, matvec_compute_blocks((int)(2 * H), (int)D, PRO_RMSNORM, EPI_SWIGLU),
+                       matvec_block_threads((int)(2 * H), (int)D, PRO_RMSNORM, EPI_SWIGLU));
         TIMED(3, if ((st = launch_matvec(p, s, e0, e1))) return st);
 
         p = MatvecParams{};
         p.W = r->w2 + (long)l * D * H; p.ld = H; p.rows = (int)D; p.n = (int)H;
         p.x = m->hb; p.y = m->x; p.pro = PRO_NONE; p.epi = EPI_RESIDUAL;
+        p.pf = pf_plan(m, 4, l, matvec_compute_blocks((int)D, (int)H, PRO_NONE, EPI_RESIDUAL),
+                       matvec_block_threads((int)D, (int)H, PRO_NONE, EPI_RESIDUAL));
         TIMED(4, if ((st = launch_matvec(p, s, e0, e1))) return st);
     }
     MatvecParams p = {};
     p.W = r->wcls; p.ld = D; p.rows = c.vocab; p.n = (int)D;
     p.x = m->x; p.pro = PRO_RMSNORM; p.norm_w = r->rms_final; p.y = m->logits; p.epi = EPI_STORE;
-    p.pf = pf_matvec(m, 4, r->wqkv, QR, (int)D, PRO_EMBED_RMSNORM, EPI_QKV_ROPE,
-                     matvec_compute_blocks(c.vocab, (int)D, PRO_RMSNORM, EPI_STORE),
-                     matvec_block_threads(c.vocab, (int)D, PRO_RMSNORM, EPI_STORE));
+    p.pf = pf_plan(m, 5, c.n_layers, matvec_compute_blocks(c.vocab, (int)D, PRO_RMSNORM, EPI_STORE),
+                   matvec_block_threads(c.vocab, (int)D, PRO_RMSNORM, EPI_STORE));
     TIMED(5, if ((st = launch_matvec(p, s, e0, e1))) return st);
-    const PrefetchDesc none = {};
-    TIMED(6, launch_k(k_argmax_step, dim3(1), dim3(1024), 0, s, e0, e1, m->logits, c.vocab, m->ctl, m->prompt,
-                      m->out_tokens, none));
+    PrefetchDesc apf = pf_plan(m, 6, c.n_layers, 1, 1024);
+    apf.first_block = 1;
+    TIMED(6, launch_k(k_argmax_step, dim3(1 + apf.blocks), dim3(1024), 0, s, e0, e1, m->logits, c.vocab, m->ctl,
+                      m->prompt, m->out_tokens, apf));
     PTMI_HIP(hipGetLastError());
     return PTMI_OK;
 }
@@ -555,7 +570,16 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
     m->eager = eager && eager[0] == '1';
     const char *nopf = getenv("PTMI_NO_PREFETCH");
     m->prefetch = !(nopf && nopf[0] == '1');
-    if (const char *pm = getenv("PTMI_PREFETCH_MASK")) m->prefetch_mask = (unsigned)strtoul(pm, nullptr, 0);
+    if (const char *pp = getenv("PTMI_PREFETCH_PLAN")) {
+        if (strlen(pp) != 7 || strspn(pp, "ofdqOF-") != 7) {
+            st = set_error(PTMI_ERR_ARG, "PTMI_PREFETCH_PLAN: 7 letters of ofdqOF- expected, got \"%s\"", pp);
+            (void)hipFree(m->mem);
+            delete m;
+            release_blob(r);
+            return st;
+        }
+        memcpy(m->prefetch_plan, pp, 8);
+    }
     if ((st = decode_step_create(m)) || (!m->eager && (st = build_graph(m))) ||
         (max_T > 0 && (st = train_create(m)))) {
         train_destroy(m);

@@ -42,12 +42,13 @@ struct ptmi_model {
     hipGraphExec_t exec = nullptr;
     bool eager = false;                  // PTMI_DECODE_EAGER=1: no graph
     bool prefetch = true;                // PTMI_NO_PREFETCH=1: no L2 prefetch blocks
-    // Producer stages that prefetch (bit 0 QKV->Wo, 1 attention->w1|w3,
-    // 2 Wo->w2, 3 w1|w3->next QKV, 4 classifier->next token's QKV).  The
-    // default, bits 0-2, measured best of all 16 subsets of bits 0-3 on
-    // stories110M (3775 tok/s; all five 3617; none 3637).
-    // PTMI_PREFETCH_MASK overrides it.
-    unsigned prefetch_mask = 7;
+    // Which weights each launch of the step prefetches (into the MALL,
+    // where they outlive the kernel boundary), one letter per producer:
+    // QKV, attention, Wo, w1|w3, w2, classifier, argmax.  Targets, relative
+    // to the producer's layer l: o = Wo_l, f = w1|w3_l, d = w2_l,
+    // q = QKV_{l+1} (the next token's layer 0 after the last layer), O = Wo_{l+1},
+    // F = w1|w3_{l+1}, '-' = none.  PTMI_PREFETCH_PLAN overrides it.
+    char prefetch_plan[8] = "ofd----";
     float *sink = nullptr;               // prefetch load sink
     // one-kernel decode step (null step_mem: the multi-kernel step)
     uint64_t *step_mem = nullptr;        // its tagged exchange buffers
