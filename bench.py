@@ -332,6 +332,67 @@ def pmc_workload(pa, name, positions):
     print(f"[bench] pmc workload: {positions} positions of {name}, then the calibration copy", file=sys.stderr)
 
 
+def step_stamps(pa, name, at):
+    """The one-kernel decode step's stage timeline (PTMI_DECODE_STEP=1 with
+    stage stamps): a greedy decode from position 0; for the step at each
+    position in `at`, every workgroup's stamps (the GPU's 100 MHz real-time
+    counter) give, per stage and layer: the span, from the last workgroup
+    finishing the previous stage to the last finishing this one; the
+    release, from that same point to the median workgroup of this stage
+    seeing its input (the hand-off); and the median work after the release.
+    Medians and maxima are over the layers.  Prints markdown on stdout."""
+    import numpy as np
+    os.environ["PTMI_DECODE_STEP"] = "1"
+    os.environ["PTMI_STEP_STAMPS"] = "1"
+    cfg = pa.STORIES[name]
+    L = cfg[2]
+    blob = pa.synth_model(cfg, pa.SEED_MODEL[name])
+    prompt = pa.seed_tokens(pa.SEED_PROMPT, pa.N_PROMPT, cfg[5])
+    m = pa.Model(blob)
+    stages = ["qkv", "attention", "wo", "w13", "w2"]
+    us = 0.01                                    # one tick = 10 ns
+    print("| position | stage | workgroups | span median µs | span max µs | release median µs | release max µs "
+          "| work median µs |")
+    print("|---:|---|---:|---:|---:|---:|---:|---:|")
+    rows = []
+    tok = int(prompt[0])
+    for pos in range(max(at) + 1):
+        nxt = m.forward_step(tok)
+        tok = int(prompt[pos + 1]) if pos + 1 < len(prompt) else nxt
+        if pos not in at:
+            continue
+        st = m.step_stamps().astype(np.int64)
+        span = {s_: [] for s_ in stages}
+        rel = {s_: [] for s_ in stages}
+        work = {s_: [] for s_ in stages}
+        n_wg = {}
+        prev_end = st[:, 0].max()                # the last workgroup's start
+        layer_ends = [prev_end]
+        for l in range(L):
+            for k, s_ in enumerate(stages):
+                we, wk = st[:, 1 + 10 * l + 2 * k], st[:, 2 + 10 * l + 2 * k]
+                part = (we > 0) & (wk > 0)
+                n_wg[s_] = int(part.sum())
+                end = wk[part].max()
+                span[s_].append((end - prev_end) * us)
+                rel[s_].append((np.median(we[part]) - prev_end) * us)
+                work[s_].append(np.median((wk - we)[part]) * us)
+                prev_end = end
+            layer_ends.append(prev_end)
+        for s_ in stages:
+            print(f"| {pos} | {s_} | {n_wg[s_]} | {np.median(span[s_]):.2f} | {max(span[s_]):.2f} | "
+                  f"{np.median(rel[s_]):.2f} | {max(rel[s_]):.2f} | {np.median(work[s_]):.2f} |")
+        layer = np.diff(np.array(layer_ends)) * us
+        total = (st[st > 0].max() - st[:, 0].min()) * us
+        rows.append((pos, np.median(layer), layer.max(), total))
+    print()
+    print("| position | layer median µs | layer max µs | step (first start to last stamp) µs |")
+    print("|---:|---:|---:|---:|")
+    for pos, med, mx, total in rows:
+        print(f"| {pos} | {med:.2f} | {mx:.2f} | {total:.2f} |")
+    m.close()
+
+
 def pmc_gemm(pa, reps):
     """Every training GEMM shape of stories15M at T=256, `reps` launches
     each, enqueued directly (no graph) with one synchronisation per shape:
@@ -375,6 +436,9 @@ def main():
                     help="counter-profile workload, no timing: POSITIONS decode steps of the --config model "
                          "enqueued without graphs, 8 at a time (rocprofv3 --pmc faults on its host side with "
                          "thousands of dispatches in flight), then the 256 MiB calibration copy")
+    ap.add_argument("--step-stamps", type=str, default="", metavar="POSITIONS",
+                    help="print the one-kernel decode step's stage timeline at these comma-separated positions "
+                         "(greedy decode of the --config model from position 0), not the bench line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -393,6 +457,9 @@ def main():
         return
     if args.pmc_workload:
         pmc_workload(pa, args.config, args.pmc_workload)
+        return
+    if args.step_stamps:
+        step_stamps(pa, args.config, sorted(int(p) for p in args.step_stamps.split(",")))
         return
 
     name = args.config
