@@ -221,10 +221,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void k_attn_chunk(AttnParams a) {
     }
 }
 
-// argmax (pt_ops.c:65-70: first index of the maximum) + step bookkeeping
-// (pt.c:269 pos++, pt_text.c:344-350 prefill forcing).  float4 loads, eight
-// in flight per thread; each thread scans ascending indices, ties resolve
-// to the smaller index.
+// argmax (pt_ops.c:65-70: the first index of the maximum; a NaN at index 0
+// makes it 0, other NaNs never win) + step bookkeeping (pt.c:269 pos++,
+// pt_text.c:344-350 prefill forcing).  float4 loads, eight in flight per
+// thread; each thread scans ascending indices, ties resolve to the smaller
+// index.
 __global__ __launch_bounds__(1024) void k_argmax_step(const float *logits, int n, DecodeCtl *ctl,
                                                       const int *prompt, int *out_tokens, PrefetchDesc pf) {
     if (blockIdx.x > 0) {
@@ -257,41 +258,12 @@ __global__ __launch_bounds__(1024) void k_argmax_step(const float *logits, int n
         const float v = logits[i];
         if (v > bv) { bv = v; bi = i; }
     }
-    // wave argmax, ties to the smaller index (a symmetric choice, so any
-    // pairing of lanes forms the same result): DPP within rows of 16, then
-    // the permlane swaps across rows and halves
-    auto take = [&](float ov, int oi) {
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    };
-    auto dpp_pair = [&](auto ctrl) {
-        constexpr int C = decltype(ctrl)::value;
-        take(__int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(bv), C, 0xF, 0xF, true)),
-             __builtin_amdgcn_mov_dpp(bi, C, 0xF, 0xF, true));
-    };
-    dpp_pair(std::integral_constant<int, 0xB1>{});
-    dpp_pair(std::integral_constant<int, 0x4E>{});
-    dpp_pair(std::integral_constant<int, 0x141>{});
-    dpp_pair(std::integral_constant<int, 0x140>{});
-    {
-        int ih;
-        const int il = pl16i(bi, ih);
-        const LanePair p = pl16(bv);
-        bv = p.lo; bi = il;
-        take(p.hi, ih);
-    }
-    {
-        int ih;
-        const int il = pl32i(bi, ih);
-        const LanePair p = pl32(bv);
-        bv = p.lo; bi = il;
-        take(p.hi, ih);
-    }
+    wave_argmax(bv, bi);
     if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
     __syncthreads();
     if (tid == 0) {
-        for (int w = 1; w < 16; w++)
-            if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
-        if (bi == 0x7fffffff) bi = 0;        // all NaN: the reference returns 0
+        for (int w = 1; w < 16; w++) take_max(bv, bi, sv[w], si[w]);
+        if (bi == 0x7fffffff || logits[0] != logits[0]) bi = 0;   // nothing above -inf, or a NaN first: 0
         const int pos = ctl->pos;
         const int next = (pos < ctl->n_prompt - 1) ? prompt[pos + 1] : bi;
         ctl->next = bi;

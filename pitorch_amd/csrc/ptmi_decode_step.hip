@@ -842,7 +842,10 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
         float v = bv;
         int i = bi;
         for (int w = 1; w < kW; w++) take_best(v, i, sm.ybuf[w][0], __float_as_int(sm.ybuf[w][1]));
-        if (i == 0x7fffffff) i = 0;              // all NaN: the reference returns 0
+        // nothing above -inf, or a NaN first logit (pt_ops.c:65-70 keeps
+        // index 0 then): 0.  Row 0 is this workgroup's own first row.
+        const float l0 = gl(a->logits)[0];
+        if (i == 0x7fffffff || l0 != l0) i = 0;
         const int pos = tk.pos;
         PTMI_GLOBAL DecodeCtl *ctl = gl(a->ctl);
         const int next = (pos < ctl->n_prompt - 1) ? gl(a->prompt)[pos + 1] : i;

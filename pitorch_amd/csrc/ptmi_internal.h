@@ -143,6 +143,34 @@ __device__ __forceinline__ int pl32i(int v, int &hi) {
     hi = r[1];
     return r[0];
 }
+// (value, index) argmax step: the larger value, ties to the smaller index
+// (pt_ops.c:65-70 keeps the first index of the maximum); NaNs never win.
+__device__ __forceinline__ void take_max(float &bv, int &bi, float ov, int oi) {
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+// Every lane ends with its wave's (value, index) argmax: DPP within rows of
+// 16 (quad xor 1, quad xor 2, half-row mirror, row mirror), then the
+// permlane swaps across rows and halves (the step is symmetric, so any
+// pairing of lanes gives the same result).
+__device__ __forceinline__ void wave_argmax(float &bv, int &bi) {
+#define PTMI_DPP_TAKE(ctrl)                                                                               \
+    take_max(bv, bi, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(bv), ctrl, 0xF, 0xF, true)), \
+             __builtin_amdgcn_mov_dpp(bi, ctrl, 0xF, 0xF, true))
+    PTMI_DPP_TAKE(0xB1);
+    PTMI_DPP_TAKE(0x4E);
+    PTMI_DPP_TAKE(0x141);
+    PTMI_DPP_TAKE(0x140);
+#undef PTMI_DPP_TAKE
+    int ih;
+    int il = pl16i(bi, ih);
+    LanePair p = pl16(bv);
+    bv = p.lo; bi = il;
+    take_max(bv, bi, p.hi, ih);
+    il = pl32i(bi, ih);
+    p = pl32(bv);
+    bv = p.lo; bi = il;
+    take_max(bv, bi, p.hi, ih);
+}
 // v + (lane l^16's v), v + (lane l^32's v)
 __device__ __forceinline__ float xsum16(float v) { const LanePair p = pl16(v); return p.lo + p.hi; }
 __device__ __forceinline__ float xsum32(float v) { const LanePair p = pl32(v); return p.lo + p.hi; }

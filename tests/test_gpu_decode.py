@@ -152,6 +152,31 @@ def test_generate_stop_and_clamp_semantics(decode_path):
     om.close()
 
 
+def test_argmax_keeps_index_0_when_first_logit_is_nan(decode_path):
+    """pt_ops.c:65-70 starts from index 0 and no comparison with NaN is true:
+    a classifier whose row 0 yields NaN makes every next token 0, while NaNs
+    elsewhere never win.  Untied classifier (llama2.c's unshared layout) with
+    row 0 and row 7 NaN; tokens against the oracle's."""
+    from tests.test_gpu_train import untie
+    cfg = (64, 160, 1, 4, 4, 512, 16)
+    V, D = cfg[5], cfg[0]
+    blob = untie(pa.synth_model(cfg, 7, 0.05), cfg, 8)
+    w = blob[28:].view(np.float32)
+    w[w.size - V * D: w.size - V * D + D] = np.nan          # wcls row 0
+    w[w.size - V * D + 7 * D: w.size - V * D + 8 * D] = np.nan
+    m = pa.Model(blob)
+    om = OracleModel(blob.copy())
+    tok = 5
+    for _ in range(4):
+        a, b = m.forward_step(tok), om.forward_step(tok)
+        assert a == b == 0
+        assert np.isnan(m.logits()[0]) and np.isnan(m.logits()[7])
+        tok = a
+    check_path(m, decode_path)
+    m.close()
+    om.close()
+
+
 def test_errors_are_reported():
     cfg = (64, 160, 1, 4, 4, 512, 8)
     blob = pa.synth_model(cfg, 6)
