@@ -347,8 +347,8 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
     const long D = c.dim, H = c.hidden, KV = c.kv_dim, S = c.seq_len;
     const int QR = (int)(D + 2 * KV);
     int st = PTMI_OK;
-    if (m->step_mem) {                                    // the one-kernel step
-        TIMED(7, st = launch_decode_step(m, s, e0, e1));
+    if (m->step_mem) {                                    // the one-kernel step (or its windows)
+        for (int w = 0; w < decode_step_windows(m) && st == PTMI_OK; w++) TIMED(7, st = launch_decode_step(m, w, s, e0, e1));
         return st;
     }
     for (int l = 0; l < c.n_layers; l++) {

@@ -25,8 +25,9 @@
 //
 // Stages per layer (workgroup b takes row blocks b, b+NB, ...):
 //   QKV  : RMSNorm(x) . [Wq;Wk;Wv], RoPE, q|k|v published, K/V cache row
-//   ATT  : (head, chunk of positions) units: scores, chunk softmax, e.v
-//   WO   : combine the chunks of every head, . Wo, + residual  -> x_a
+//   ATT  : (head, chunk of positions) units: scores, chunk softmax, e.v;
+//          the head's chunk-0 unit merges the chunks           -> att
+//   WO   : att . Wo, + residual                                -> x_a
 //   W13  : RMSNorm(x_a) . [w1|w3] rows interleaved, SwiGLU     -> hb
 //   W2   : hb . w2 + x_a                                         -> x_b
 // then the classifier (RMSNorm . Wcls, per-workgroup argmax candidates)
@@ -53,7 +54,8 @@ constexpr int kMaxChunk = 128;               // attention positions per unit
 constexpr int kMaxChunks = 8;                // units per head
 constexpr int kWriter = kW - 1;              // the wave that issues the workgroup's global stores
 constexpr int kPollT = kWriter * 64;         // threads that poll (all other waves)
-constexpr int kPartLds = 16 * kPollT;        // floats of chunk partials a workgroup combines
+constexpr int kMaxHd = 64;                   // head_dim of the instantiated kernels (16 lanes x float4)
+constexpr int kPartLds = kMaxChunks * (kMaxHd + 2);  // floats of one head's chunk records
 constexpr uint64_t kWaitTicks = 2000000;     // default wait bound: 20 ms at 100 MHz
 
 typedef float fx4 __attribute__((ext_vector_type(4)));
@@ -63,6 +65,7 @@ struct StepArgs {
     const float *emb, *rms_att, *wqkv, *wo, *rms_ffn, *w13, *w2, *rms_final, *wcls;
     int D, H, L, NH, KV, hd, kv_mul, V, S;
     int chunk, n_chunks;                     // attention unit = chunk positions of one head
+    int ubase;                               // workgroup of attention unit 0
     float att_scale;
     float *kc, *vc;                          // [L][S][KV]
     float *logits;                           // [V]
@@ -71,7 +74,8 @@ struct StepArgs {
     int *out_tokens;
     // tagged exchange buffers: word = tag << 32 | float bits
     uint64_t *t_qkv;                         // [L][D + 2KV]
-    uint64_t *t_part;                        // [L][n_chunks][NH][hd + 2]  (o[hd], max, sum)
+    uint64_t *t_part;                        // [L][NH][n_chunks][hd + 2]  (o[hd], max, sum)
+    uint64_t *t_att;                         // [L][D]  merged attention output per head
     uint64_t *t_xa, *t_xb;                   // [L][D]
     uint64_t *t_hb;                          // [L][H]
     uint64_t *t_cand;                        // [nb][2]  (best logit, its index)
@@ -81,6 +85,8 @@ struct StepArgs {
     uint64_t *stamps;                        // [nb][n_stamps]
     int n_stamps;                            // 1 + 10 L + 4
     uint64_t wait_ticks;                     // bound of every wait (100 MHz ticks)
+    int poll_sleep;                          // s_sleep(1) per unsuccessful poll round
+    int l2pf;                                // L2 staging by idle workgroups: 1 w1|w3 + w2, 2 next QKV + Wo
 };
 
 
@@ -150,15 +156,18 @@ __device__ __forceinline__ float4 ntload4(const float *p) {
 // Only waves other than the writer wave poll: on this GPU a wave's loads
 // and stores share one in-order counter, so a wave that has just stored
 // would see its poll wait for the acknowledgement of its stores.
+// The shared error word is a single line that every waiting thread of the
+// chip would read on every round; it is read every 32nd round only.
 template <int K>
-__device__ bool poll_words(const uint64_t *src, int n, uint32_t tag, float *dst, const DecodeCtl *ctl, int t,
-                           uint64_t wait_ticks) {
+__device__ bool poll_words(const uint64_t *src, int n, uint32_t tag, float *dst, const PTMI_CONST StepArgs *a, int t) {
     t = opaque(t);
     bool ok[K];
 #pragma unroll
     for (int k = 0; k < K; k++) ok[k] = t + k * kPollT >= n;
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    for (;;) {
+    const uint64_t wait_ticks = a->wait_ticks;
+    const int sleep = a->poll_sleep;
+    for (int round = 1;; round++) {
         uint64_t v[K];
 #pragma unroll
         for (int k = 0; k < K; k++)
@@ -175,8 +184,9 @@ __device__ bool poll_words(const uint64_t *src, int n, uint32_t tag, float *dst,
             }
         }
         if (all) return true;
-        if (err_seen(ctl) || __builtin_amdgcn_s_memrealtime() - t0 > wait_ticks) return false;
-        __builtin_amdgcn_s_sleep(1);
+        if (__builtin_amdgcn_s_memrealtime() - t0 > wait_ticks) return false;
+        if ((round & 31) == 0 && err_seen(a->ctl)) return false;
+        for (int i = 0; i < sleep; i++) __builtin_amdgcn_s_sleep(1);
     }
 }
 
@@ -215,16 +225,16 @@ struct Tok {
 // Workgroup LDS.
 struct Smem {
     float xs[2048];                    // the stage's input vector (<= max(D, H))
-    float part[kPartLds];              // WO: chunk partials of every head
-    float wts[64][kMaxChunks];         // WO: chunk weights per head
+    float part[kPartLds];              // ATT, chunk 0: the head's chunk records
+    float wts[1][kMaxChunks];          // ATT, chunk 0: the chunks' merge weights
     float xres[kRowsD];                // WO: residual rows of this block
     float xres2[kRowsH];               // W2: residual rows of this block
     float rope_c[64], rope_s[64];      // RoPE cos/sin of this position, pair i = 2*k (all layers)
     float ybuf[kW][2];                 // argmax per wave
     float qs[128], kp[128], vp[128];   // ATT: q, and k/v of this position
-    float sc[kMaxChunk];               // ATT: scores -> weights
     float red[kW][128];
     float wred[kW];
+    float sc[kMaxChunk];               // ATT: scores -> weights
     float cand[1024];                  // final argmax: (value, index) per workgroup
     float yout[kRowsD];                // results the writer wave stores
     int fail;
@@ -367,14 +377,22 @@ __device__ __forceinline__ float prefetch_rows(const float *W, int rows, int n, 
     return acc;
 }
 
+// Stage g = kStages * layer + s (s: QKV, ATT, WO, W13, W2); g = kStages * L
+// is the classifier with the final argmax.  One launch runs stages
+// [g0, g1) of the token: the whole step, or a window of it (the host
+// splits the step at chosen stages).  Values cross windows through the
+// same tagged words; a window loads its first stage's weights at start.
+constexpr int kStages = 5;
+
 template <int ITD, int ITH, int GA>
-__global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
+__global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, int g1) {
     using Rg = Regs<ITD, ITH, GA>;
     __shared__ Smem sm;
     Rg R;
     float pf_acc = 0.0f;                              // keeps prefetch loads alive
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int b = blockIdx.x, nb = gridDim.x;
+    auto in = [&](int g) { return g >= g0 && g < g1; };
     Tok tk;
     int L;
     {
@@ -393,20 +411,45 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
             sm.rope_c[tid] = c;
             sm.rope_s[tid] = sn;
         }
-        if (b < (a->D + 2 * a->KV + kRowsD - 1) / kRowsD) load_wD(a, R, a->wqkv, a->D + 2 * a->KV, b, a->rms_att);
-        stamp(a, 0);
+        // the first stage's weights (later stages' come during the stage before)
+        const int D = a->D, H = a->H, QR = D + 2 * a->KV, l = g0 / kStages;
+        switch (l < L ? g0 % kStages : kStages) {
+        case 0:
+            if (b < (QR + kRowsD - 1) / kRowsD) load_wD(a, R, a->wqkv + (long)l * QR * D, QR, b, a->rms_att + (long)l * D);
+            break;
+        case 1: {
+            const int u = b - a->ubase;
+            if (u >= 0 && u < a->NH * a->n_chunks && u / a->NH < tk.nact) load_kv(a, R, tk, l, u);
+            if (in(g0 + 1) && b < (D + kRowsD - 1) / kRowsD) load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
+            break;
+        }
+        case 2:
+            if (b < (D + kRowsD - 1) / kRowsD) load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
+            break;
+        case 3:
+            if (b < (2 * H + kRowsD - 1) / kRowsD) load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, b, a->rms_ffn + (long)l * D);
+            break;
+        case 4:
+            if (b < (D + kRowsH - 1) / kRowsH) load_wH(a, R, a->w2 + (long)l * D * H, D, b);
+            break;
+        default:
+            if (b < (a->V + kRowsD - 1) / kRowsD) load_wD(a, R, a->wcls, a->V, b, a->rms_final);
+            break;
+        }
+        if (g0 == 0) stamp(a, 0);
     }
     __syncthreads();
 
-    for (int l = 0; l < L; l++) {
+    for (int l = g0 / kStages; l < L && kStages * l < g1; l++) {
         // ── QKV: y = [Wq;Wk;Wv] . rmsnorm(x), RoPE on q and k (llama2.c:
         //    143-151); k and v also into the cache row of pos ──
-        {
+        if (in(kStages * l)) {
             const PTMI_CONST StepArgs *a = fresh(ap);
             const int D = a->D, KV = a->KV, QR = D + 2 * KV;
             const int blocks_qkv = (QR + kRowsD - 1) / kRowsD, blocks_wo = (D + kRowsD - 1) / kRowsD;
-            const int n_units = a->NH * a->n_chunks;
-            const bool unit = b < n_units && b / a->NH < tk.nact;
+            const int n_units = a->NH * a->n_chunks, u = b - a->ubase;
+            const bool unit = in(kStages * l + 1) && u >= 0 && u < n_units && u / a->NH < tk.nact;
+            const bool pre_wo = in(kStages * l + 2) && b < blocks_wo;
             if (b < blocks_qkv) {
                 __syncthreads();                              // xs is free again
                 bool ok = true;
@@ -414,7 +457,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
                     const float *x = a->emb + (long)tk.token * D;
                     for (int i = tid; i < D; i += kT) sm.xs[i] = gl(x)[i];
                 } else {
-                    ok = tid >= kPollT || poll_words<5>(a->t_xb + (long)(l - 1) * D, D, tk.tag, sm.xs, a->ctl, tid, a->wait_ticks);
+                    ok = tid >= kPollT || poll_words<5>(a->t_xb + (long)(l - 1) * D, D, tk.tag, sm.xs, a, tid);
                 }
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, 1 + 10 * l);
@@ -428,8 +471,8 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
                     }
                     const float acc = dot_d(a, R, sm.xs, true);
                     if (rb + nb >= blocks_qkv) {              // this block's last rows: next stages' loads
-                        if (unit) load_kv(a, R, tk, l, b);
-                        if (b < blocks_wo) load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
+                        if (unit) load_kv(a, R, tk, l, u);
+                        if (pre_wo) load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
                     }
                     // RoPE pairs: rows 2k (lanes 0-31) and 2k+1 (lanes 32-63) of a wave
                     const LanePair pr = pl32(acc);
@@ -460,15 +503,15 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
                 }
                 stamp(a, 2 + 10 * l);
             } else {
-                if (unit) load_kv(a, R, tk, l, b);
-                if (b < blocks_wo) load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
+                if (unit) load_kv(a, R, tk, l, u);
+                if (pre_wo) load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
             }
             // Workgroups with no QKV, attention or Wo work wait until the
             // w1|w3 stage: meanwhile they stage this layer's w1|w3 and w2
-            // rows in their XCD's L2.
+            // rows in their XCD's L2 (and through it the MALL).
             const int H = a->H;
-            const int first_idle = max(max(blocks_qkv, blocks_wo), n_units);
-            if (b >= first_idle) {
+            const int first_idle = max(max(blocks_qkv, blocks_wo), a->ubase + n_units);
+            if (b >= first_idle && (a->l2pf & 1)) {
                 pf_acc = prefetch_rows(a->w13 + (long)l * 2 * H * D, 2 * H, D, kRowsD, (2 * H + kRowsD - 1) / kRowsD,
                                        first_idle, nb, pf_acc);
                 pf_acc = prefetch_rows(a->w2 + (long)l * D * H, D, H, kRowsH, (D + kRowsH - 1) / kRowsH, first_idle, nb,
@@ -478,14 +521,15 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
 
         // ── ATT: unit (head h, chunk c) over positions [t0, t_end) (llama2.c:
         //    153-177): scores, the chunk's softmax statistics and e.v ──
-        {
+        if (in(kStages * l + 1)) {
             const PTMI_CONST StepArgs *a = fresh(ap);
             const int D = a->D, KV = a->KV, hd = a->hd, NH = a->NH, QR = D + 2 * KV;
-            const int n_units = NH * a->n_chunks;
-            for (int u = b; u < n_units; u += nb) {
+            const int n_units = NH * a->n_chunks, u0 = b - a->ubase;
+            for (int u = u0; u < n_units; u += nb) {
+                if (u < 0) continue;                          // uniform
                 const int h = u % NH, c = u / NH;
                 if (c >= tk.nact) continue;                   // uniform: chunk past pos
-                if (u != b) load_kv(a, R, tk, l, u);
+                if (u != u0) load_kv(a, R, tk, l, u);
                 const int t0 = c * a->chunk, t_end = min(t0 + a->chunk, tk.pos + 1), cnt = t_end - t0;
                 const bool has_pos = tk.pos < t_end;
                 const int kvh = h / a->kv_mul;
@@ -493,11 +537,11 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
                 __syncthreads();
                 bool ok = true;
                 if (tid < hd) {
-                    ok = poll_words<1>(t_qkv + h * hd, hd, tk.tag, sm.qs, a->ctl, tid, a->wait_ticks);
+                    ok = poll_words<1>(t_qkv + h * hd, hd, tk.tag, sm.qs, a, tid);
                 } else if (has_pos && tid >= 128 && tid < 128 + hd) {
-                    ok = poll_words<1>(t_qkv + D + kvh * hd, hd, tk.tag, sm.kp, a->ctl, tid - 128, a->wait_ticks);
+                    ok = poll_words<1>(t_qkv + D + kvh * hd, hd, tk.tag, sm.kp, a, tid - 128);
                 } else if (has_pos && tid >= 256 && tid < 256 + hd) {
-                    ok = poll_words<1>(t_qkv + D + KV + kvh * hd, hd, tk.tag, sm.vp, a->ctl, tid - 256, a->wait_ticks);
+                    ok = poll_words<1>(t_qkv + D + KV + kvh * hd, hd, tk.tag, sm.vp, a, tid - 256);
                 }
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, 3 + 10 * l);
@@ -562,28 +606,72 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
                     sm.red[wave][4 * sub + 3] = acc.w;
                 }
                 __syncthreads();
-                uint64_t *dst = a->t_part + (((long)l * a->n_chunks + c) * NH + h) * (hd + 2);
-                if (wave == kWriter) {
-                    if (lane < hd) {
-                        float o = 0.0f;
+                // the chunk's record: o = sum_t e_t v_t, max, sum_t e_t
+                auto rec_o = [&](int d) {
+                    float o = 0.0f;
 #pragma unroll
-                        for (int w = 0; w < kW; w++) o += sm.red[w][lane];
-                        tstore(dst + lane, o, tk.tag);
+                    for (int w = 0; w < kW; w++) o += sm.red[w][d];
+                    return o;
+                };
+                auto rec_l = [&]() {
+                    float ls = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < kW; w++) ls += sm.wred[w];
+                    return ls;
+                };
+                const uint64_t *head_part = a->t_part + ((long)l * NH + h) * a->n_chunks * (hd + 2);
+                if (c > 0) {
+                    // a later chunk: its record (o, max, sum) goes to the
+                    // head's chunk-0 unit
+                    uint64_t *dst = const_cast<uint64_t *>(head_part) + (long)c * (hd + 2);
+                    if (wave == kWriter) {
+                        if (lane < hd) tstore(dst + lane, rec_o(lane), tk.tag);
+                        if (lane == 0) tstore(dst + hd, mx, tk.tag);
+                        if (lane == 1) tstore(dst + hd + 1, rec_l(), tk.tag);
                     }
-                    if (lane == 0) tstore(dst + hd, mx, tk.tag);
-                    if (lane == 1) {
-                        float lsum = 0.0f;
+                } else {
+                    // chunk 0 merges the head's active chunks: its own
+                    // record from LDS, the others' records polled, then
+                    // w_c = e^(m_c - M) / sum_c' l_c' e^(m_c' - M) and
+                    // out = sum_c w_c o_c, published for the WO stage
+                    const int nother = tk.nact - 1;
+                    if (wave == kWriter) {
+                        if (lane < hd) sm.part[lane] = rec_o(lane);
+                        if (lane == 0) sm.part[hd] = mx;
+                        if (lane == 1) sm.part[hd + 1] = rec_l();
+                    }
+                    bool ok = true;
+                    if (nother > 0 && tid < kPollT)
+                        ok = poll_words<2>(head_part + (hd + 2), nother * (hd + 2), tk.tag, sm.part + (hd + 2), a, tid);
+                    if (!block_ok(ok, &sm.fail, a->ctl)) return;
+                    if (tid == 0) {
+                        const int nact = tk.nact;
+                        float M = -INFINITY;
+                        for (int cc = 0; cc < nact; cc++) M = fmaxf(M, sm.part[cc * (hd + 2) + hd]);
+                        float f[kMaxChunks], Ls = 0.0f;
 #pragma unroll
-                        for (int w = 0; w < kW; w++) lsum += sm.wred[w];
-                        tstore(dst + hd + 1, lsum, tk.tag);
+                        for (int cc = 0; cc < kMaxChunks; cc++) {
+                            const float *pc = sm.part + min(cc, nact - 1) * (hd + 2);
+                            f[cc] = cc < nact ? d_expf(pc[hd] - M) : 0.0f;
+                            Ls = cc < nact ? fmaf(pc[hd + 1], f[cc], Ls) : Ls;
+                        }
+                        const float inv = 1.0f / Ls;
+#pragma unroll
+                        for (int cc = 0; cc < kMaxChunks; cc++) sm.wts[0][cc] = f[cc] * inv;
+                    }
+                    __syncthreads();
+                    if (wave == kWriter && lane < hd) {
+                        float v = 0.0f;
+                        for (int cc = 0; cc < tk.nact; cc++) v = fmaf(sm.part[cc * (hd + 2) + lane], sm.wts[0][cc], v);
+                        tstore(a->t_att + (long)l * D + h * hd + lane, v, tk.tag);
                     }
                 }
                 stamp(a, 4 + 10 * l);
             }
         }
 
-        // ── WO: x_a = x + Wo . combine(chunks) (llama2.c:179-180) ──
-        {
+        // ── WO: x_a = x + Wo . att (llama2.c:179-180) ──
+        if (in(kStages * l + 2)) {
             const PTMI_CONST StepArgs *a = fresh(ap);
             const int D = a->D, H = a->H, hd = a->hd, NH = a->NH;
             const int blocks_wo = (D + kRowsD - 1) / kRowsD, blocks_w13 = (2 * H + kRowsD - 1) / kRowsD;
@@ -591,51 +679,26 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
             const uint64_t *t_xin = a->t_xb + (long)(l - 1) * D;      // used for l > 0 only
             uint64_t *t_xa = a->t_xa + (long)l * D;
             if (b < blocks_wo) {
-                const int nwords = tk.nact * NH * (hd + 2);
                 __syncthreads();
-                // (the first block's residual rows came with the QKV input)
-                bool ok = tid >= kPollT || poll_words<kPartLds / kPollT>(a->t_part + (long)l * a->n_chunks * NH * (hd + 2),
-                                                                         nwords, tk.tag, sm.part, a->ctl, tid, a->wait_ticks);
+                bool ok = tid >= kPollT || poll_words<5>(a->t_att + (long)l * D, D, tk.tag, sm.xs, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, 5 + 10 * l);
-                // chunk weights w[h][c] = e^(m_c - M) / sum_c' l_c' e^(m_c' - M)
-                if (tid < NH) {
-                    const int nact = tk.nact;
-                    float M = -INFINITY;
-                    for (int c = 0; c < nact; c++) M = fmaxf(M, sm.part[(c * NH + tid) * (hd + 2) + hd]);
-                    float f[kMaxChunks], Ls = 0.0f;
-#pragma unroll
-                    for (int c = 0; c < kMaxChunks; c++) {
-                        const float *pc = sm.part + (min(c, nact - 1) * NH + tid) * (hd + 2);
-                        f[c] = c < nact ? d_expf(pc[hd] - M) : 0.0f;
-                        Ls = c < nact ? fmaf(pc[hd + 1], f[c], Ls) : Ls;
-                    }
-                    const float inv = 1.0f / Ls;
-#pragma unroll
-                    for (int c = 0; c < kMaxChunks; c++) sm.wts[tid][c] = f[c] * inv;
-                }
-                __syncthreads();
-                for (int i = tid; i < D; i += kT) {
-                    const int h = i / hd, d = i - h * hd;
-                    float v = 0.0f;
-                    for (int c = 0; c < tk.nact; c++) v = fmaf(sm.part[(c * NH + h) * (hd + 2) + d], sm.wts[h][c], v);
-                    sm.xs[i] = v;
-                }
-                __syncthreads();
+                // the residual rows came with this layer's QKV input when the
+                // QKV stage ran in this launch; otherwise they are read here
+                const bool res_here = !in(kStages * l);
                 for (int rb = b; rb < blocks_wo; rb += nb) {
-                    if (rb != b) {
+                    if (rb != b || res_here) {
                         __syncthreads();                      // the writer wave is done with yout
-                        load_wD(a, R, a->wo + (long)l * D * D, D, rb, nullptr);
+                        if (rb != b) load_wD(a, R, a->wo + (long)l * D * D, D, rb, nullptr);
                         bool ok2 = true;
                         if (tid < kRowsD) {
                             if (l == 0) sm.xres[tid] = gl(x_emb)[min(rb * kRowsD + tid, D - 1)];
-                            else ok2 = poll_words<1>(t_xin + rb * kRowsD, min(kRowsD, D - rb * kRowsD), tk.tag, sm.xres,
-                                                     a->ctl, tid, a->wait_ticks);
+                            else ok2 = poll_words<1>(t_xin + rb * kRowsD, min(kRowsD, D - rb * kRowsD), tk.tag, sm.xres, a, tid);
                         }
                         if (!block_ok(ok2, &sm.fail, a->ctl)) return;
                     }
                     const float acc = dot_d(a, R, sm.xs, false);
-                    if (rb + nb >= blocks_wo && b < blocks_w13)
+                    if (rb + nb >= blocks_wo && b < blocks_w13 && in(kStages * l + 3))
                         load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, b, a->rms_ffn + (long)l * D);
                     const int slot = slot_d();
                     if ((lane & 31) == 0) sm.yout[slot] = sm.xres[slot] + acc;
@@ -644,20 +707,20 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
                         tstore(t_xa + rb * kRowsD + lane, sm.yout[lane], tk.tag);
                 }
                 stamp(a, 6 + 10 * l);
-            } else if (b < blocks_w13) {
+            } else if (b < blocks_w13 && in(kStages * l + 3)) {
                 load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, b, a->rms_ffn + (long)l * D);
             }
         }
 
         // ── W13: hb = silu(w1 . xn) * (w3 . xn), xn = rmsnorm(x_a)
         //    (llama2.c:184-188; w1/w3 rows interleaved) ──
-        {
+        if (in(kStages * l + 3)) {
             const PTMI_CONST StepArgs *a = fresh(ap);
             const int D = a->D, H = a->H;
             const int blocks_w13 = (2 * H + kRowsD - 1) / kRowsD, blocks_w2 = (D + kRowsH - 1) / kRowsH;
             if (b < blocks_w13) {
                 __syncthreads();                              // xs and xres2 are free again
-                bool ok = tid >= kPollT || poll_words<5>(a->t_xa + (long)l * D, D, tk.tag, sm.xs, a->ctl, tid, a->wait_ticks);
+                bool ok = tid >= kPollT || poll_words<5>(a->t_xa + (long)l * D, D, tk.tag, sm.xs, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, 7 + 10 * l);
                 // the W2 residual rows are rows of this same input
@@ -669,7 +732,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
                         load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, rb, a->rms_ffn + (long)l * D);
                     }
                     const float acc = dot_d(a, R, sm.xs, true);
-                    if (rb + nb >= blocks_w13 && b < blocks_w2) load_wH(a, R, a->w2 + (long)l * D * H, D, b);
+                    if (rb + nb >= blocks_w13 && b < blocks_w2 && in(kStages * l + 4)) load_wH(a, R, a->w2 + (long)l * D * H, D, b);
                     const LanePair pr = pl32(acc);
                     if (lane == 0) {
                         const float h1 = pr.lo, h3 = pr.hi;
@@ -681,20 +744,20 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
                     if (wave == kWriter && lane < kRowsD / 2 && 2 * i < 2 * H) tstore(t_hb + i, sm.yout[lane], tk.tag);
                 }
                 stamp(a, 8 + 10 * l);
-            } else if (b < blocks_w2) {
+            } else if (b < blocks_w2 && in(kStages * l + 4)) {
                 load_wH(a, R, a->w2 + (long)l * D * H, D, b);
             }
         }
 
         // ── W2: x_b = x_a + w2 . hb (llama2.c:189-190) ──
-        {
+        if (in(kStages * l + 4)) {
             const PTMI_CONST StepArgs *a = fresh(ap);
             const int D = a->D, H = a->H, QR = D + 2 * a->KV;
             const int blocks_w2 = (D + kRowsH - 1) / kRowsH, blocks_w13 = (2 * H + kRowsD - 1) / kRowsD;
             const bool last_layer = l + 1 == a->L;
             const int next_blocks = last_layer ? (a->V + kRowsD - 1) / kRowsD : (QR + kRowsD - 1) / kRowsD;
             auto preload_next = [&]() {
-                if (b >= next_blocks) return;
+                if (b >= next_blocks || !in(kStages * (l + 1))) return;
                 if (last_layer) load_wD(a, R, a->wcls, a->V, b, a->rms_final);
                 else load_wD(a, R, a->wqkv + (long)(l + 1) * QR * D, QR, b, a->rms_att + (long)(l + 1) * D);
             };
@@ -702,9 +765,9 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
                 const uint64_t *t_xa = a->t_xa + (long)l * D;
                 uint64_t *t_xb = a->t_xb + (long)l * D;
                 __syncthreads();
-                bool ok = tid >= kPollT || poll_words<5>(a->t_hb + (long)l * H, H, tk.tag, sm.xs, a->ctl, tid, a->wait_ticks);
-                if (ok && tid < kRowsH && b >= blocks_w13)   // residual rows not taken in W13
-                    ok = poll_words<1>(t_xa + b * kRowsH, min(kRowsH, D - b * kRowsH), tk.tag, sm.xres2, a->ctl, tid, a->wait_ticks);
+                bool ok = tid >= kPollT || poll_words<5>(a->t_hb + (long)l * H, H, tk.tag, sm.xs, a, tid);
+                if (ok && tid < kRowsH && (b >= blocks_w13 || !in(kStages * l + 3)))   // residual rows not taken in W13
+                    ok = poll_words<1>(t_xa + b * kRowsH, min(kRowsH, D - b * kRowsH), tk.tag, sm.xres2, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, 9 + 10 * l);
                 for (int rb = b; rb < blocks_w2; rb += nb) {
@@ -713,8 +776,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
                         load_wH(a, R, a->w2 + (long)l * D * H, D, rb);
                         bool ok2 = true;
                         if (tid < kRowsH)
-                            ok2 = poll_words<1>(t_xa + rb * kRowsH, min(kRowsH, D - rb * kRowsH), tk.tag, sm.xres2,
-                                                a->ctl, tid, a->wait_ticks);
+                            ok2 = poll_words<1>(t_xa + rb * kRowsH, min(kRowsH, D - rb * kRowsH), tk.tag, sm.xres2, a, tid);
                         if (!block_ok(ok2, &sm.fail, a->ctl)) return;
                     }
                     const float acc = dot_h(a, R, sm.xs);
@@ -729,7 +791,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
                 preload_next();
                 // idle until the next layer's QKV input: stage its QKV and Wo
                 // rows in this XCD's L2
-                if (!last_layer) {
+                if (!last_layer && (a->l2pf & 2)) {
                     pf_acc = prefetch_rows(a->wqkv + (long)(l + 1) * QR * D, QR, D, kRowsD, (QR + kRowsD - 1) / kRowsD,
                                            blocks_w2, nb, pf_acc);
                     pf_acc = prefetch_rows(a->wo + (long)(l + 1) * D * D, D, D, kRowsD, (D + kRowsD - 1) / kRowsD,
@@ -739,6 +801,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
         }
     }
     if (pf_acc == 1.2345e-37f) sm.fail = 2;            // never true: keeps the prefetch loads
+    if (!in(kStages * L)) return;                     // the classifier is in a later launch
 
     // ── classifier: logits = Wcls . rmsnorm(x) (llama2.c:195-197), and this
     //    workgroup's argmax candidate ──
@@ -749,7 +812,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
         const int blocks_cls = (a->V + kRowsD - 1) / kRowsD;
         if (b < blocks_cls) {
             __syncthreads();
-            bool ok = tid >= kPollT || poll_words<5>(a->t_xb + (long)(a->L - 1) * a->D, a->D, tk.tag, sm.xs, a->ctl, tid, a->wait_ticks);
+            bool ok = tid >= kPollT || poll_words<5>(a->t_xb + (long)(a->L - 1) * a->D, a->D, tk.tag, sm.xs, a, tid);
             if (!block_ok(ok, &sm.fail, a->ctl)) return;
             stamp(a, 1 + 10 * a->L);
             for (int rb = b; rb < blocks_cls; rb += nb) {
@@ -811,7 +874,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
     // ── workgroup 0: the step's argmax, prompt forcing and position
     //    advance (pt.c:267-271, pt_text.c:344-350) ──
     __syncthreads();
-    bool ok = tid >= kPollT || poll_words<3>(a->t_cand, 2 * nb, tk.tag, sm.cand, a->ctl, tid, a->wait_ticks);
+    bool ok = tid >= kPollT || poll_words<3>(a->t_cand, 2 * nb, tk.tag, sm.cand, a, tid);
     if (!block_ok(ok, &sm.fail, a->ctl)) return;
     stamp(a, 3 + 10 * a->L);
     bv = -INFINITY;
@@ -858,7 +921,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap) {
     stamp(a, 4 + 10 * a->L);
 }
 
-using StepFn = void (*)(const StepArgs *);
+using StepFn = void (*)(const StepArgs *, int, int);
 
 // Instantiated shapes: (float4 per lane of a D-row, of an H-row, lanes per
 // K/V row).  Other shapes keep the multi-kernel step.
@@ -885,7 +948,7 @@ static const StepKernel *pick_step(const Config &c, int *chunk, int *n_chunks) {
     ch = (ch + gran - 1) / gran * gran;
     if (ch > kMaxChunk) return nullptr;
     const int nc = (c.seq_len + ch - 1) / ch;
-    if ((long)nc * c.n_heads * (c.head_dim + 2) > kPartLds) return nullptr;
+    if (c.n_heads * c.head_dim != c.dim || nc * (c.head_dim + 2) > kPartLds) return nullptr;
     for (const StepKernel &k : kStepKernels)
         if (k.ga == ga && k.itd >= itd && k.ith >= ith && k.itd <= itd + 1 && k.ith <= ith + 2) {
             *chunk = ch;
@@ -910,7 +973,7 @@ int decode_step_create(ptmi_model *m) {
     const long L = c.n_layers, D = c.dim, H = c.hidden, KV = c.kv_dim, NH = c.n_heads, hd = c.head_dim;
     const int nb = std::min(cus, 512);
     // tagged words, then the argument block (32-byte aligned)
-    const size_t words = L * (D + 2 * KV) + L * nc * NH * (hd + 2) + 2 * L * D + L * H + 2 * (size_t)nb;
+    const size_t words = L * (D + 2 * KV) + L * nc * NH * (hd + 2) + 3 * L * D + L * H + 2 * (size_t)nb;
     const char *st_env = getenv("PTMI_STEP_STAMPS");
     const int n_stamps = (st_env && st_env[0] == '1') ? (int)(1 + 10 * L + 4) : 0;
     const size_t args_off = (words * sizeof(uint64_t) + 255) / 256 * 256;
@@ -925,12 +988,21 @@ int decode_step_create(ptmi_model *m) {
     a.D = c.dim; a.H = c.hidden; a.L = c.n_layers; a.NH = c.n_heads; a.KV = c.kv_dim; a.hd = c.head_dim;
     a.kv_mul = c.n_heads / c.n_kv_heads; a.V = c.vocab; a.S = c.seq_len;
     a.chunk = chunk; a.n_chunks = nc;
+    // The attention units sit on the workgroups after the QKV row blocks
+    // when they fit (PTMI_STEP_UNIT_BASE=0: from workgroup 0), so their K/V
+    // loads go out at the start of the QKV stage
+    {
+        const char *ub = getenv("PTMI_STEP_UNIT_BASE");
+        const int blocks_qkv = (int)((D + 2 * KV + kRowsD - 1) / kRowsD);
+        a.ubase = (!(ub && ub[0] == '0') && blocks_qkv + NH * nc <= nb) ? blocks_qkv : 0;
+    }
     a.att_scale = host_att_scale(c.head_dim);
     a.kc = m->kc; a.vc = m->vc; a.logits = m->logits; a.ctl = m->ctl;
     a.prompt = m->prompt; a.out_tokens = m->out_tokens;
     uint64_t *p = reinterpret_cast<uint64_t *>(mem);
     a.t_qkv = p;  p += L * (D + 2 * KV);
     a.t_part = p; p += L * nc * NH * (hd + 2);
+    a.t_att = p;  p += L * D;
     a.t_xa = p;   p += L * D;
     a.t_xb = p;   p += L * D;
     a.t_hb = p;   p += L * H;
@@ -941,6 +1013,10 @@ int decode_step_create(ptmi_model *m) {
     // timeout path: the step then fails and reports, and every wave exits)
     const char *wt = getenv("PTMI_STEP_WAIT_TICKS");
     a.wait_ticks = wt ? strtoull(wt, nullptr, 10) : kWaitTicks;
+    const char *ps = getenv("PTMI_STEP_POLL_SLEEP");
+    a.poll_sleep = ps ? std::max(0, std::min(64, atoi(ps))) : 1;
+    const char *pf = getenv("PTMI_STEP_L2PF");
+    a.l2pf = pf ? atoi(pf) & 3 : 2;
     hipError_t e = hipMemsetAsync(mem, 0, total, lib_stream());
     if (e == hipSuccess) e = hipMemcpyAsync(mem + args_off, &a, sizeof(a), hipMemcpyHostToDevice, lib_stream());
     if (e == hipSuccess) e = hipStreamSynchronize(lib_stream());
@@ -952,6 +1028,20 @@ int decode_step_create(ptmi_model *m) {
     m->step_chunks = nc;
     m->step_stamps = a.stamps;
     m->step_n_stamps = n_stamps;
+    // Launch windows: PTMI_STEP_SPLIT names the stages before which a new
+    // launch starts, in every layer: q QKV, a attention, o Wo, f w1|w3,
+    // d w2, c the classifier.  Unset or empty: one launch per token.
+    m->step_cuts.assign(1, 0);
+    if (const char *sp = getenv("PTMI_STEP_SPLIT")) {
+        static const char kLetters[] = "qaofd";
+        for (const char *q = sp; *q; q++)
+            if (!strchr("qaofdc", *q)) return set_error(PTMI_ERR_ARG, "PTMI_STEP_SPLIT: unknown stage '%c'", *q);
+        for (long g = 1; g <= kStages * L; g++) {
+            const bool cut = g == kStages * L ? strchr(sp, 'c') != nullptr : strchr(sp, kLetters[g % kStages]) != nullptr;
+            if (cut) m->step_cuts.push_back((int)g);
+        }
+    }
+    m->step_cuts.push_back((int)(kStages * L + 1));
     return PTMI_OK;
 }
 
@@ -961,13 +1051,16 @@ void decode_step_destroy(ptmi_model *m) {
     m->step_args = nullptr;
 }
 
-int launch_decode_step(ptmi_model *m, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+int decode_step_windows(const ptmi_model *m) { return (int)m->step_cuts.size() - 1; }
+
+int launch_decode_step(ptmi_model *m, int w, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     int chunk = 0, nc = 0;
     const StepKernel *k = pick_step(m->c, &chunk, &nc);
     if (!k || !m->step_args || chunk != m->step_chunk || nc != m->step_chunks)
         return set_error(PTMI_ERR_STATE, "decode step kernel not set up for this model");
+    if (w < 0 || w >= decode_step_windows(m)) return set_error(PTMI_ERR_ARG, "decode step window %d out of range", w);
     const StepArgs *args = reinterpret_cast<const StepArgs *>(m->step_args);
-    launch_k(k->fn, dim3(m->step_nb), dim3(kT), 0, s, e0, e1, args);
+    launch_k(k->fn, dim3(m->step_nb), dim3(kT), 0, s, e0, e1, args, m->step_cuts[w], m->step_cuts[w + 1]);
     PTMI_HIP(hipGetLastError());
     return PTMI_OK;
 }

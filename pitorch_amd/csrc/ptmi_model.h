@@ -3,6 +3,8 @@
 
 #include "ptmi_internal.h"
 
+#include <vector>
+
 namespace ptmi {
 
 // Per-step control block in device memory.  Kernels of a captured decode
@@ -57,6 +59,7 @@ struct ptmi_model {
     int step_chunk = 0, step_chunks = 0; // attention positions per unit, units per head
     uint64_t *step_stamps = nullptr;     // stage stamps (PTMI_STEP_STAMPS=1)
     int step_n_stamps = 0;
+    std::vector<int> step_cuts;          // launch windows: stages [cuts[w], cuts[w+1])
     ptmi::TrainState *train = nullptr;
 };
 
@@ -69,5 +72,6 @@ float host_att_scale(int head_dim);
 // has an instantiated kernel), tear down, enqueue one step.
 int  decode_step_create(ptmi_model *m);
 void decode_step_destroy(ptmi_model *m);
-int  launch_decode_step(ptmi_model *m, hipStream_t s, hipEvent_t e0, hipEvent_t e1);
+int  decode_step_windows(const ptmi_model *m);
+int  launch_decode_step(ptmi_model *m, int w, hipStream_t s, hipEvent_t e0, hipEvent_t e1);
 }

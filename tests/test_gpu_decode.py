@@ -5,9 +5,9 @@ make_golden.py).  Greedy tokens must be IDENTICAL over the full runs
 (256 positions for 15M, 1024 for 42M/110M); logits are compared with the
 oracle at a relative tolerance (matvec reduction order differs).
 
-Both decode paths are held to this: the captured multi-kernel step (the
-default) and the one-kernel step (PTMI_DECODE_STEP=1, read when a model is
-created).
+Every decode path is held to this: the captured multi-kernel step (the
+default), the one-kernel step (PTMI_DECODE_STEP=1, read when a model is
+created) and that step cut into launch windows (PTMI_STEP_SPLIT).
 """
 import ctypes
 import hashlib
@@ -24,19 +24,22 @@ pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-@pytest.fixture(params=["multi_kernel", "one_kernel"])
+@pytest.fixture(params=["multi_kernel", "one_kernel", "windows"])
 def decode_path(request, monkeypatch):
-    monkeypatch.setenv("PTMI_DECODE_STEP", "1" if request.param == "one_kernel" else "0")
+    """The captured multi-kernel step, the one-kernel step, and the
+    one-kernel step cut into two launches per layer (PTMI_STEP_SPLIT=qo)."""
+    monkeypatch.setenv("PTMI_DECODE_STEP", "0" if request.param == "multi_kernel" else "1")
+    monkeypatch.setenv("PTMI_STEP_SPLIT", "qo" if request.param == "windows" else "")
     return request.param
 
 
 def check_path(m, decode_path):
     """The model ran the decode path the test was parametrized for (one
-    profiled step from position 0: a "step" launch only on the one-kernel
-    path)."""
+    profiled step from position 0: "step" launches only on the one-kernel
+    path, one per launch window of PTMI_STEP_SPLIT)."""
     m.reset_kv()
     prof = m.profile(1, 1)
-    assert prof["step"][1] == (1 if decode_path == "one_kernel" else 0), prof["step"]
+    assert (prof["step"][1] >= 1) == (decode_path != "multi_kernel"), prof["step"]
 
 
 def fixture(name):
@@ -213,25 +216,38 @@ def test_reference_forward_with_ptmi_matvec_dropin():
         L.ptmi_unregister_weights(P(blob))
 
 
-@pytest.mark.parametrize("one_kernel", [True, False])
-def test_profile_roles_cover_every_launch(one_kernel, monkeypatch):
-    """The one-kernel step is one launch per token (role "step"); the
-    multi-kernel step (PTMI_DECODE_STEP=0) is 5 launches per layer plus the
-    classifier and the argmax."""
-    monkeypatch.setenv("PTMI_DECODE_STEP", "1" if one_kernel else "0")
+@pytest.mark.parametrize("mode", ["graph", "one_kernel", "split_qo", "split_qaofdc"])
+def test_profile_roles_cover_every_launch(mode, monkeypatch):
+    """The one-kernel step is one launch per token (role "step"), or one per
+    launch window when PTMI_STEP_SPLIT cuts it before chosen stages of every
+    layer; the multi-kernel step (PTMI_DECODE_STEP=0) is 5 launches per layer
+    plus the classifier and the argmax."""
+    monkeypatch.setenv("PTMI_DECODE_STEP", "0" if mode == "graph" else "1")
+    split = mode[len("split_"):] if mode.startswith("split_") else ""
+    monkeypatch.setenv("PTMI_STEP_SPLIT", split)
     cfg = pa.STORIES["stories15M"]
     blob = model_for("stories15M")
     m = pa.Model(blob)
     prof = m.profile(1, 4)
     Lyr = cfg[2]
-    if one_kernel:
-        assert prof["step"][1] == 4 and prof["step"][0] > 0
+    if mode != "graph":
+        per_layer = sum(c in split for c in "qaofd")
+        windows = 1 + per_layer * Lyr - ("q" in split) + ("c" in split)
+        assert prof["step"][1] == 4 * windows and prof["step"][0] > 0
         assert all(cnt == 0 for r, (ms, cnt) in prof.items() if r != "step")
     else:
         assert prof["qkv"][1] == prof["attention"][1] == prof["wo"][1] == prof["w13"][1] == prof["w2"][1] == 4 * Lyr
         assert prof["classifier"][1] == prof["argmax"][1] == 4 and prof["step"][1] == 0
         assert all(ms > 0 for r, (ms, _) in prof.items() if r != "step")
     m.close()
+
+
+def test_step_split_rejects_unknown_stage(monkeypatch):
+    """PTMI_STEP_SPLIT takes only the stage letters q a o f d c."""
+    monkeypatch.setenv("PTMI_DECODE_STEP", "1")
+    monkeypatch.setenv("PTMI_STEP_SPLIT", "qx")
+    with pytest.raises(pa.PtmiError):
+        pa.Model(model_for("stories15M"))
 
 
 def test_one_kernel_step_stage_stamps(monkeypatch):
