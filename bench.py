@@ -384,12 +384,20 @@ def step_stamps(pa, name, at):
                   f"{np.median(rel[s_]):.2f} | {max(rel[s_]):.2f} | {np.median(work[s_]):.2f} |")
         layer = np.diff(np.array(layer_ends)) * us
         total = (st[st > 0].max() - st[:, 0].min()) * us
-        rows.append((pos, np.median(layer), layer.max(), total))
+        # the step's two ends: workgroup starts, then the classifier (from
+        # the last w2 workgroup to the last classifier workgroup) and the
+        # final argmax on workgroup 0 (its wait for every candidate, then
+        # the end)
+        c0 = 1 + 10 * L
+        cls_end = st[:, c0 + 1][st[:, c0 + 1] > 0].max()
+        rows.append((pos, np.median(layer), layer.max(), total, (st[:, 0].max() - st[:, 0].min()) * us,
+                     (cls_end - prev_end) * us, (st[0, c0 + 2] - cls_end) * us, (st[0, c0 + 3] - st[0, c0 + 2]) * us))
     print()
-    print("| position | layer median µs | layer max µs | step (first start to last stamp) µs |")
-    print("|---:|---:|---:|---:|")
-    for pos, med, mx, total in rows:
-        print(f"| {pos} | {med:.2f} | {mx:.2f} | {total:.2f} |")
+    print("| position | layer median µs | layer max µs | step (first start to last stamp) µs "
+          "| workgroup start spread µs | classifier span µs | argmax release µs | argmax work µs |")
+    print("|---:|---:|---:|---:|---:|---:|---:|---:|")
+    for pos, med, mx, total, spread, cls, arel, awork in rows:
+        print(f"| {pos} | {med:.2f} | {mx:.2f} | {total:.2f} | {spread:.2f} | {cls:.2f} | {arel:.2f} | {awork:.2f} |")
     m.close()
 
 
