@@ -673,7 +673,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
         // ── WO: x_a = x + Wo . att (llama2.c:179-180) ──
         if (in(kStages * l + 2)) {
             const PTMI_CONST StepArgs *a = fresh(ap);
-            const int D = a->D, H = a->H, hd = a->hd, NH = a->NH;
+            const int D = a->D, H = a->H;
             const int blocks_wo = (D + kRowsD - 1) / kRowsD, blocks_w13 = (2 * H + kRowsD - 1) / kRowsD;
             const float *x_emb = a->emb + (long)tk.token * D;
             const uint64_t *t_xin = a->t_xb + (long)(l - 1) * D;      // used for l > 0 only

@@ -43,6 +43,7 @@ struct GemmArgs {
     float *partial;        // split-K workspace [splits][M][N] or null
     int k_per_split;
     GemmEpi epi;           // fused element-wise epilogue (whole-K launches only)
+    GemmNorm nrm;          // fused RMSNorm of the A rows (NT, whole K)
     float *upd;            // fused SGD step of the weight C is the gradient of (TnGemm), or null
     const float *lr;
     const unsigned *keep;
@@ -157,7 +158,7 @@ __device__ __forceinline__ void store_tile(float (*S)[R], int tid, const float (
 // 4*(l/16) + r, column l%16 of it (the 16x16x4 MFMA result layout).
 template <int EPI, int FM, int FN>
 __device__ __forceinline__ void gemm_store(const GemmArgs &g, const floatx4 (&acc)[FM][FN], int mb, int nb, int z,
-                                           int li, int lk) {
+                                           int li, int lk, const float *rs = nullptr, int rs_m0 = 0) {
     const float lrv = g.upd ? *g.lr : 0.0f;
     // C[4*(l/16)+r][l%16] of each 16x16 block; columns n and n^1 of a row sit
     // in lanes l and l^1, which the fused epilogues pair with a DPP swap
@@ -171,6 +172,7 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &g, const floatx4 (&ac
             for (int r = 0; r < 4; r++) {
                 const int m = mb + i * 16 + 4 * lk + r;
                 float v = acc[i][j][r];
+                if (rs) v *= rs[m - rs_m0];                     // fused RMSNorm: the row's 1/rms
                 if constexpr (EPI == GEMM_EPI_ROPE) {
                     // RoPE of the q and k columns at position m (pt_ops.c:33-49;
                     // training forward pt_train.c:217)
@@ -221,12 +223,66 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &g, const floatx4 (&ac
     }
 }
 
+// Fused RMSNorm: the block of N tile j stores its share of rows m0 ..
+// m0+R-1 (float4 columns [j*c4, (j+1)*c4) of K/4, c4 = ceil(K/4 / tiles))
+// of X (to x_out when completed here) and of X * inv * w (to xn_out), all
+// loads of a pass in flight together; the block of tile 0 also marks the
+// rows' tokens (EMBED, rows < M-1) in tok_bits.
+template <int NORM, int R>
+__device__ __forceinline__ void norm_rows_out(const GemmArgs &g, int m0, int j, int tiles, const float *inv) {
+    const GemmNorm &nm = g.nrm;
+    const int K4 = g.K / 4, c4 = (K4 + tiles - 1) / tiles, c_lo = j * c4, c_n = min(c4, K4 - c_lo);
+    const int tid = threadIdx.x;
+    const float *zero = g_gemm_zero;
+    for (int e = tid; e < R * c_n; e += 256) {
+        const int r = e / c_n, m = m0 + r;
+        const bool in = m < g.M;
+        const long col = 4L * (c_lo + (e - r * c_n));
+        const long o = (long)min(m, g.M - 1) * g.K + col;
+        float4 x;
+        if constexpr (NORM == GEMM_NORM_SPLITS) {
+            float4 p[kNormSplits];
+#pragma unroll
+            for (int zz = 0; zz < kNormSplits; zz++)
+                p[zz] = *reinterpret_cast<const float4 *>(zz < nm.pk.splits ? nm.pk.parts + zz * nm.pk.stride + o : zero);
+            const float4 c = *reinterpret_cast<const float4 *>(nm.cin ? nm.cin + o : zero);
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int zz = 0; zz < kNormSplits; zz++) {
+                const bool use = zz < nm.pk.splits;
+                v.x = use ? v.x + p[zz].x : v.x;
+                v.y = use ? v.y + p[zz].y : v.y;
+                v.z = use ? v.z + p[zz].z : v.z;
+                v.w = use ? v.w + p[zz].w : v.w;
+            }
+            x = nm.cin ? make_float4(c.x + v.x, c.y + v.y, c.z + v.z, c.w + v.w) : v;
+        } else if constexpr (NORM == GEMM_NORM_EMBED) {
+            x = *reinterpret_cast<const float4 *>(nm.emb + (long)nm.tok[min(m, g.M - 1)] * g.K + col);
+        } else {
+            x = *reinterpret_cast<const float4 *>(g.A + o);
+        }
+        const float4 w = *reinterpret_cast<const float4 *>(nm.w + col);
+        if (!in) continue;
+        if constexpr (NORM != GEMM_NORM_PLAIN) *reinterpret_cast<float4 *>(nm.x_out + o) = x;
+        const float iv = inv[r];
+        *reinterpret_cast<float4 *>(nm.xn_out + o) = make_float4(x.x * iv * w.x, x.y * iv * w.y, x.z * iv * w.z, x.w * iv * w.w);
+    }
+    if constexpr (NORM == GEMM_NORM_EMBED) {
+        const int m = m0 + tid;
+        if (j == 0 && tid < R && m < g.M - 1) {
+            const int tk = nm.tok[m];
+            atomicOr(&nm.tok_bits[tk >> 5], 1u << (tk & 31));
+        }
+    }
+}
+
 // One TMxTN output tile of g at (m0, n0) over K range split z.  The LDS
 // tiles use the swizzled layout of lds_col.
-template <bool AT, bool BT, int TM, int TN, int P, bool VEC, int EPI = GEMM_EPI_NONE>
+template <bool AT, bool BT, int TM, int TN, int P, bool VEC, int EPI = GEMM_EPI_NONE, int NORM = 0>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int z) {
     constexpr int FM = TM / 32, FN = TN / 32;          // 16x16 MFMA blocks per wave
     constexpr int EA = TM * BK / 256, EB = TN * BK / 256;
+    static_assert(NORM == 0 || (!AT && TM == 32 && VEC && EA == 4), "fused norm: NT, 32-row float4 A tiles");
     __shared__ float As[2][BK][TM];
     __shared__ float Bs[2][BK][TN];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -245,12 +301,61 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
     // P K tiles in flight in a register ring (tile t in slot t % P); the
     // loop is unrolled by P so every slot index is a compile-time constant.
     float ra[P][EA], rb[P][EB];
-    auto load = [&](int s, float (&xa)[EA], float (&xb)[EB]) {
-        load_tile<AT, TM, VEC>(g.A, g.lda, g.M, m0, kb + s * BK, kend, tid, xa);
+    // Fused RMSNorm: thread tid owns A row na_i and k offset na_k of every K
+    // step (the load_tile mapping); the ring holds the raw row values (the
+    // split-K partials and the addend, summed at the LDS store) and the norm
+    // weights; the A tile takes x * w, and the row's sum of squares builds up.
+    constexpr int NL = NORM == GEMM_NORM_SPLITS ? kNormSplits + 1 : 1;
+    const int na_i = m0 + tid / (BK / EA), na_k = EA * (tid % (BK / EA));
+    float4 nr[P][NL], ng[P];
+    float nss = 0.0f;
+    const float *na_row = g.A + (long)min(na_i, g.M - 1) * g.lda;
+    if constexpr (NORM == GEMM_NORM_EMBED) na_row = g.nrm.emb + (long)g.nrm.tok[min(na_i, g.M - 1)] * g.K;
+    auto load = [&](int s, int slot, float (&xa)[EA], float (&xb)[EB]) {
+        if constexpr (NORM != 0) {
+            const float *zero = g_gemm_zero;
+            const int k = kb + s * BK + na_k;
+            const bool in = na_i < g.M && k < kend;
+            if constexpr (NORM == GEMM_NORM_SPLITS) {
+                const long o = (long)min(na_i, g.M - 1) * g.K + k;
+#pragma unroll
+                for (int zz = 0; zz < kNormSplits; zz++)
+                    nr[slot][zz] = *reinterpret_cast<const float4 *>(
+                        in && zz < g.nrm.pk.splits ? g.nrm.pk.parts + zz * g.nrm.pk.stride + o : zero);
+                nr[slot][kNormSplits] = *reinterpret_cast<const float4 *>(in && g.nrm.cin ? g.nrm.cin + o : zero);
+            } else {
+                nr[slot][0] = *reinterpret_cast<const float4 *>(in ? na_row + k : zero);
+            }
+            ng[slot] = *reinterpret_cast<const float4 *>(in ? g.nrm.w + k : zero);
+        } else {
+            load_tile<AT, TM, VEC>(g.A, g.lda, g.M, m0, kb + s * BK, kend, tid, xa);
+        }
         load_tile<!BT, TN, VEC>(g.B, g.ldb, g.N, n0, kb + s * BK, kend, tid, xb);
     };
-    auto store = [&](int s, const float (&xa)[EA], const float (&xb)[EB]) {
-        store_tile<AT, TM>(As[s & 1], tid, xa);
+    auto store = [&](int s, int slot, const float (&xa)[EA], const float (&xb)[EB]) {
+        if constexpr (NORM != 0) {
+            float4 x = nr[slot][0];
+            if constexpr (NORM == GEMM_NORM_SPLITS) {
+                // the standalone kernel's order: ((0 + p0) + p1) + ..., then cin + sum
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int zz = 0; zz < kNormSplits; zz++) {
+                    const bool use = zz < g.nrm.pk.splits;
+                    v.x = use ? v.x + nr[slot][zz].x : v.x;
+                    v.y = use ? v.y + nr[slot][zz].y : v.y;
+                    v.z = use ? v.z + nr[slot][zz].z : v.z;
+                    v.w = use ? v.w + nr[slot][zz].w : v.w;
+                }
+                const float4 c = nr[slot][kNormSplits];
+                x = g.nrm.cin ? make_float4(c.x + v.x, c.y + v.y, c.z + v.z, c.w + v.w) : v;
+            }
+            nss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+            const float4 w = ng[slot];
+            const float xw[EA] = {x.x * w.x, x.y * w.y, x.z * w.z, x.w * w.w};
+            store_tile<AT, TM>(As[s & 1], tid, xw);
+        } else {
+            store_tile<AT, TM>(As[s & 1], tid, xa);
+        }
         store_tile<!BT, TN>(Bs[s & 1], tid, xb);
     };
     // The operands of k group kk+4*RA are read from LDS before the MFMAs of
@@ -286,8 +391,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
     // Loads are unconditional (tiles past the K range read zeros): a load
     // under a branch leaves the compiler unsure how many loads are in flight,
     // and it then waits for all of them, which empties the ring.
-    for (int t = 0; t < P; t++) load(t, ra[t], rb[t]);
-    store(0, ra[0], rb[0]);
+    for (int t = 0; t < P; t++) load(t, t, ra[t], rb[t]);
+    store(0, 0, ra[0], rb[0]);
     __syncthreads();
     // Step s: tile s is in LDS; its register slot (s % P) is free, so tile
     // s+P is fetched into it; tile s+1 goes to the other LDS buffer.  Full
@@ -296,10 +401,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
     for (; s0 + P <= nk; s0 += P) {
 #pragma unroll
         for (int u = 0; u < P; u++) {
-            load(s0 + u + P, ra[u], rb[u]);
+            load(s0 + u + P, u, ra[u], rb[u]);
             __builtin_amdgcn_sched_barrier(0);              // issue the loads before the MFMAs
             compute(s0 + u);
-            store(s0 + u + 1, ra[(u + 1) % P], rb[(u + 1) % P]);
+            store(s0 + u + 1, (u + 1) % P, ra[(u + 1) % P], rb[(u + 1) % P]);
             __syncthreads();
         }
     }
@@ -307,12 +412,23 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
     for (int u = 0; u + 1 < P; u++) {
         if (s0 + u < nk) {                                  // uniform
             compute(s0 + u);
-            store(s0 + u + 1, ra[(u + 1) % P], rb[(u + 1) % P]);
+            store(s0 + u + 1, (u + 1) % P, ra[(u + 1) % P], rb[(u + 1) % P]);
             __syncthreads();
         }
     }
 
-    gemm_store<EPI, FM, FN>(g, acc, m0 + wm * (TM / 2), n0 + wn * (TN / 2), z, li, lk);
+    if constexpr (NORM != 0) {
+        // 1/rms of the block's rows (the standalone kernel's formula); every
+        // N tile's block stores its share of the rows and normalized rows
+        __shared__ float n_inv[TM];
+        nss = group_sum<BK / EA>(nss);
+        if (tid % (BK / EA) == 0) n_inv[tid / (BK / EA)] = 1.0f / d_sqrtf(nss / (float)g.K + 1e-5f);
+        __syncthreads();
+        norm_rows_out<NORM, TM>(g, m0, n0 / TN, (g.N + TN - 1) / TN, n_inv);
+        gemm_store<EPI, FM, FN>(g, acc, m0 + wm * (TM / 2), n0 + wn * (TN / 2), z, li, lk, n_inv, m0);
+    } else {
+        gemm_store<EPI, FM, FN>(g, acc, m0 + wm * (TM / 2), n0 + wn * (TN / 2), z, li, lk);
+    }
 }
 
 // ── Direct-to-LDS tiles for the large training GEMMs ─────────────────────
@@ -486,7 +602,7 @@ __device__ __forceinline__ int xcd_tile(int b, int total) {
 // index slowest; within a split, neighbouring tiles share the tile of the
 // larger operand (A's rows when M > N, else B's columns).  Smaller grids
 // (at most a few blocks per CU, no reuse to gain) keep the grid's order.
-template <bool AT, bool BT, int TM, int TN, int P, bool VEC, int EPI = GEMM_EPI_NONE>
+template <bool AT, bool BT, int TM, int TN, int P, bool VEC, int EPI = GEMM_EPI_NONE, int NORM = 0>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     const int gx = gridDim.x, gy = gridDim.y, per_z = gx * gy, total = per_z * gridDim.z;
     int m = blockIdx.y, n = blockIdx.x, z = blockIdx.z;
@@ -497,7 +613,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
         if (g.M > g.N) m = u / gx, n = u - m * gx;
         else n = u / gy, m = u - n * gy;
     }
-    gemm_tile<AT, BT, TM, TN, P, VEC, EPI>(g, m * TM, n * TN, z);
+    gemm_tile<AT, BT, TM, TN, P, VEC, EPI, NORM>(g, m * TM, n * TN, z);
 }
 
 // The direct-to-LDS GEMM (grid and tile order as k_gemm).
@@ -566,6 +682,21 @@ SplitPlan split_plan(int op, int M, int N, int K, size_t ws_floats, int ek) {
 
 }  // namespace
 
+bool gemm_norm_fusable(int M, int N, int K, const float *A, long lda, const float *B, long ldb, int epi_kind,
+                       const GemmNorm &nm) {
+    if (nm.kind < GEMM_NORM_PLAIN || nm.kind > GEMM_NORM_EMBED || !nm.w || !nm.xn_out) return false;
+    if (epi_kind != GEMM_EPI_ROPE && epi_kind != GEMM_EPI_SWIGLU) return false;
+    if (M <= 0 || N <= 0 || K <= 0 || K % 4 || lda != K || ldb % 4 || ldb < K || gemm_big_tiles(2, M, N, K)) return false;
+    if (!A || !B || !al16(A) || !al16(B) || !al16(nm.w) || !al16(nm.xn_out)) return false;
+    if (nm.kind != GEMM_NORM_PLAIN && (!nm.x_out || !al16(nm.x_out))) return false;
+    if (nm.kind == GEMM_NORM_SPLITS &&
+        (nm.pk.splits < 1 || nm.pk.splits > kNormSplits || !nm.pk.parts || !al16(nm.pk.parts) || nm.pk.stride % 4 ||
+         nm.pk.stride < (long)M * K || (nm.cin && !al16(nm.cin))))
+        return false;
+    if (nm.kind == GEMM_NORM_EMBED && (!nm.tok || !nm.emb || !nm.tok_bits || !al16(nm.emb))) return false;
+    return true;
+}
+
 size_t gemm_workspace_floats(int op, int M, int N, int K, size_t ws_floats) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     const SplitPlan p = split_plan(op, M, N, K, ws_floats, GEMM_EPI_NONE);
@@ -576,9 +707,12 @@ size_t gemm_workspace_floats(int op, int M, int N, int K, size_t ws_floats) {
 // workspace of ws_floats floats.
 int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc, int M, int N,
                 int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s, const float *Cin, SplitK *defer,
-                const GemmEpi *epi) {
+                const GemmEpi *epi, const GemmNorm *norm) {
     if (defer) *defer = SplitK{nullptr, 0, 0};
     const int ek = epi ? epi->kind : GEMM_EPI_NONE;
+    const int nk_kind = norm ? norm->kind : 0;
+    if (nk_kind && (op != 2 || accumulate || !gemm_norm_fusable(M, N, K, A, lda, B, ldb, ek, *norm)))
+        return set_error(PTMI_ERR_ARG, "gemm: the fused norm does not fit this GEMM");
     if (ek == GEMM_EPI_SWIGLU_BWD ? (op != 0 || !epi->out || !epi->out2 || !epi->aux)
                                   : ek != GEMM_EPI_NONE && (op != 2 || N % 2 || (ek == GEMM_EPI_SWIGLU && !epi->out) ||
                                                             (ek == GEMM_EPI_ROPE && (epi->rope_dim % 2 || epi->head_dim <= 0))))
@@ -613,6 +747,7 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
     g.k_per_split = plan.k_per_split;
     g.partial = splits > 1 ? ws : nullptr;
     g.epi = epi ? *epi : GemmEpi{};
+    g.nrm = norm ? *norm : GemmNorm{};
     if (gy > 65535) return set_error(PTMI_ERR_ARG, "gemm: M too large");
     dim3 grid(gx, gy, splits);
     using KFn = void (*)(GemmArgs);
@@ -638,6 +773,17 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
             {k_gemm<false, false, 64, 64, kRing64, false, GEMM_EPI_SWIGLU_BWD>,
              k_gemm<false, false, 64, 64, kRing64, true, GEMM_EPI_SWIGLU_BWD>}};
         fn = ek == GEMM_EPI_SWIGLU_BWD ? fused_nn[big][vec] : fused[ek == GEMM_EPI_SWIGLU][big][vec];
+    }
+    if (nk_kind) {                                       // fusable: 32x32 float4 tiles, whole K
+        static const KFn fused_norm[2][3] = {
+            {k_gemm<false, true, 32, 32, kRing32, true, GEMM_EPI_ROPE, GEMM_NORM_PLAIN>,
+             k_gemm<false, true, 32, 32, kRing32, true, GEMM_EPI_ROPE, GEMM_NORM_SPLITS>,
+             k_gemm<false, true, 32, 32, kRing32, true, GEMM_EPI_ROPE, GEMM_NORM_EMBED>},
+            {k_gemm<false, true, 32, 32, kRing32, true, GEMM_EPI_SWIGLU, GEMM_NORM_PLAIN>,
+             k_gemm<false, true, 32, 32, kRing32, true, GEMM_EPI_SWIGLU, GEMM_NORM_SPLITS>,
+             k_gemm<false, true, 32, 32, kRing32, true, GEMM_EPI_SWIGLU, GEMM_NORM_EMBED>}};
+        if (big || !vec || splits != 1) return set_error(PTMI_ERR_STATE, "gemm: fused norm without whole-K float4 tiles");
+        fn = fused_norm[ek == GEMM_EPI_SWIGLU][nk_kind - 1];
     }
     int threads = 256;
     // The large whole-K GEMMs without a fused epilogue (the classifier's

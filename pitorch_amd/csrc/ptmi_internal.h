@@ -360,6 +360,36 @@ struct GemmEpi {
     long aux_ld;
 };
 
+// RMSNorm (pt_ops.c:5-12) fused into the A operand of an NT GEMM with a
+// fused epilogue (whole K = the row length, 32x32 tiles, float4 rows):
+// C = epi(diag(inv) . (X . diag(w)) . B^T), inv[m] = 1/sqrt(mean_k x[m][k]^2
+// + 1e-5), where the rows X are
+//   PLAIN:  A itself;
+//   SPLITS: cin + the pending split-K partial sums pk (at most kNormSplits);
+//   EMBED:  emb[tok[m]] (and tok_bits marks the tokens of rows < M-1).
+// The blocks of each row tile also store, each a share of the columns, X
+// to x_out (SPLITS, EMBED) and the normalized rows x * inv * w to xn_out, as
+// the standalone RMSNorm kernel does.  Every row array has leading
+// dimension K.
+enum { GEMM_NORM_PLAIN = 1, GEMM_NORM_SPLITS = 2, GEMM_NORM_EMBED = 3 };
+constexpr int kNormSplits = 4;
+struct GemmNorm {
+    int kind;              // 0: no fused norm
+    const float *w;        // norm weights [K]
+    SplitK pk;             // SPLITS
+    const float *cin;      // SPLITS: residual addend (may be null)
+    const int *tok;        // EMBED
+    const float *emb;
+    unsigned *tok_bits;
+    float *x_out;          // SPLITS, EMBED: the completed rows
+    float *xn_out;         // the normalized rows
+};
+// Whether launch_gemm fuses the norm nm into the NT GEMM [M,N,K] with A
+// rows of stride lda, B = W [N][K] (stride ldb) and epilogue `epi_kind`
+// (else the caller runs the norm, then the GEMM).
+bool gemm_norm_fusable(int M, int N, int K, const float *A, long lda, const float *B, long ldb, int epi_kind,
+                       const GemmNorm &nm);
+
 // C[M,N] (+)= op(A).op(B) on the matrix cores; op 0 NN, 1 TN (A stored
 // [K][M]), 2 NT (B stored [N][K]).  ws: split-K workspace (may be null).
 // With accumulate, Cin (same leading dimension as C; null = C itself) is
@@ -368,7 +398,7 @@ struct GemmEpi {
 // C is then not written); otherwise defer->splits = 0.
 int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc, int M, int N,
                 int K, int accumulate, float *ws, size_t ws_floats, hipStream_t s, const float *Cin = nullptr,
-                SplitK *defer = nullptr, const GemmEpi *epi = nullptr);
+                SplitK *defer = nullptr, const GemmEpi *epi = nullptr, const GemmNorm *norm = nullptr);
 
 // Workspace floats launch_gemm needs to split this GEMM's K the way it does
 // with a workspace of ws_floats floats (0: no split).

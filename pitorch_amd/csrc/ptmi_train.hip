@@ -52,6 +52,9 @@ struct TrainState {
     hipGraphExec_t exec = nullptr;
     int graph_T = 0;
     bool eager = false;
+    // Which RMSNorm kinds run fused into the next GEMM where launch_gemm can:
+    // bit k-1 for GemmNorm kind k (PTMI_TRAIN_FUSE_NORM overrides)
+    int fuse_norm = 5;
 };
 
 namespace {
@@ -1171,6 +1174,8 @@ int train_create(ptmi_model *m) {
     if (e != hipSuccess) { (void)hipFree(ts->mem); delete ts; return hip_check(e, "zero training state"); }
     const char *eager = getenv("PTMI_TRAIN_EAGER");
     ts->eager = eager && eager[0] == '1';
+    const char *fuse = getenv("PTMI_TRAIN_FUSE_NORM");
+    if (fuse) ts->fuse_norm = atoi(fuse) & 7;
     m->train = ts;
     return PTMI_OK;
 }
@@ -1188,8 +1193,8 @@ namespace {
 
 int gemm(hipStream_t s, TrainState *ts, int op, const float *A, long lda, const float *B, long ldb, float *C, long ldc,
          int M, int N, int K, int acc, const float *Cin = nullptr, SplitK *defer = nullptr,
-         const GemmEpi *epi = nullptr) {
-    return launch_gemm(op, A, lda, B, ldb, C, ldc, M, N, K, acc, ts->ws, ts->ws_floats, s, Cin, defer, epi);
+         const GemmEpi *epi = nullptr, const GemmNorm *norm = nullptr) {
+    return launch_gemm(op, A, lda, B, ldb, C, ldc, M, N, K, acc, ts->ws, ts->ws_floats, s, Cin, defer, epi, norm);
 }
 
 void fill0(hipStream_t s, float *p, long n) {
@@ -1360,6 +1365,22 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr
             hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, in, w, out, D, pk, cin);
         }
     };
+    // RMSNorm then an NT GEMM with a fused epilogue, C = epi(rmsnorm(x) . W^T):
+    // the norm runs inside the GEMM's A loads when launch_gemm can fuse it
+    // (the first N tile's blocks then store x and the normalized rows as
+    // the norm kernel would), else as its own launch first.
+    auto norm_gemm = [&](float *in, const float *w, float *out, SplitK pk, const float *cin, bool embed,
+                         const float *W, int N, float *C, const GemmEpi *epi) -> int {
+        GemmNorm nm = {};
+        nm.kind = embed ? GEMM_NORM_EMBED : pk.splits > 0 ? GEMM_NORM_SPLITS : GEMM_NORM_PLAIN;
+        nm.w = w; nm.pk = pk; nm.cin = cin;
+        nm.tok = ts->tok; nm.emb = r->emb; nm.tok_bits = ts->tok_bits;
+        nm.x_out = in; nm.xn_out = out;
+        if (wave_norm && (ts->fuse_norm >> (nm.kind - 1) & 1) && gemm_norm_fusable(T, N, D, in, D, W, D, epi->kind, nm))
+            return gemm(s, ts, 2, in, D, W, D, C, N, T, N, D, 0, nullptr, nullptr, epi, &nm);
+        norm_fwd(in, w, out, pk, cin, embed);
+        return gemm(s, ts, 2, out, D, W, D, C, N, T, N, D, 0, nullptr, nullptr, epi);
+    };
     const bool tied = r->wcls == r->emb;
     SPAN("train_step", "train", -1);                      // pt.c:339-364
     SPAN("zero_grads", "train", -1);
@@ -1382,10 +1403,10 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr
         float *ao = ts->att_out + l * TD, *xf = ts->xb_ffn + l * TD, *h13 = ts->h13 + (long)l * T * 2 * H;
         SPAN("layer", "fwd", l);
         SPAN("qkv", "fwd", l);
-        norm_fwd(rin, r->rms_att + (long)l * D, xa, pend, pend_cin, l == 0);
-        // qkv = x . Wqkv^T with RoPE on the q and k columns in the GEMM's epilogue
+        // qkv = rmsnorm(x) . Wqkv^T with RoPE on the q and k columns in the GEMM's epilogue
         const GemmEpi rope = {GEMM_EPI_ROPE, nullptr, 0, D, hd};
-        if ((st = gemm(s, ts, 2, xa, D, r->wqkv + (long)l * QS * D, D, qkv, QS, T, QS, D, 0, nullptr, nullptr, &rope)))
+        if ((st = norm_gemm(rin, r->rms_att + (long)l * D, xa, pend, pend_cin, l == 0, r->wqkv + (long)l * QS * D, QS,
+                            qkv, &rope)))
             return st;
         SPAN_END();
         SPAN("attention", "fwd", l);
@@ -1400,11 +1421,10 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr
         if ((st = gemm(s, ts, 2, ao, D, r->wo + (long)l * D * D, D, rmid, D, T, D, D, 1, rin))) return st;
         SPAN_END();
         SPAN("ffn", "fwd", l);
-        norm_fwd(rmid, r->rms_ffn + (long)l * D, xf, none, nullptr, false);
-        // h13 = x . W13^T (rows interleaved w1/w3), sh = silu(h1)*h3 in the GEMM's epilogue
+        // h13 = rmsnorm(x) . W13^T (rows interleaved w1/w3), sh = silu(h1)*h3 in the GEMM's epilogue
         const GemmEpi swiglu = {GEMM_EPI_SWIGLU, ts->sh, H, 0, 0};
-        if ((st = gemm(s, ts, 2, xf, D, r->w13 + (long)l * 2 * H * D, D, h13, 2 * H, T, 2 * H, D, 0, nullptr, nullptr,
-                       &swiglu)))
+        if ((st = norm_gemm(rmid, r->rms_ffn + (long)l * D, xf, none, nullptr, false, r->w13 + (long)l * 2 * H * D,
+                            2 * H, h13, &swiglu)))
             return st;
         if ((st = gemm(s, ts, 2, ts->sh, H, r->w2 + (long)l * D * H, H, rout, D, T, D, H, 1, rmid, &pend))) return st;
         pend_cin = rmid;

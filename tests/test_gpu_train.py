@@ -46,6 +46,24 @@ def tensor_slices(cfg):
                                    ((128, 256, 1, 1, 1, 1300, 160), 144), ((48, 128, 1, 2, 2, 400, 40), 40),
                                    ((72, 128, 1, 2, 2, 301, 20), 19), ((2304, 64, 1, 36, 36, 64, 8), 4)])
 def test_one_step_matches_oracle(cfg, T):
+    check_one_step(cfg, T)
+
+
+# The forward RMSNorms run inside the next GEMM's A loads when it can take
+# them (GemmNorm kinds: 1 the row itself, 2 the pending split-K partials
+# plus the residual, 4 the embedding gather; default 1|4).  Every choice is
+# held to the oracle, on shapes whose w2 GEMM splits K (hidden 384: two
+# partials pending before the next layer's QKV GEMM), with a ragged T.
+@pytest.mark.parametrize("fuse", ["0", "5", "7"])
+@pytest.mark.parametrize("cfg,T", [((64, 384, 2, 4, 4, 512, 32), 32), ((72, 384, 2, 2, 2, 301, 20), 19)])
+def test_fused_norm_kinds_match_oracle(cfg, T, fuse, monkeypatch):
+    monkeypatch.setenv("PTMI_TRAIN_FUSE_NORM", fuse)
+    check_one_step(cfg, T)
+
+
+def check_one_step(cfg, T):
+    """One training step on the GPU against the oracle: loss, every gradient
+    tensor, and the SGD update."""
     blob = pa.synth_model(cfg, 11, 0.05)
     tokens = pa.seed_tokens(5, T, cfg[5])
     om = OracleModel(blob.copy(), max_T=T)
