@@ -85,7 +85,6 @@ struct StepArgs {
     uint64_t *stamps;                        // [nb][n_stamps]
     int n_stamps;                            // 1 + 10 L + 4
     uint64_t wait_ticks;                     // bound of every wait (100 MHz ticks)
-    int poll_sleep;                          // s_sleep(1) per unsuccessful poll round
     int l2pf;                                // L2 staging by idle workgroups: 1 w1|w3 + w2, 2 next QKV + Wo
 };
 
@@ -166,7 +165,6 @@ __device__ bool poll_words(const uint64_t *src, int n, uint32_t tag, float *dst,
     for (int k = 0; k < K; k++) ok[k] = t + k * kPollT >= n;
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     const uint64_t wait_ticks = a->wait_ticks;
-    const int sleep = a->poll_sleep;
     for (int round = 1;; round++) {
         uint64_t v[K];
 #pragma unroll
@@ -186,7 +184,7 @@ __device__ bool poll_words(const uint64_t *src, int n, uint32_t tag, float *dst,
         if (all) return true;
         if (__builtin_amdgcn_s_memrealtime() - t0 > wait_ticks) return false;
         if ((round & 31) == 0 && err_seen(a->ctl)) return false;
-        for (int i = 0; i < sleep; i++) __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_s_sleep(1);
     }
 }
 
@@ -619,11 +617,11 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     for (int w = 0; w < kW; w++) ls += sm.wred[w];
                     return ls;
                 };
-                const uint64_t *head_part = a->t_part + ((long)l * NH + h) * a->n_chunks * (hd + 2);
+                uint64_t *head_part = a->t_part + ((long)l * NH + h) * a->n_chunks * (hd + 2);
                 if (c > 0) {
                     // a later chunk: its record (o, max, sum) goes to the
                     // head's chunk-0 unit
-                    uint64_t *dst = const_cast<uint64_t *>(head_part) + (long)c * (hd + 2);
+                    uint64_t *dst = head_part + (long)c * (hd + 2);
                     if (wave == kWriter) {
                         if (lane < hd) tstore(dst + lane, rec_o(lane), tk.tag);
                         if (lane == 0) tstore(dst + hd, mx, tk.tag);
@@ -1013,8 +1011,6 @@ int decode_step_create(ptmi_model *m) {
     // timeout path: the step then fails and reports, and every wave exits)
     const char *wt = getenv("PTMI_STEP_WAIT_TICKS");
     a.wait_ticks = wt ? strtoull(wt, nullptr, 10) : kWaitTicks;
-    const char *ps = getenv("PTMI_STEP_POLL_SLEEP");
-    a.poll_sleep = ps ? std::max(0, std::min(64, atoi(ps))) : 1;
     const char *pf = getenv("PTMI_STEP_L2PF");
     a.l2pf = pf ? atoi(pf) & 3 : 2;
     hipError_t e = hipMemsetAsync(mem, 0, total, lib_stream());
