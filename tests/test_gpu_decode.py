@@ -199,7 +199,7 @@ def test_errors_are_reported():
 @pytest.mark.skipif(not ref_available(), reason="oracle/_ref not built")
 def test_reference_forward_with_ptmi_matvec_dropin():
     """The reference's own pt_forward_step (pitorch/pt.c:267-271) with
-    ctx->matvec = ptmi_matvec: the drop-in binding of INTEGRATION.md."""
+    ctx->matvec = ptmi_matvec, the drop-in binding a pitorch caller adds."""
     fx = fixture("stories15M")
     blob = model_for("stories15M")
     L = pa.load_ptmi()
