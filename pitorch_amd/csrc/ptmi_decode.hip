@@ -417,10 +417,12 @@ int enqueue_step(ptmi_model *m, hipStream_t s, StepTimer *tm = nullptr) {
 }
 #undef TIMED
 
-int build_graph(ptmi_model *m) {
+// Capture `steps` consecutive decode steps as one graph.
+int capture_steps(ptmi_model *m, int steps, hipGraph_t *graph_out, hipGraphExec_t *exec_out) {
     hipStream_t s = lib_stream();
     PTMI_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    int st = enqueue_step(m, s);
+    int st = PTMI_OK;
+    for (int i = 0; i < steps && st == PTMI_OK; i++) st = enqueue_step(m, s);
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(s, &graph);
     if (st) { if (graph) (void)hipGraphDestroy(graph); return st; }
@@ -428,9 +430,15 @@ int build_graph(ptmi_model *m) {
     hipGraphExec_t exec = nullptr;
     e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     if (e != hipSuccess) { (void)hipGraphDestroy(graph); return hip_check(e, "hipGraphInstantiate"); }
-    m->graph = graph;
-    m->exec = exec;
+    *graph_out = graph;
+    *exec_out = exec;
     return PTMI_OK;
+}
+
+int build_graph(ptmi_model *m) {
+    int st = capture_steps(m, 1, &m->graph, &m->exec);
+    if (st == PTMI_OK && m->graph_steps > 1) st = capture_steps(m, m->graph_steps, &m->graph_k, &m->exec_k);
+    return st;
 }
 
 // One decode step: the captured graph, or the same launches enqueued
@@ -439,6 +447,17 @@ int build_graph(ptmi_model *m) {
 int launch_step(ptmi_model *m, hipStream_t s) {
     if (m->eager) return enqueue_step(m, s);
     PTMI_HIP(hipGraphLaunch(m->exec, s));
+    return PTMI_OK;
+}
+
+// n consecutive decode steps: graphs of graph_steps steps while enough
+// remain, then single steps.
+int launch_steps(ptmi_model *m, hipStream_t s, int n) {
+    int st;
+    if (!m->eager && m->exec_k)
+        for (; n >= m->graph_steps; n -= m->graph_steps) PTMI_HIP(hipGraphLaunch(m->exec_k, s));
+    for (; n > 0; n--)
+        if ((st = launch_step(m, s))) return st;
     return PTMI_OK;
 }
 
@@ -540,6 +559,7 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
     }
     const char *eager = getenv("PTMI_DECODE_EAGER");
     m->eager = eager && eager[0] == '1';
+    if (const char *gs = getenv("PTMI_DECODE_GRAPH_STEPS")) m->graph_steps = std::max(1, std::min(64, atoi(gs)));
     const char *nopf = getenv("PTMI_NO_PREFETCH");
     m->prefetch = !(nopf && nopf[0] == '1');
     if (const char *pp = getenv("PTMI_PREFETCH_PLAN")) {
@@ -558,6 +578,8 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
         decode_step_destroy(m);
         if (m->exec) (void)hipGraphExecDestroy(m->exec);
         if (m->graph) (void)hipGraphDestroy(m->graph);
+        if (m->exec_k) (void)hipGraphExecDestroy(m->exec_k);
+        if (m->graph_k) (void)hipGraphDestroy(m->graph_k);
         (void)hipFree(m->mem);
         delete m;
         release_blob(r);
@@ -573,6 +595,8 @@ void ptmi_model_destroy(ptmi_model_t *m) {
     train_destroy(m);
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
     if (m->graph) (void)hipGraphDestroy(m->graph);
+    if (m->exec_k) (void)hipGraphExecDestroy(m->exec_k);
+    if (m->graph_k) (void)hipGraphDestroy(m->graph_k);
     decode_step_destroy(m);
     (void)hipFree(m->mem);
     release_blob(m->res);
@@ -639,8 +663,7 @@ int ptmi_model_generate(ptmi_model_t *m, const int *prompt, int n_prompt, int ma
     if ((st = zero_kv(m))) return st;
     PTMI_HIP(hipMemcpyAsync(m->prompt, prompt, (size_t)n_prompt * sizeof(int), hipMemcpyHostToDevice, s));
     if ((st = set_ctl(m, prompt[0], 0, n_prompt))) return st;
-    for (int i = 0; i < max_tokens; i++)
-        if ((st = launch_step(m, s))) return st;
+    if ((st = launch_steps(m, s, max_tokens))) return st;
     PTMI_HIP(hipMemcpyAsync(out, m->out_tokens, (size_t)max_tokens * sizeof(int), hipMemcpyDeviceToHost, s));
     DecodeCtl h;
     PTMI_HIP(hipMemcpyAsync(&h, m->ctl, sizeof(h), hipMemcpyDeviceToHost, s));
@@ -663,8 +686,7 @@ int ptmi_model_decode_async(ptmi_model_t *m, int first_token, int n_steps) {
     hipStream_t s = lib_stream();
     int st;
     if ((st = set_ctl(m, first_token, m->host_pos, 0))) return st;
-    for (int i = 0; i < n_steps; i++)
-        if ((st = launch_step(m, s))) return st;
+    if ((st = launch_steps(m, s, n_steps))) return st;
     m->host_pos += n_steps;
     return PTMI_OK;
 }

@@ -42,6 +42,11 @@ struct ptmi_model {
     int *prompt = nullptr, *out_tokens = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    // A second graph of graph_steps consecutive steps (PTMI_DECODE_GRAPH_STEPS,
+    // 1 = none), launched while at least that many steps remain
+    int graph_steps = 8;
+    hipGraph_t graph_k = nullptr;
+    hipGraphExec_t exec_k = nullptr;
     bool eager = false;                  // PTMI_DECODE_EAGER=1: no graph
     bool prefetch = true;                // PTMI_NO_PREFETCH=1: no L2 prefetch blocks
     // Which weights each launch of the step prefetches (into the MALL,
