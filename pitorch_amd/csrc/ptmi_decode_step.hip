@@ -395,9 +395,15 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
     int L;
     {
         const PTMI_CONST StepArgs *a = fresh(ap);
-        tk.pos = gl(a->ctl)->pos;
-        tk.tag = (uint32_t)gl(a->ctl)->seq + 1u;
-        tk.token = gl(a->ctl)->tok_in;
+        // a step or launch window before this one in the same submission
+        // failed: its words carry the tag this step would use, so do nothing
+        // (the host reports the failure and moves the sequence number on)
+        const PTMI_GLOBAL DecodeCtl *ctl = gl(a->ctl);
+        const int err = ctl->err;
+        tk.pos = ctl->pos;
+        tk.tag = (uint32_t)ctl->seq + 1u;
+        tk.token = ctl->tok_in;
+        if (err) return;
         tk.nact = tk.pos / a->chunk + 1;
         L = a->L;
         if (tid == 0) sm.fail = 0;

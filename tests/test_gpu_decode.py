@@ -281,8 +281,9 @@ def test_one_kernel_step_stage_stamps(monkeypatch):
 def test_one_kernel_step_timeout_is_reported(monkeypatch):
     """A wait of the one-kernel step that runs out is an error of the call,
     forced here from the host with a one-tick wait bound: the kernel still
-    exits normally (every wait is bounded and checks the shared error word),
-    the call raises, and the model stays usable for the next call."""
+    exits normally (every wait is bounded and checks the shared error word;
+    later steps of the same graph see the word and do nothing), the call
+    raises, and the model stays usable for the next call."""
     monkeypatch.setenv("PTMI_DECODE_STEP", "1")
     monkeypatch.setenv("PTMI_STEP_WAIT_TICKS", "1")
     m = pa.Model(model_for("stories15M"))
