@@ -176,8 +176,9 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
     // plain y = Wx has no prologue arithmetic; there the weights go first
     // (measured faster on the large classifier-shaped matrices).
     constexpr bool kXFirst = !(PRO == PRO_NONE && EPI == EPI_STORE);
-    // PRO_ATTN_COMBINE inputs: every allocated chunk's partial sums and
-    // statistics; chunks past the active ones are dropped later by selects.
+    // PRO_ATTN_COMBINE inputs: the active chunks' partial sums and
+    // statistics (the slots past them re-read the last active chunk, the same
+    // cache lines, and are dropped later by selects; att_chunk >= 1).
     constexpr int kFastI = 6;                            // n <= 6 * threads in one round trip
     float ov[kFastI][kMaxAttnChunks], mv[kMaxAttnChunks], lv[kMaxAttnChunks];
     const int nthr = blockDim.x;
@@ -193,14 +194,14 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
                 const int h = i / hd, d = i - h * hd;
                 const float *o = p.att_o + (long)h * nch * hd + d;
 #pragma unroll
-                for (int c = 0; c < kMaxAttnChunks; c++) ov[k][c] = o[(long)min(c, nch - 1) * hd];
+                for (int c = 0; c < kMaxAttnChunks; c++) ov[k][c] = o[(long)min(c, min(nch, pos / p.att_chunk + 1) - 1) * hd];
             }
         }
         const int h_ml = min((int)threadIdx.x, p.att_heads - 1);
         const float *ml = p.att_ml + 2L * h_ml * nch;
 #pragma unroll
         for (int c = 0; c < kMaxAttnChunks; c++) {
-            const int cc = min(c, nch - 1);
+            const int cc = min(c, min(nch, pos / p.att_chunk + 1) - 1);
             mv[c] = ml[2 * cc];
             lv[c] = ml[2 * cc + 1];
         }
