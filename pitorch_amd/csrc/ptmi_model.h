@@ -55,7 +55,7 @@ struct ptmi_model {
     // to the producer's layer l: o = Wo_l, f = w1|w3_l, d = w2_l,
     // q = QKV_{l+1} (the next token's layer 0 after the last layer), O = Wo_{l+1},
     // F = w1|w3_{l+1}, '-' = none.  PTMI_PREFETCH_PLAN overrides it.
-    char prefetch_plan[8] = "ofd----";
+    char prefetch_plan[8] = "ofd---q";
     float *sink = nullptr;               // prefetch load sink
     // one-kernel decode step (null step_mem: the multi-kernel step)
     uint64_t *step_mem = nullptr;        // its tagged exchange buffers
