@@ -963,10 +963,13 @@ static const StepKernel *pick_step(const Config &c, int *chunk, int *n_chunks) {
 }
 
 int decode_step_create(ptmi_model *m) {
-    // Opt-in (PTMI_DECODE_STEP=1): measured slower than the captured
-    // multi-kernel step on stories110M (3145 vs 3640 tok/s).
+    // PTMI_DECODE_STEP=1 / 0 forces this step / the captured multi-kernel
+    // step.  Unset: this step for dim <= 512, where it was measured faster
+    // (stories15M 9190 vs 8063 tok/s, stories42M 6463 vs 5799), the graph
+    // above (stories110M: 3834 vs 3843-3852, level).
     const char *env = getenv("PTMI_DECODE_STEP");
-    if (!env || env[0] != '1') return PTMI_OK;
+    const bool on = env && env[0] ? env[0] == '1' : m->c.dim <= 512;
+    if (!on) return PTMI_OK;
     int chunk = 0, nc = 0;
     if (!pick_step(m->c, &chunk, &nc)) return PTMI_OK;       // multi-kernel step
     int dev = 0, cus = 0;

@@ -6,8 +6,9 @@ make_golden.py).  Greedy tokens must be IDENTICAL over the full runs
 oracle at a relative tolerance (matvec reduction order differs).
 
 Every decode path is held to this: the captured multi-kernel step (the
-default), the one-kernel step (PTMI_DECODE_STEP=1, read when a model is
-created) and that step cut into launch windows (PTMI_STEP_SPLIT).
+default for dim > 512), the one-kernel step (the default for dim <= 512;
+PTMI_DECODE_STEP=1 / 0 forces either, read when a model is created) and
+that step cut into launch windows (PTMI_STEP_SPLIT).
 """
 import ctypes
 import hashlib
@@ -240,6 +241,19 @@ def test_profile_roles_cover_every_launch(mode, monkeypatch):
         assert prof["classifier"][1] == prof["argmax"][1] == 4 and prof["step"][1] == 0
         assert all(ms > 0 for r, (ms, _) in prof.items() if r != "step")
     m.close()
+
+
+def test_default_path_by_model_size(monkeypatch):
+    """Without PTMI_DECODE_STEP the one-kernel step serves models with
+    dim <= 512 (measured faster there) and the captured multi-kernel step
+    larger ones."""
+    monkeypatch.delenv("PTMI_DECODE_STEP", raising=False)
+    monkeypatch.delenv("PTMI_STEP_SPLIT", raising=False)
+    for cfg, one_kernel in [(pa.STORIES["stories15M"], True), ((768, 512, 1, 12, 12, 512, 64), False)]:
+        m = pa.Model(pa.synth_model(cfg, 3))
+        prof = m.profile(1, 1)
+        assert (prof["step"][1] > 0) == one_kernel, (cfg, prof["step"])
+        m.close()
 
 
 def test_step_split_rejects_unknown_stage(monkeypatch):
