@@ -1020,8 +1020,17 @@ int decode_step_create(ptmi_model *m) {
     // timeout path: the step then fails and reports, and every wave exits)
     const char *wt = getenv("PTMI_STEP_WAIT_TICKS");
     a.wait_ticks = wt ? strtoull(wt, nullptr, 10) : kWaitTicks;
-    const char *pf = getenv("PTMI_STEP_L2PF");
-    a.l2pf = pf ? atoi(pf) & 3 : 2;
+    // Idle workgroups stage the next stages' weights in L2: this layer's
+    // w1|w3 and w2 during QKV (1) only when enough of them are idle (64+:
+    // stories15M/42M, +0.2% / +1.7%; with 16 idle on stories110M the staging
+    // delays their own w1|w3 rows), the next layer's QKV and Wo during w2 (2)
+    // always.  PTMI_STEP_L2PF overrides.
+    {
+        const int blocks_qkv = (int)((D + 2 * KV + kRowsD - 1) / kRowsD), blocks_wo = (int)((D + kRowsD - 1) / kRowsD);
+        const int first_idle = std::max(std::max(blocks_qkv, blocks_wo), a.ubase + (int)(NH * nc));
+        const char *pf = getenv("PTMI_STEP_L2PF");
+        a.l2pf = pf ? atoi(pf) & 3 : (nb - first_idle >= 64 ? 3 : 2);
+    }
     hipError_t e = hipMemsetAsync(mem, 0, total, lib_stream());
     if (e == hipSuccess) e = hipMemcpyAsync(mem + args_off, &a, sizeof(a), hipMemcpyHostToDevice, lib_stream());
     if (e == hipSuccess) e = hipStreamSynchronize(lib_stream());
