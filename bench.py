@@ -2,16 +2,17 @@
 
 One step = one full greedy decode of the 1024-position context (BASELINE
 config 4): pt_generate over token ids (prompt forcing, then argmax), each
-position one hipGraph launch of the device-resident pt_forward_step (85
-projections + attention + argmax), positions 0..1023 of the KV cache,
-synthetic random-init weights ~N(0, 0.02).  `value` = decoded tokens per
-second over the K timed decodes.
+position one launch of the device-resident pt_forward_step (85 projections +
+attention + argmax as one kernel, the library's default decode path; graphs
+of 8 positions), positions 0..1023 of the KV cache, synthetic random-init
+weights ~N(0, 0.02).  `value` = decoded tokens per second over the K timed
+decodes.
 
 Prints ONE JSON line: decode tok/s as `value`, the dominant kernel's HBM
 roofline (per-launch HIP-event timing of eager steps over all 1024
-positions, algorithmic bytes per launch, counter-measured HBM traffic) and
-the reference's own CPU decode timed on a bounded sample, pinned to one
-core.
+positions, algorithmic bytes per launch, counter-measured HBM traffic), the
+same decode on the captured multi-kernel path for comparison, and the
+reference's own CPU decode timed on a bounded sample, pinned to one core.
 """
 import argparse
 import json
@@ -321,15 +322,19 @@ def pmc_workload(pa, name, positions):
     cfg = pa.STORIES[name]
     blob = pa.synth_model(cfg, pa.SEED_MODEL[name])
     prompt = pa.seed_tokens(pa.SEED_PROMPT, pa.N_PROMPT, cfg[5])
-    m = pa.Model(blob)
     L = pa.load_ptmi()
-    m.reset_kv()
-    for k in range(0, positions, 8):
-        m.decode_async(int(prompt[0]), min(8, positions - k))
-        pa._ffi.check(L.ptmi_sync())
-    m.close()
+    for path in ("1", "0"):                      # the one-kernel step, then the multi-kernel step
+        os.environ["PTMI_DECODE_STEP"] = path
+        m = pa.Model(blob)
+        m.reset_kv()
+        for k in range(0, positions, 8):
+            m.decode_async(int(prompt[0]), min(8, positions - k))
+            pa._ffi.check(L.ptmi_sync())
+        m.close()
+    os.environ.pop("PTMI_DECODE_STEP")
     calib_copy(pa)
-    print(f"[bench] pmc workload: {positions} positions of {name}, then the calibration copy", file=sys.stderr)
+    print(f"[bench] pmc workload: {positions} positions of {name} on both decode paths, then the calibration copy",
+          file=sys.stderr)
 
 
 def step_stamps(pa, name, at):
@@ -504,16 +509,21 @@ def main():
     # kernel's own start and end (hipExtLaunchKernelGGL), library stream
     m.reset_kv()
     n_prof = min(args.profile_steps, S)
-    prof = m.profile(int(prompt[0]), n_prof)
     rb = role_bytes(cfg, range(n_prof))
-    breakdown = {}
-    for role, (ms, cnt) in prof.items():
-        if cnt == 0:
-            continue
-        avg_us = ms * 1e3 / cnt
-        e = {"avg_us": round(avg_us, 3), "launches": cnt, "total_ms": round(ms, 4),
-             "bytes_per_launch": rb[role], "GBps": round(rb[role] / (avg_us * 1e-6) / 1e9, 1)}
-        breakdown[role] = e
+
+    def per_role(model):
+        prof = model.profile(int(prompt[0]), n_prof)
+        out = {}
+        for role, (ms, cnt) in prof.items():
+            if cnt == 0:
+                continue
+            avg_us = ms * 1e3 / cnt
+            out[role] = {"avg_us": round(avg_us, 3), "launches": cnt, "total_ms": round(ms, 4),
+                         "bytes_per_launch": rb[role], "GBps": round(rb[role] / (avg_us * 1e-6) / 1e9, 1)}
+        return out
+
+    breakdown = per_role(m)
+    one_kernel = "step" in breakdown
     dominant = max(breakdown, key=lambda r: breakdown[r]["total_ms"])
     dom = breakdown[dominant]
     achieved = dom["GBps"]
@@ -522,8 +532,29 @@ def main():
         print(f"[bench] {r:12s} {json.dumps(e)}", file=sys.stderr, flush=True)
     step_bytes = decode_bytes_per_token(cfg, range(S))
     step_gbs = step_bytes / (dt / n_tok) / 1e9
-
     m.close()
+
+    # the same decode on the other path (the captured multi-kernel step when
+    # the default is the one-kernel step), timed the same way, with its
+    # per-kernel breakdown
+    os.environ["PTMI_DECODE_STEP"] = "0" if one_kernel else "1"
+    m2 = pa.Model(blob)
+    os.environ.pop("PTMI_DECODE_STEP")
+    gen2 = lambda: m2.generate(prompt, S, stop_on_eos=False)
+    for _ in range(args.warmup):
+        gen2()
+    pa._ffi.check(L.ptmi_sync())
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        gen2()
+    pa._ffi.check(L.ptmi_sync())
+    other = {"path": "multi_kernel" if one_kernel else "one_kernel",
+             "tok_s": round(n_tok / (time.perf_counter() - t0), 2)}
+    m2.reset_kv()
+    other["breakdown"] = per_role(m2)
+    m2.close()
+    print(f"[bench] other path {json.dumps({k: v for k, v in other.items() if k != 'breakdown'})}",
+          file=sys.stderr, flush=True)
     del blob
     sweep = None if args.no_sweep else matvec_sweep(pa)
     for e in sweep or []:
@@ -554,7 +585,9 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (random-init N(0,0.02) weights, seeded prompt ids)",
-        "config": {"workload": f"{name}-shaped greedy decode, hipGraph per token", "model_shape": list(cfg),
+        "config": {"workload": f"{name}-shaped greedy decode, "
+                               + ("one kernel per token" if one_kernel else "62 kernels per token")
+                               + ", hipGraphs of 8 tokens", "model_shape": list(cfg),
                    "step": f"one full greedy decode of positions 0..{S - 1} (pt_generate over ids)",
                    "positions": f"0..{S - 1}", "tokens_timed": n_tok, "batch": 1},
         "roofline": {"bound": "hbm", "kernel": f"decode[{dominant}]", "achieved": achieved,
@@ -566,6 +599,7 @@ def main():
         "cpu_baseline": cpu,
         "cpu_extra": cpu_more,
         "breakdown": breakdown,
+        "other_path": other,
         "train": train,
     }
     print(json.dumps(line), flush=True)

@@ -66,6 +66,7 @@ struct StepArgs {
     int D, H, L, NH, KV, hd, kv_mul, V, S;
     int chunk, n_chunks;                     // attention unit = chunk positions of one head
     int ubase;                               // workgroup of attention unit 0
+    int qbase;                               // workgroup of QKV row block 0
     float att_scale;
     float *kc, *vc;                          // [L][S][KV]
     float *logits;                           // [V]
@@ -418,9 +419,12 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
         // the first stage's weights (later stages' come during the stage before)
         const int D = a->D, H = a->H, QR = D + 2 * a->KV, l = g0 / kStages;
         switch (l < L ? g0 % kStages : kStages) {
-        case 0:
-            if (b < (QR + kRowsD - 1) / kRowsD) load_wD(a, R, a->wqkv + (long)l * QR * D, QR, b, a->rms_att + (long)l * D);
+        case 0: {
+            const int qb = b - a->qbase;
+            if (qb >= 0 && qb < (QR + kRowsD - 1) / kRowsD)
+                load_wD(a, R, a->wqkv + (long)l * QR * D, QR, qb, a->rms_att + (long)l * D);
             break;
+        }
         case 1: {
             const int u = b - a->ubase;
             if (u >= 0 && u < a->NH * a->n_chunks && u / a->NH < tk.nact) load_kv(a, R, tk, l, u);
@@ -454,7 +458,8 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             const int n_units = a->NH * a->n_chunks, u = b - a->ubase;
             const bool unit = in(kStages * l + 1) && u >= 0 && u < n_units && u / a->NH < tk.nact;
             const bool pre_wo = in(kStages * l + 2) && b < blocks_wo;
-            if (b < blocks_qkv) {
+            const int qb = b - a->qbase;
+            if (qb >= 0 && qb < blocks_qkv) {
                 __syncthreads();                              // xs is free again
                 bool ok = true;
                 if (l == 0) {
@@ -468,8 +473,8 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 // the WO residual rows are rows of this same input
                 if (b < blocks_wo && tid < kRowsD) sm.xres[tid] = sm.xs[min(b * kRowsD + tid, D - 1)];
                 uint64_t *t_qkv = a->t_qkv + (long)l * QR;
-                for (int rb = b; rb < blocks_qkv; rb += nb) {
-                    if (rb != b) {
+                for (int rb = qb; rb < blocks_qkv; rb += nb) {
+                    if (rb != qb) {
                         __syncthreads();                      // the writer wave is done with yout
                         load_wD(a, R, a->wqkv + (long)l * QR * D, QR, rb, a->rms_att + (long)l * D);
                     }
@@ -508,13 +513,24 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 stamp(a, 2 + 10 * l);
             } else {
                 if (unit) load_kv(a, R, tk, l, u);
-                if (pre_wo) load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
+                if (pre_wo) {
+                    load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
+                    // a Wo block without QKV rows takes its residual rows here
+                    __syncthreads();
+                    bool ok = true;
+                    if (tid < kRowsD) {
+                        if (l == 0) sm.xres[tid] = gl(a->emb + (long)tk.token * D)[min(b * kRowsD + tid, D - 1)];
+                        else ok = poll_words<1>(a->t_xb + (long)(l - 1) * D + b * kRowsD, min(kRowsD, D - b * kRowsD),
+                                                tk.tag, sm.xres, a, tid);
+                    }
+                    if (!block_ok(ok, &sm.fail, a->ctl)) return;
+                }
             }
             // Workgroups with no QKV, attention or Wo work wait until the
             // w1|w3 stage: meanwhile they stage this layer's w1|w3 and w2
             // rows in their XCD's L2 (and through it the MALL).
             const int H = a->H;
-            const int first_idle = max(max(blocks_qkv, blocks_wo), a->ubase + n_units);
+            const int first_idle = max(max(a->qbase + blocks_qkv, blocks_wo), a->ubase + n_units);
             if (b >= first_idle && (a->l2pf & 1)) {
                 pf_acc = prefetch_rows(a->w13 + (long)l * 2 * H * D, 2 * H, D, kRowsD, (2 * H + kRowsD - 1) / kRowsD,
                                        first_idle, nb, pf_acc);
@@ -761,9 +777,10 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             const bool last_layer = l + 1 == a->L;
             const int next_blocks = last_layer ? (a->V + kRowsD - 1) / kRowsD : (QR + kRowsD - 1) / kRowsD;
             auto preload_next = [&]() {
-                if (b >= next_blocks || !in(kStages * (l + 1))) return;
+                const int nb_idx = last_layer ? b : b - a->qbase;   // the next stage's row block
+                if (nb_idx < 0 || nb_idx >= next_blocks || !in(kStages * (l + 1))) return;
                 if (last_layer) load_wD(a, R, a->wcls, a->V, b, a->rms_final);
-                else load_wD(a, R, a->wqkv + (long)(l + 1) * QR * D, QR, b, a->rms_att + (long)(l + 1) * D);
+                else load_wD(a, R, a->wqkv + (long)(l + 1) * QR * D, QR, nb_idx, a->rms_att + (long)(l + 1) * D);
             };
             if (b < blocks_w2) {
                 const uint64_t *t_xa = a->t_xa + (long)l * D;
@@ -796,8 +813,11 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 // idle until the next layer's QKV input: stage its QKV and Wo
                 // rows in this XCD's L2
                 if (!last_layer && (a->l2pf & 2)) {
-                    pf_acc = prefetch_rows(a->wqkv + (long)(l + 1) * QR * D, QR, D, kRowsD, (QR + kRowsD - 1) / kRowsD,
-                                           blocks_w2, nb, pf_acc);
+                    // (with the QKV blocks past the w2 blocks, their rows are
+                    // already in registers)
+                    if (a->qbase == 0)
+                        pf_acc = prefetch_rows(a->wqkv + (long)(l + 1) * QR * D, QR, D, kRowsD, (QR + kRowsD - 1) / kRowsD,
+                                               blocks_w2, nb, pf_acc);
                     pf_acc = prefetch_rows(a->wo + (long)(l + 1) * D * D, D, D, kRowsD, (D + kRowsD - 1) / kRowsD,
                                            blocks_w2, nb, pf_acc);
                 }
@@ -964,11 +984,10 @@ static const StepKernel *pick_step(const Config &c, int *chunk, int *n_chunks) {
 
 int decode_step_create(ptmi_model *m) {
     // PTMI_DECODE_STEP=1 / 0 forces this step / the captured multi-kernel
-    // step.  Unset: this step for dim <= 512, where it was measured faster
-    // (stories15M 9190 vs 8063 tok/s, stories42M 6463 vs 5799), the graph
-    // above (stories110M: 3834 vs 3843-3852, level).
+    // step.  Unset: this step wherever its shape is supported (measured
+    // faster on stories15M, 42M and 110M).
     const char *env = getenv("PTMI_DECODE_STEP");
-    const bool on = env && env[0] ? env[0] == '1' : m->c.dim <= 512;
+    const bool on = env && env[0] ? env[0] == '1' : true;
     if (!on) return PTMI_OK;
     int chunk = 0, nc = 0;
     if (!pick_step(m->c, &chunk, &nc)) return PTMI_OK;       // multi-kernel step
@@ -998,10 +1017,20 @@ int decode_step_create(ptmi_model *m) {
     // The attention units sit on the workgroups after the QKV row blocks
     // when they fit (PTMI_STEP_UNIT_BASE=0: from workgroup 0), so their K/V
     // loads go out at the start of the QKV stage
+    // The QKV row blocks sit on the workgroups after the w2 row blocks (when
+    // they fit; PTMI_STEP_QBASE=0: from workgroup 0), which then preload
+    // their next-layer QKV rows during w2 (stories15M/42M/110M +2.7/+2.4/
+    // +3.4%)
     {
         const char *ub = getenv("PTMI_STEP_UNIT_BASE");
-        const int blocks_qkv = (int)((D + 2 * KV + kRowsD - 1) / kRowsD);
-        a.ubase = (!(ub && ub[0] == '0') && blocks_qkv + NH * nc <= nb) ? blocks_qkv : 0;
+        const char *qs = getenv("PTMI_STEP_QBASE");
+        const int blocks_qkv = (int)((D + 2 * KV + kRowsD - 1) / kRowsD), blocks_w2 = (int)((D + kRowsH - 1) / kRowsH);
+        a.qbase = (!(qs && qs[0] == '0') && blocks_w2 + blocks_qkv <= nb) ? blocks_w2 : 0;
+        const bool ub_on = !(ub && ub[0] == '0');
+        if (a.qbase > 0)
+            a.ubase = NH * nc <= a.qbase ? 0 : (ub_on && a.qbase + blocks_qkv + NH * nc <= nb ? a.qbase + blocks_qkv : 0);
+        else
+            a.ubase = (ub_on && blocks_qkv + NH * nc <= nb) ? blocks_qkv : 0;
     }
     a.att_scale = host_att_scale(c.head_dim);
     a.kc = m->kc; a.vc = m->vc; a.logits = m->logits; a.ctl = m->ctl;
@@ -1027,7 +1056,7 @@ int decode_step_create(ptmi_model *m) {
     // always.  PTMI_STEP_L2PF overrides.
     {
         const int blocks_qkv = (int)((D + 2 * KV + kRowsD - 1) / kRowsD), blocks_wo = (int)((D + kRowsD - 1) / kRowsD);
-        const int first_idle = std::max(std::max(blocks_qkv, blocks_wo), a.ubase + (int)(NH * nc));
+        const int first_idle = std::max(std::max(a.qbase + blocks_qkv, blocks_wo), a.ubase + (int)(NH * nc));
         const char *pf = getenv("PTMI_STEP_L2PF");
         a.l2pf = pf ? atoi(pf) & 3 : (nb - first_idle >= 64 ? 3 : 2);
     }
