@@ -5,10 +5,11 @@ make_golden.py).  Greedy tokens must be IDENTICAL over the full runs
 (256 positions for 15M, 1024 for 42M/110M); logits are compared with the
 oracle at a relative tolerance (matvec reduction order differs).
 
-Every decode path is held to this: the captured multi-kernel step (the
-default for dim > 512), the one-kernel step (the default for dim <= 512;
-PTMI_DECODE_STEP=1 / 0 forces either, read when a model is created) and
-that step cut into launch windows (PTMI_STEP_SPLIT).
+Every decode path is held to this: the one-kernel step (the default for
+every shape it supports), the captured multi-kernel step (PTMI_DECODE_STEP=0,
+and the shapes the one kernel does not take; PTMI_DECODE_STEP is read when
+a model is created) and the one kernel cut into launch windows
+(PTMI_STEP_SPLIT).
 """
 import ctypes
 import hashlib
@@ -244,12 +245,13 @@ def test_profile_roles_cover_every_launch(mode, monkeypatch):
 
 
 def test_default_path_by_model_size(monkeypatch):
-    """Without PTMI_DECODE_STEP the one-kernel step serves models with
-    dim <= 512 (measured faster there) and the captured multi-kernel step
-    larger ones."""
+    """Without PTMI_DECODE_STEP the one-kernel step serves every shape it
+    supports (stories15M, and a one-layer model of stories110M's widths);
+    a shape it does not take (head_dim 128) gets the multi-kernel step."""
     monkeypatch.delenv("PTMI_DECODE_STEP", raising=False)
     monkeypatch.delenv("PTMI_STEP_SPLIT", raising=False)
-    for cfg, one_kernel in [(pa.STORIES["stories15M"], True), ((768, 512, 1, 12, 12, 512, 64), False)]:
+    for cfg, one_kernel in [(pa.STORIES["stories15M"], True), ((768, 2048, 1, 12, 12, 512, 64), True),
+                            ((256, 512, 1, 2, 2, 512, 64), False)]:
         m = pa.Model(pa.synth_model(cfg, 3))
         prof = m.profile(1, 1)
         assert (prof["step"][1] > 0) == one_kernel, (cfg, prof["step"])
