@@ -236,6 +236,7 @@ struct Smem {
     float sc[kMaxChunk];               // ATT: scores -> weights
     float cand[1024];                  // final argmax: (value, index) per workgroup
     float yout[kRowsD];                // results the writer wave stores
+    float ycls[2][kRowsD];             // classifier logits, alternate row blocks
     int fail;
 };
 
@@ -308,6 +309,49 @@ __device__ __forceinline__ float dot_d(const PTMI_CONST StepArgs *a, const Regs<
     float acc = 0.0f;
 #pragma unroll
     for (int it = 0; it < ITD; it++) acc = dot4(sel4(sub + it * 32 < nD4, R.wD[it]), xr[it], acc);
+    return group_sum<32>(acc);
+}
+
+// The classifier's two halves of dot_d: its rows all take the same
+// RMSNorm'd input, so the lane's columns of it are computed once (the same
+// operations as dot_d's, so the sums are bit-identical), and each row block
+// is a dot of those against the block's weights.
+template <int ITD, int ITH, int GA>
+__device__ __forceinline__ void norm_x_d(const PTMI_CONST StepArgs *a, const Regs<ITD, ITH, GA> &R, const float *xs,
+                                         float4 (&xr)[ITD]) {
+    const int nD4 = a->D >> 2, sub = sub_d();
+#pragma unroll
+    for (int it = 0; it < ITD; it++) {
+        const int c = sub + it * 32;
+        xr[it] = sel4(c < nD4, reinterpret_cast<const float4 *>(xs)[min(c, nD4 - 1)]);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int it = 0; it < ITD; it++)
+        ss += xr[it].x * xr[it].x + xr[it].y * xr[it].y + xr[it].z * xr[it].z + xr[it].w * xr[it].w;
+    ss = group_sum<32>(ss);
+    const float inv = 1.0f / d_sqrtf(ss / (float)a->D + 1e-5f);
+#pragma unroll
+    for (int it = 0; it < ITD; it++) {
+        xr[it].x = xr[it].x * inv * R.nw[it].x;
+        xr[it].y = xr[it].y * inv * R.nw[it].y;
+        xr[it].z = xr[it].z * inv * R.nw[it].z;
+        xr[it].w = xr[it].w * inv * R.nw[it].w;
+    }
+}
+template <int ITD>
+__device__ __forceinline__ void load_rows_d(const PTMI_CONST StepArgs *a, float4 (&w)[ITD], const float *W, int rows, int rb) {
+    const int nD4 = a->D >> 2, sub = sub_d();
+    const float *row = W + (long)min(rb * kRowsD + slot_d(), rows - 1) * a->D;
+#pragma unroll
+    for (int it = 0; it < ITD; it++) w[it] = ntload4(row + 4 * min(sub + it * 32, nD4 - 1));
+}
+template <int ITD>
+__device__ __forceinline__ float dot_rows_d(const PTMI_CONST StepArgs *a, const float4 (&w)[ITD], const float4 (&xr)[ITD]) {
+    const int nD4 = a->D >> 2, sub = sub_d();
+    float acc = 0.0f;
+#pragma unroll
+    for (int it = 0; it < ITD; it++) acc = dot4(sel4(sub + it * 32 < nD4, w[it]), xr[it], acc);
     return group_sum<32>(acc);
 }
 
@@ -835,24 +879,42 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
         const PTMI_CONST StepArgs *a = fresh(ap);
         const int blocks_cls = (a->V + kRowsD - 1) / kRowsD;
         if (b < blocks_cls) {
+            // Two row blocks in flight: R.wD holds block b (loaded during the
+            // last layer), wB the next one, issued before the wait for x.
+            // Each block's loads go out as soon as the block two before it
+            // is consumed.
+            float4 wB[ITD], xr[ITD];
+            if (b + nb < blocks_cls) load_rows_d(a, wB, a->wcls, a->V, b + nb);
             __syncthreads();
             bool ok = tid >= kPollT || poll_words<5>(a->t_xb + (long)(a->L - 1) * a->D, a->D, tk.tag, sm.xs, a, tid);
             if (!block_ok(ok, &sm.fail, a->ctl)) return;
             stamp(a, 1 + 10 * a->L);
-            for (int rb = b; rb < blocks_cls; rb += nb) {
-                if (rb != b) {
-                    __syncthreads();                          // the writer wave is done with yout
-                    load_wD(a, R, a->wcls, a->V, rb, a->rms_final);
-                }
-                const float acc = dot_d(a, R, sm.xs, true);
+            norm_x_d(a, R, sm.xs, xr);
+            // one row block: its logits (ycls[p], stored by the writer wave)
+            // and this lane's argmax candidate.  ycls alternates, so the
+            // barrier of the next block also orders the writer's reads of
+            // this one before the block after overwrites it.
+            auto block = [&](const float4 (&w)[ITD], int rb, int p) {
+                const float acc = dot_rows_d(a, w, xr);
                 const int r = rb * kRowsD + slot_d();
                 if (r < a->V) {
-                    if ((lane & 31) == 0) sm.yout[slot_d()] = acc;
+                    if ((lane & 31) == 0) sm.ycls[p][slot_d()] = acc;
                     take_best(bv, bi, acc, r);
                 }
+            };
+            auto store = [&](int rb, int p) {
                 __syncthreads();
                 if (wave == kWriter && lane < kRowsD && rb * kRowsD + lane < a->V)
-                    gl(a->logits)[rb * kRowsD + lane] = sm.yout[lane];
+                    gl(a->logits)[rb * kRowsD + lane] = sm.ycls[p][lane];
+            };
+            for (int rb = b; rb < blocks_cls; rb += 2 * nb) {
+                block(R.wD, rb, 0);
+                if (rb + 2 * nb < blocks_cls) load_rows_d(a, R.wD, a->wcls, a->V, rb + 2 * nb);
+                store(rb, 0);
+                if (rb + nb >= blocks_cls) break;
+                block(wB, rb + nb, 1);
+                if (rb + 3 * nb < blocks_cls) load_rows_d(a, wB, a->wcls, a->V, rb + 3 * nb);
+                store(rb + nb, 1);
             }
             stamp(a, 2 + 10 * a->L);
         }
