@@ -225,7 +225,6 @@ struct Tok {
 struct Smem {
     float xs[2048];                    // the stage's input vector (<= max(D, H))
     float part[kPartLds];              // ATT, chunk 0: the head's chunk records
-    float wts[1][kMaxChunks];          // ATT, chunk 0: the chunks' merge weights
     float xres[kRowsD];                // WO: residual rows of this block
     float xres2[kRowsH];               // W2: residual rows of this block
     float rope_c[64], rope_s[64];      // RoPE cos/sin of this position, pair i = 2*k (all layers)
@@ -695,39 +694,43 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     }
                 } else {
                     // chunk 0 merges the head's active chunks: its own
-                    // record from LDS, the others' records polled, then
-                    // w_c = e^(m_c - M) / sum_c' l_c' e^(m_c' - M) and
-                    // out = sum_c w_c o_c, published for the WO stage
-                    const int nother = tk.nact - 1;
+                    // record in the writer wave's registers, the others'
+                    // polled into LDS, then w_c = e^(m_c - M) / sum_c' l_c'
+                    // e^(m_c' - M) and out = sum_c w_c o_c, published for
+                    // the WO stage.  The writer wave does the merge alone,
+                    // lane c holding chunk c's statistics, so no thread
+                    // walks the records serially through LDS; the sums keep
+                    // the chunk order of one fmaf chain each.
+                    const int nact = tk.nact, nother = nact - 1;
+                    float o0 = 0.0f, m0 = 0.0f, l0 = 0.0f;
                     if (wave == kWriter) {
-                        if (lane < hd) sm.part[lane] = rec_o(lane);
-                        if (lane == 0) sm.part[hd] = mx;
-                        if (lane == 1) sm.part[hd + 1] = rec_l();
+                        o0 = rec_o(min(lane, hd - 1));
+                        m0 = mx;
+                        l0 = rec_l();
                     }
                     bool ok = true;
                     if (nother > 0 && tid < kPollT)
                         ok = poll_words<2>(head_part + (hd + 2), nother * (hd + 2), tk.tag, sm.part + (hd + 2), a, tid);
                     if (!block_ok(ok, &sm.fail, a->ctl)) return;
-                    if (tid == 0) {
-                        const int nact = tk.nact;
-                        float M = -INFINITY;
-                        for (int cc = 0; cc < nact; cc++) M = fmaxf(M, sm.part[cc * (hd + 2) + hd]);
-                        float f[kMaxChunks], Ls = 0.0f;
+                    if (wave == kWriter) {
+                        auto rl = [](float x, int k) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k)); };
+                        const float *pc = sm.part + min(lane, kMaxChunks - 1) * (hd + 2);
+                        const bool act = lane < nact;
+                        const float mc = lane == 0 ? m0 : pc[hd], lc = lane == 0 ? l0 : pc[hd + 1];
+                        const float M = group_max<64>(act ? mc : -INFINITY);
+                        const float f = act ? d_expf(mc - M) : 0.0f;
+                        float Ls = 0.0f;
 #pragma unroll
-                        for (int cc = 0; cc < kMaxChunks; cc++) {
-                            const float *pc = sm.part + min(cc, nact - 1) * (hd + 2);
-                            f[cc] = cc < nact ? d_expf(pc[hd] - M) : 0.0f;
-                            Ls = cc < nact ? fmaf(pc[hd + 1], f[cc], Ls) : Ls;
-                        }
+                        for (int k = 0; k < kMaxChunks; k++) Ls = k < nact ? fmaf(rl(lc, k), rl(f, k), Ls) : Ls;
                         const float inv = 1.0f / Ls;
-#pragma unroll
-                        for (int cc = 0; cc < kMaxChunks; cc++) sm.wts[0][cc] = f[cc] * inv;
-                    }
-                    __syncthreads();
-                    if (wave == kWriter && lane < hd) {
+                        const int d = min(lane, hd - 1);
                         float v = 0.0f;
-                        for (int cc = 0; cc < tk.nact; cc++) v = fmaf(sm.part[cc * (hd + 2) + lane], sm.wts[0][cc], v);
-                        tstore(a->t_att + (long)l * D + h * hd + lane, v, tk.tag);
+#pragma unroll
+                        for (int k = 0; k < kMaxChunks; k++) {
+                            const float ok_ = k == 0 ? o0 : sm.part[k * (hd + 2) + d];
+                            v = k < nact ? fmaf(ok_, rl(f, k) * inv, v) : v;
+                        }
+                        if (lane < hd) tstore(a->t_att + (long)l * D + h * hd + lane, v, tk.tag);
                     }
                 }
                 stamp(a, 4 + 10 * l);
