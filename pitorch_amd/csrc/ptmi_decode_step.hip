@@ -67,6 +67,7 @@ struct StepArgs {
     int chunk, n_chunks;                     // attention unit = chunk positions of one head
     int ubase;                               // workgroup of attention unit 0
     int qbase;                               // workgroup of QKV row block 0
+    int wbase;                               // workgroup of Wo row block 0 (a QKV workgroup)
     float att_scale;
     float *kc, *vc;                          // [L][S][KV]
     float *logits;                           // [V]
@@ -104,10 +105,19 @@ __device__ __forceinline__ PTMI_GLOBAL T *gl(T *p) {
 // fields come in with scalar loads.
 #define PTMI_CONST __attribute__((address_space(4)))
 
-// Stamp slot `i` of this workgroup (thread 0 only; no-op without stamps).
-__device__ __forceinline__ void stamp(const PTMI_CONST StepArgs *a, int i) {
-    if (a->stamps && threadIdx.x == kPollT)
-        gl(a->stamps)[(long)blockIdx.x * a->n_stamps + i] = __builtin_amdgcn_s_memrealtime();
+// Stamp slot `i` of this workgroup (one thread of the writer wave; no-op
+// without stamps).  Stamps collect in LDS and reach global memory only as
+// the workgroup leaves (flush_stamps): a global store here would sit in the
+// wave's memory counter and delay its next wait.
+constexpr int kStampSlots = 1 + 10 * 32 + 4;       // up to 32 layers
+__device__ __forceinline__ void stamp(const PTMI_CONST StepArgs *a, uint64_t *st, int i) {
+    if (a->stamps && threadIdx.x == kPollT) st[i] = __builtin_amdgcn_s_memrealtime();
+}
+// The writer wave copies this launch's stamps (the non-zero slots) out.
+__device__ __forceinline__ void flush_stamps(const PTMI_CONST StepArgs *a, const uint64_t *st) {
+    if (!a->stamps || ((int)threadIdx.x >> 6) != kWriter) return;
+    for (int i = (int)threadIdx.x & 63; i < a->n_stamps; i += 64)
+        if (st[i]) gl(a->stamps)[(long)blockIdx.x * a->n_stamps + i] = st[i];
 }
 
 __device__ __forceinline__ uint64_t tload(const uint64_t *p) {
@@ -235,6 +245,7 @@ struct Smem {
     float sc[kMaxChunk];               // ATT: scores -> weights
     float cand[1024];                  // final argmax: (value, index) per workgroup
     float yout[kRowsD];                // results the writer wave stores
+    uint64_t st[kStampSlots];          // stage stamps until the workgroup leaves
     float ycls[2][kRowsD];             // classifier logits, alternate row blocks
     int fail;
 };
@@ -277,6 +288,31 @@ __device__ __forceinline__ void load_wH(const PTMI_CONST StepArgs *a, Regs<ITD, 
     const float *row = W + (long)r * a->H;
 #pragma unroll
     for (int it = 0; it < ITH; it++) R.wH[it] = ntload4(row + 4 * min(sub + it * 64, nH4 - 1));
+}
+
+// Wo rows are D-length rows like the QKV and w1|w3 rows (same lane layout),
+// held in the first ITD registers of the w2 set: it is free from the w2 dot
+// to the next layer's Wo dot, so a workgroup can hold the Wo rows and the
+// w1|w3 rows at once.
+template <int ITD, int ITH, int GA>
+__device__ __forceinline__ void load_wo(const PTMI_CONST StepArgs *a, Regs<ITD, ITH, GA> &R, int l, int rb) {
+    static_assert(ITH >= ITD, "the Wo rows live in the w2 registers");
+    const int D = a->D, nD4 = D >> 2, sub = sub_d();
+    const float *row = a->wo + (long)l * D * D + (long)min(rb * kRowsD + slot_d(), D - 1) * D;
+#pragma unroll
+    for (int it = 0; it < ITD; it++) R.wH[it] = ntload4(row + 4 * min(sub + it * 32, nD4 - 1));
+}
+template <int ITD, int ITH, int GA>
+__device__ __forceinline__ float dot_wo(const PTMI_CONST StepArgs *a, const Regs<ITD, ITH, GA> &R, const float *xs) {
+    const int nD4 = a->D >> 2, sub = sub_d();
+    float acc = 0.0f;
+#pragma unroll
+    for (int it = 0; it < ITD; it++) {
+        const int c = sub + it * 32;
+        const float4 x = sel4(c < nD4, reinterpret_cast<const float4 *>(xs)[min(c, nD4 - 1)]);
+        acc = dot4(sel4(c < nD4, R.wH[it]), x, acc);
+    }
+    return group_sum<32>(acc);
 }
 
 // The lane's D-row weights against xs (RMSNorm'd when norm): the row's sum
@@ -448,6 +484,8 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
         tk.tag = (uint32_t)ctl->seq + 1u;
         tk.token = ctl->tok_in;
         if (err) return;
+        if (a->stamps && wave == kWriter)
+            for (int i = lane; i < a->n_stamps; i += 64) sm.st[i] = 0;
         tk.nact = tk.pos / a->chunk + 1;
         L = a->L;
         if (tid == 0) sm.fail = 0;
@@ -459,35 +497,40 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             sm.rope_c[tid] = c;
             sm.rope_s[tid] = sn;
         }
-        // the first stage's weights (later stages' come during the stage before)
-        const int D = a->D, H = a->H, QR = D + 2 * a->KV, l = g0 / kStages;
-        switch (l < L ? g0 % kStages : kStages) {
-        case 0: {
-            const int qb = b - a->qbase;
-            if (qb >= 0 && qb < (QR + kRowsD - 1) / kRowsD)
-                load_wD(a, R, a->wqkv + (long)l * QR * D, QR, qb, a->rms_att + (long)l * D);
-            break;
-        }
-        case 1: {
-            const int u = b - a->ubase;
-            if (u >= 0 && u < a->NH * a->n_chunks && u / a->NH < tk.nact) load_kv(a, R, tk, l, u);
-            if (in(g0 + 1) && b < (D + kRowsD - 1) / kRowsD) load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
-            break;
-        }
-        case 2:
-            if (b < (D + kRowsD - 1) / kRowsD) load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
-            break;
-        case 3:
-            if (b < (2 * H + kRowsD - 1) / kRowsD) load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, b, a->rms_ffn + (long)l * D);
-            break;
-        case 4:
-            if (b < (D + kRowsH - 1) / kRowsH) load_wH(a, R, a->w2 + (long)l * D * H, D, b);
-            break;
-        default:
+        // Each register set is loaded at one point: after the stage that
+        // last read it, a stage or more ahead of its use (w1|w3 rows after
+        // QKV, w2 rows after Wo, the next QKV or classifier rows after
+        // w1|w3, the next K/V and Wo rows after w2).  A load issued from two
+        // places would leave the compiler copying registers where the paths
+        // join, which waits for the loads there.  A launch loads here what
+        // those points before its first stage would have loaded.
+        const int D = a->D, H = a->H, QR = D + 2 * a->KV, l = g0 / kStages, k0 = l < L ? g0 % kStages : kStages;
+        const int qb = b - a->qbase, wb = b - a->wbase, u = b - a->ubase;
+        if (k0 == kStages) {
             if (b < (a->V + kRowsD - 1) / kRowsD) load_wD(a, R, a->wcls, a->V, b, a->rms_final);
-            break;
+        } else {
+            if (k0 == 0) {
+                if (qb >= 0 && qb < (QR + kRowsD - 1) / kRowsD)
+                    load_wD(a, R, a->wqkv + (long)l * QR * D, QR, qb, a->rms_att + (long)l * D);
+            } else if (k0 <= 3) {
+                if (in(kStages * l + 3) && b < (2 * H + kRowsD - 1) / kRowsD)
+                    load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, b, a->rms_ffn + (long)l * D);
+            } else if (in(kStages * (l + 1))) {
+                if (l + 1 == L) {
+                    if (b < (a->V + kRowsD - 1) / kRowsD) load_wD(a, R, a->wcls, a->V, b, a->rms_final);
+                } else if (qb >= 0 && qb < (QR + kRowsD - 1) / kRowsD) {
+                    load_wD(a, R, a->wqkv + (long)(l + 1) * QR * D, QR, qb, a->rms_att + (long)(l + 1) * D);
+                }
+            }
+            if (k0 <= 2) {
+                if (in(kStages * l + 2) && wb >= 0 && wb < (D + kRowsD - 1) / kRowsD) load_wo(a, R, l, wb);
+            } else if (in(kStages * l + 4) && b < (D + kRowsH - 1) / kRowsH) {
+                load_wH(a, R, a->w2 + (long)l * D * H, D, b);
+            }
+            if (k0 <= 1 && in(kStages * l + 1) && u >= 0 && u < a->NH * a->n_chunks && u / a->NH < tk.nact)
+                load_kv(a, R, tk, l, u);
         }
-        if (g0 == 0) stamp(a, 0);
+        if (g0 == 0) stamp(a, sm.st, 0);
     }
     __syncthreads();
 
@@ -498,9 +541,9 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             const PTMI_CONST StepArgs *a = fresh(ap);
             const int D = a->D, KV = a->KV, QR = D + 2 * KV;
             const int blocks_qkv = (QR + kRowsD - 1) / kRowsD, blocks_wo = (D + kRowsD - 1) / kRowsD;
-            const int n_units = a->NH * a->n_chunks, u = b - a->ubase;
-            const bool unit = in(kStages * l + 1) && u >= 0 && u < n_units && u / a->NH < tk.nact;
-            const bool pre_wo = in(kStages * l + 2) && b < blocks_wo;
+            const int n_units = a->NH * a->n_chunks;
+            const int wb = b - a->wbase;
+            const bool pre_wo = in(kStages * l + 2) && wb >= 0 && wb < blocks_wo;
             const int qb = b - a->qbase;
             if (qb >= 0 && qb < blocks_qkv) {
                 __syncthreads();                              // xs is free again
@@ -512,9 +555,9 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     ok = tid >= kPollT || poll_words<5>(a->t_xb + (long)(l - 1) * D, D, tk.tag, sm.xs, a, tid);
                 }
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
-                stamp(a, 1 + 10 * l);
+                stamp(a, sm.st, 1 + 10 * l);
                 // the WO residual rows are rows of this same input
-                if (b < blocks_wo && tid < kRowsD) sm.xres[tid] = sm.xs[min(b * kRowsD + tid, D - 1)];
+                if (pre_wo && tid < kRowsD) sm.xres[tid] = sm.xs[min(wb * kRowsD + tid, D - 1)];
                 uint64_t *t_qkv = a->t_qkv + (long)l * QR;
                 for (int rb = qb; rb < blocks_qkv; rb += nb) {
                     if (rb != qb) {
@@ -522,10 +565,6 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                         load_wD(a, R, a->wqkv + (long)l * QR * D, QR, rb, a->rms_att + (long)l * D);
                     }
                     const float acc = dot_d(a, R, sm.xs, true);
-                    if (rb + nb >= blocks_qkv) {              // this block's last rows: next stages' loads
-                        if (unit) load_kv(a, R, tk, l, u);
-                        if (pre_wo) load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
-                    }
                     // RoPE pairs: rows 2k (lanes 0-31) and 2k+1 (lanes 32-63) of a wave
                     const LanePair pr = pl32(acc);
                     const int r = rb * kRowsD + slot_d();
@@ -553,27 +592,26 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                         }
                     }
                 }
-                stamp(a, 2 + 10 * l);
-            } else {
-                if (unit) load_kv(a, R, tk, l, u);
-                if (pre_wo) {
-                    load_wD(a, R, a->wo + (long)l * D * D, D, b, nullptr);
-                    // a Wo block without QKV rows takes its residual rows here
-                    __syncthreads();
-                    bool ok = true;
-                    if (tid < kRowsD) {
-                        if (l == 0) sm.xres[tid] = gl(a->emb + (long)tk.token * D)[min(b * kRowsD + tid, D - 1)];
-                        else ok = poll_words<1>(a->t_xb + (long)(l - 1) * D + b * kRowsD, min(kRowsD, D - b * kRowsD),
-                                                tk.tag, sm.xres, a, tid);
-                    }
-                    if (!block_ok(ok, &sm.fail, a->ctl)) return;
+                stamp(a, sm.st, 2 + 10 * l);
+            } else if (pre_wo) {
+                // a Wo block without QKV rows takes its residual rows here
+                __syncthreads();
+                bool ok = true;
+                if (tid < kRowsD) {
+                    if (l == 0) sm.xres[tid] = gl(a->emb + (long)tk.token * D)[min(wb * kRowsD + tid, D - 1)];
+                    else ok = poll_words<1>(a->t_xb + (long)(l - 1) * D + wb * kRowsD, min(kRowsD, D - wb * kRowsD),
+                                            tk.tag, sm.xres, a, tid);
                 }
+                if (!block_ok(ok, &sm.fail, a->ctl)) return;
             }
+            // after QKV: this layer's w1|w3 rows (used in W13)
+            const int H = a->H;
+            if (in(kStages * l + 3) && b < (2 * H + kRowsD - 1) / kRowsD)
+                load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, b, a->rms_ffn + (long)l * D);
             // Workgroups with no QKV, attention or Wo work wait until the
             // w1|w3 stage: meanwhile they stage this layer's w1|w3 and w2
             // rows in their XCD's L2 (and through it the MALL).
-            const int H = a->H;
-            const int first_idle = max(max(a->qbase + blocks_qkv, blocks_wo), a->ubase + n_units);
+            const int first_idle = max(max(a->qbase + blocks_qkv, a->wbase + blocks_wo), a->ubase + n_units);
             if (b >= first_idle && (a->l2pf & 1)) {
                 pf_acc = prefetch_rows(a->w13 + (long)l * 2 * H * D, 2 * H, D, kRowsD, (2 * H + kRowsD - 1) / kRowsD,
                                        first_idle, nb, pf_acc);
@@ -607,7 +645,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     ok = poll_words<1>(t_qkv + D + KV + kvh * hd, hd, tk.tag, sm.vp, a, tid - 256);
                 }
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
-                stamp(a, 3 + 10 * l);
+                stamp(a, sm.st, 3 + 10 * l);
                 const int slot = lane / GA, sub = lane % GA;
                 const bool has = sub < (hd >> 2);
                 const int sub_c = has ? sub : 0;
@@ -733,7 +771,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                         if (lane < hd) tstore(a->t_att + (long)l * D + h * hd + lane, v, tk.tag);
                     }
                 }
-                stamp(a, 4 + 10 * l);
+                stamp(a, sm.st, 4 + 10 * l);
             }
         }
 
@@ -741,22 +779,23 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
         if (in(kStages * l + 2)) {
             const PTMI_CONST StepArgs *a = fresh(ap);
             const int D = a->D, H = a->H;
-            const int blocks_wo = (D + kRowsD - 1) / kRowsD, blocks_w13 = (2 * H + kRowsD - 1) / kRowsD;
+            const int blocks_wo = (D + kRowsD - 1) / kRowsD;
             const float *x_emb = a->emb + (long)tk.token * D;
             const uint64_t *t_xin = a->t_xb + (long)(l - 1) * D;      // used for l > 0 only
             uint64_t *t_xa = a->t_xa + (long)l * D;
-            if (b < blocks_wo) {
+            const int wb = b - a->wbase;
+            if (wb >= 0 && wb < blocks_wo) {
                 __syncthreads();
                 bool ok = tid >= kPollT || poll_words<5>(a->t_att + (long)l * D, D, tk.tag, sm.xs, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
-                stamp(a, 5 + 10 * l);
+                stamp(a, sm.st, 5 + 10 * l);
                 // the residual rows came with this layer's QKV input when the
                 // QKV stage ran in this launch; otherwise they are read here
                 const bool res_here = !in(kStages * l);
-                for (int rb = b; rb < blocks_wo; rb += nb) {
-                    if (rb != b || res_here) {
+                for (int rb = wb; rb < blocks_wo; rb += nb) {
+                    if (rb != wb || res_here) {
                         __syncthreads();                      // the writer wave is done with yout
-                        if (rb != b) load_wD(a, R, a->wo + (long)l * D * D, D, rb, nullptr);
+                        if (rb != wb) load_wo(a, R, l, rb);
                         bool ok2 = true;
                         if (tid < kRowsD) {
                             if (l == 0) sm.xres[tid] = gl(x_emb)[min(rb * kRowsD + tid, D - 1)];
@@ -764,19 +803,17 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                         }
                         if (!block_ok(ok2, &sm.fail, a->ctl)) return;
                     }
-                    const float acc = dot_d(a, R, sm.xs, false);
-                    if (rb + nb >= blocks_wo && b < blocks_w13 && in(kStages * l + 3))
-                        load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, b, a->rms_ffn + (long)l * D);
+                    const float acc = dot_wo(a, R, sm.xs);
                     const int slot = slot_d();
                     if ((lane & 31) == 0) sm.yout[slot] = sm.xres[slot] + acc;
                     __syncthreads();
                     if (wave == kWriter && lane < kRowsD && rb * kRowsD + lane < D)
                         tstore(t_xa + rb * kRowsD + lane, sm.yout[lane], tk.tag);
                 }
-                stamp(a, 6 + 10 * l);
-            } else if (b < blocks_w13 && in(kStages * l + 3)) {
-                load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, b, a->rms_ffn + (long)l * D);
+                stamp(a, sm.st, 6 + 10 * l);
             }
+            // after Wo: this layer's w2 rows (used in W2)
+            if (in(kStages * l + 4) && b < (D + kRowsH - 1) / kRowsH) load_wH(a, R, a->w2 + (long)l * D * H, D, b);
         }
 
         // ── W13: hb = silu(w1 . xn) * (w3 . xn), xn = rmsnorm(x_a)
@@ -789,7 +826,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 __syncthreads();                              // xs and xres2 are free again
                 bool ok = tid >= kPollT || poll_words<5>(a->t_xa + (long)l * D, D, tk.tag, sm.xs, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
-                stamp(a, 7 + 10 * l);
+                stamp(a, sm.st, 7 + 10 * l);
                 // the W2 residual rows are rows of this same input
                 if (b < blocks_w2 && tid < kRowsH) sm.xres2[tid] = sm.xs[min(b * kRowsH + tid, D - 1)];
                 uint64_t *t_hb = a->t_hb + (long)l * H;
@@ -799,7 +836,6 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                         load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, rb, a->rms_ffn + (long)l * D);
                     }
                     const float acc = dot_d(a, R, sm.xs, true);
-                    if (rb + nb >= blocks_w13 && b < blocks_w2 && in(kStages * l + 4)) load_wH(a, R, a->w2 + (long)l * D * H, D, b);
                     const LanePair pr = pl32(acc);
                     if (lane == 0) {
                         const float h1 = pr.lo, h3 = pr.hi;
@@ -810,9 +846,16 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     const int i = rb * (kRowsD / 2) + lane;       // hb index of row pair `lane`
                     if (wave == kWriter && lane < kRowsD / 2 && 2 * i < 2 * H) tstore(t_hb + i, sm.yout[lane], tk.tag);
                 }
-                stamp(a, 8 + 10 * l);
-            } else if (b < blocks_w2 && in(kStages * l + 4)) {
-                load_wH(a, R, a->w2 + (long)l * D * H, D, b);
+                stamp(a, sm.st, 8 + 10 * l);
+            }
+            // after W13: the next layer's QKV rows, or the classifier's
+            if (in(kStages * (l + 1))) {
+                const int QR = D + 2 * a->KV, qb = b - a->qbase;
+                if (l + 1 == a->L) {
+                    if (b < (a->V + kRowsD - 1) / kRowsD) load_wD(a, R, a->wcls, a->V, b, a->rms_final);
+                } else if (qb >= 0 && qb < (QR + kRowsD - 1) / kRowsD) {
+                    load_wD(a, R, a->wqkv + (long)(l + 1) * QR * D, QR, qb, a->rms_att + (long)(l + 1) * D);
+                }
             }
         }
 
@@ -822,13 +865,6 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             const int D = a->D, H = a->H, QR = D + 2 * a->KV;
             const int blocks_w2 = (D + kRowsH - 1) / kRowsH, blocks_w13 = (2 * H + kRowsD - 1) / kRowsD;
             const bool last_layer = l + 1 == a->L;
-            const int next_blocks = last_layer ? (a->V + kRowsD - 1) / kRowsD : (QR + kRowsD - 1) / kRowsD;
-            auto preload_next = [&]() {
-                const int nb_idx = last_layer ? b : b - a->qbase;   // the next stage's row block
-                if (nb_idx < 0 || nb_idx >= next_blocks || !in(kStages * (l + 1))) return;
-                if (last_layer) load_wD(a, R, a->wcls, a->V, b, a->rms_final);
-                else load_wD(a, R, a->wqkv + (long)(l + 1) * QR * D, QR, nb_idx, a->rms_att + (long)(l + 1) * D);
-            };
             if (b < blocks_w2) {
                 const uint64_t *t_xa = a->t_xa + (long)l * D;
                 uint64_t *t_xb = a->t_xb + (long)l * D;
@@ -837,7 +873,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 if (ok && tid < kRowsH && (b >= blocks_w13 || !in(kStages * l + 3)))   // residual rows not taken in W13
                     ok = poll_words<1>(t_xa + b * kRowsH, min(kRowsH, D - b * kRowsH), tk.tag, sm.xres2, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
-                stamp(a, 9 + 10 * l);
+                stamp(a, sm.st, 9 + 10 * l);
                 for (int rb = b; rb < blocks_w2; rb += nb) {
                     if (rb != b) {
                         __syncthreads();                      // the writer wave is done with yout
@@ -848,31 +884,41 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                         if (!block_ok(ok2, &sm.fail, a->ctl)) return;
                     }
                     const float acc = dot_h(a, R, sm.xs);
-                    if (rb + nb >= blocks_w2) preload_next();
                     if (lane == 0) sm.yout[wave] = sm.xres2[wave] + acc;
                     __syncthreads();
                     if (wave == kWriter && lane < kRowsH && rb * kRowsH + lane < D)
                         tstore(t_xb + rb * kRowsH + lane, sm.yout[lane], tk.tag);
                 }
-                stamp(a, 10 + 10 * l);
+                stamp(a, sm.st, 10 + 10 * l);
             } else {
-                preload_next();
                 // idle until the next layer's QKV input: stage its QKV and Wo
                 // rows in this XCD's L2
                 if (!last_layer && (a->l2pf & 2)) {
                     // (with the QKV blocks past the w2 blocks, their rows are
-                    // already in registers)
+                    // already in registers, and so are the Wo rows of the Wo
+                    // blocks on QKV workgroups)
                     if (a->qbase == 0)
                         pf_acc = prefetch_rows(a->wqkv + (long)(l + 1) * QR * D, QR, D, kRowsD, (QR + kRowsD - 1) / kRowsD,
                                                blocks_w2, nb, pf_acc);
-                    pf_acc = prefetch_rows(a->wo + (long)(l + 1) * D * D, D, D, kRowsD, (D + kRowsD - 1) / kRowsD,
-                                           blocks_w2, nb, pf_acc);
+                    if (a->wbase == 0)
+                        pf_acc = prefetch_rows(a->wo + (long)(l + 1) * D * D, D, D, kRowsD, (D + kRowsD - 1) / kRowsD,
+                                               blocks_w2, nb, pf_acc);
                 }
+            }
+            // after W2: the next layer's K/V rows (attention units) and Wo rows
+            if (!last_layer) {
+                const int u = b - a->ubase, wb = b - a->wbase;
+                if (in(kStages * (l + 1) + 1) && u >= 0 && u < a->NH * a->n_chunks && u / a->NH < tk.nact)
+                    load_kv(a, R, tk, l + 1, u);
+                if (in(kStages * (l + 1) + 2) && wb >= 0 && wb < (D + kRowsD - 1) / kRowsD) load_wo(a, R, l + 1, wb);
             }
         }
     }
     if (pf_acc == 1.2345e-37f) sm.fail = 2;            // never true: keeps the prefetch loads
-    if (!in(kStages * L)) return;                     // the classifier is in a later launch
+    if (!in(kStages * L)) {                           // the classifier is in a later launch
+        flush_stamps(fresh(ap), sm.st);
+        return;
+    }
 
     // ── classifier: logits = Wcls . rmsnorm(x) (llama2.c:195-197), and this
     //    workgroup's argmax candidate ──
@@ -891,7 +937,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             __syncthreads();
             bool ok = tid >= kPollT || poll_words<5>(a->t_xb + (long)(a->L - 1) * a->D, a->D, tk.tag, sm.xs, a, tid);
             if (!block_ok(ok, &sm.fail, a->ctl)) return;
-            stamp(a, 1 + 10 * a->L);
+            stamp(a, sm.st, 1 + 10 * a->L);
             norm_x_d(a, R, sm.xs, xr);
             // one row block: its logits (ycls[p], stored by the writer wave)
             // and this lane's argmax candidate.  ycls alternates, so the
@@ -919,7 +965,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 if (rb + 3 * nb < blocks_cls) load_rows_d(a, wB, a->wcls, a->V, rb + 3 * nb);
                 store(rb + nb, 1);
             }
-            stamp(a, 2 + 10 * a->L);
+            stamp(a, sm.st, 2 + 10 * a->L);
         }
     }
     // workgroup argmax: DPP within rows of 16, the permlane swaps, then
@@ -958,14 +1004,17 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
         tstore(a->t_cand + 2 * b, v, tk.tag);
         tstore(a->t_cand + 2 * b + 1, __int_as_float(i), tk.tag);
     }
-    if (b != 0) return;
+    if (b != 0) {
+        flush_stamps(a, sm.st);
+        return;
+    }
 
     // ── workgroup 0: the step's argmax, prompt forcing and position
     //    advance (pt.c:267-271, pt_text.c:344-350) ──
     __syncthreads();
     bool ok = tid >= kPollT || poll_words<3>(a->t_cand, 2 * nb, tk.tag, sm.cand, a, tid);
     if (!block_ok(ok, &sm.fail, a->ctl)) return;
-    stamp(a, 3 + 10 * a->L);
+    stamp(a, sm.st, 3 + 10 * a->L);
     bv = -INFINITY;
     bi = 0x7fffffff;
     for (int w = tid; w < nb; w += kT) take_best(bv, bi, sm.cand[2 * w], __float_as_int(sm.cand[2 * w + 1]));
@@ -1007,7 +1056,8 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
         ctl->seq = (int)tk.tag;
         if (a->out_tokens) gl(a->out_tokens)[pos] = next;
     }
-    stamp(a, 4 + 10 * a->L);
+    stamp(a, sm.st, 4 + 10 * a->L);
+    flush_stamps(a, sm.st);
 }
 
 using StepFn = void (*)(const StepArgs *, int, int);
@@ -1067,6 +1117,8 @@ int decode_step_create(ptmi_model *m) {
     const size_t words = L * (D + 2 * KV) + L * nc * NH * (hd + 2) + 3 * L * D + L * H + 2 * (size_t)nb;
     const char *st_env = getenv("PTMI_STEP_STAMPS");
     const int n_stamps = (st_env && st_env[0] == '1') ? (int)(1 + 10 * L + 4) : 0;
+    if (n_stamps > kStampSlots)
+        return set_error(PTMI_ERR_ARG, "PTMI_STEP_STAMPS=1: the stamps hold at most 32 layers (model has %ld)", L);
     const size_t args_off = (words * sizeof(uint64_t) + 255) / 256 * 256;
     const size_t stamps_off = (args_off + sizeof(StepArgs) + 255) / 256 * 256;
     const size_t total = stamps_off + (size_t)nb * n_stamps * sizeof(uint64_t);
@@ -1091,6 +1143,11 @@ int decode_step_create(ptmi_model *m) {
         const char *qs = getenv("PTMI_STEP_QBASE");
         const int blocks_qkv = (int)((D + 2 * KV + kRowsD - 1) / kRowsD), blocks_w2 = (int)((D + kRowsH - 1) / kRowsH);
         a.qbase = (!(qs && qs[0] == '0') && blocks_w2 + blocks_qkv <= nb) ? blocks_w2 : 0;
+        // The Wo row blocks sit on the first QKV workgroups (PTMI_STEP_WBASE=0:
+        // from workgroup 0), idle between QKV and Wo, so the w2 workgroups
+        // are idle in Wo and load their w2 rows then
+        const char *ws = getenv("PTMI_STEP_WBASE");
+        a.wbase = (ws && ws[0] == '0') ? 0 : a.qbase;
         const bool ub_on = !(ub && ub[0] == '0');
         if (a.qbase > 0)
             a.ubase = NH * nc <= a.qbase ? 0 : (ub_on && a.qbase + blocks_qkv + NH * nc <= nb ? a.qbase + blocks_qkv : 0);
@@ -1121,7 +1178,7 @@ int decode_step_create(ptmi_model *m) {
     // always.  PTMI_STEP_L2PF overrides.
     {
         const int blocks_qkv = (int)((D + 2 * KV + kRowsD - 1) / kRowsD), blocks_wo = (int)((D + kRowsD - 1) / kRowsD);
-        const int first_idle = std::max(std::max(a.qbase + blocks_qkv, blocks_wo), a.ubase + (int)(NH * nc));
+        const int first_idle = std::max(std::max(a.qbase + blocks_qkv, a.wbase + blocks_wo), a.ubase + (int)(NH * nc));
         const char *pf = getenv("PTMI_STEP_L2PF");
         a.l2pf = pf ? atoi(pf) & 3 : (nb - first_idle >= 64 ? 3 : 2);
     }
