@@ -585,10 +585,14 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                         const int rw = rb * kRowsD + lane;
                         if (rw < QR) {
                             const float out = sm.yout[lane];
-                            tstore(t_qkv + rw, out, tk.tag);
+                            // the cache row's address from the two (uniform)
+                            // base pointers, so no lane loads a pointer: a
+                            // load here would wait for the tagged store above
+                            float *const kc = a->kc, *const vc = a->vc;
                             const long crow = ((long)l * a->S + tk.pos) * KV;
-                            if (rw >= D + KV) gl(a->vc)[crow + (rw - D - KV)] = out;
-                            else if (rw >= D) gl(a->kc)[crow + (rw - D)] = out;
+                            float *cp = rw >= D + KV ? vc + crow + (rw - D - KV) : kc + crow + (rw - D);
+                            tstore(t_qkv + rw, out, tk.tag);
+                            if (rw >= D) *gl(cp) = out;
                         }
                     }
                 }
@@ -726,9 +730,14 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     // head's chunk-0 unit
                     uint64_t *dst = head_part + (long)c * (hd + 2);
                     if (wave == kWriter) {
-                        if (lane < hd) tstore(dst + lane, rec_o(lane), tk.tag);
+                        // the record's LDS reads all before its first store:
+                        // a read into registers that a store still holds
+                        // would wait for that store's acknowledgement
+                        float o = rec_o(min(lane, hd - 1)), ls = rec_l();
+                        asm volatile("" : "+v"(o), "+v"(ls));
+                        if (lane < hd) tstore(dst + lane, o, tk.tag);
                         if (lane == 0) tstore(dst + hd, mx, tk.tag);
-                        if (lane == 1) tstore(dst + hd + 1, rec_l(), tk.tag);
+                        if (lane == 1) tstore(dst + hd + 1, ls, tk.tag);
                     }
                 } else {
                     // chunk 0 merges the head's active chunks: its own
