@@ -199,6 +199,46 @@ __device__ bool poll_words(const uint64_t *src, int n, uint32_t tag, float *dst,
     }
 }
 
+// poll_words over word pairs: one 16-byte load (volatile: coherent at
+// system scope, so it bypasses the XCD's L2 like the agent-scope loads)
+// brings two tagged words, half the load requests of poll_words for a long
+// vector.  Pair p of thread t is words 2p, 2p+1, p = t, t + kPollT, ...;
+// src must be 16-byte aligned and n even.
+typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+template <int K>
+__device__ bool poll_pairs(const uint64_t *src, int n, uint32_t tag, float *dst, const PTMI_CONST StepArgs *a, int t) {
+    t = opaque(t);
+    const int np = n >> 1;
+    bool ok[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) ok[k] = t + k * kPollT >= np;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    const uint64_t wait_ticks = a->wait_ticks;
+    for (int round = 1;; round++) {
+        u64x2 v[K];
+#pragma unroll
+        for (int k = 0; k < K; k++)
+            if (!ok[k]) v[k] = *(const volatile PTMI_GLOBAL u64x2 *)(src + 2 * (t + k * kPollT));
+        bool all = true;
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            if (ok[k]) continue;
+            if ((uint32_t)(v[k].x >> 32) == tag && (uint32_t)(v[k].y >> 32) == tag) {
+                const int i = 2 * (t + k * kPollT);
+                dst[i] = __uint_as_float((uint32_t)v[k].x);
+                dst[i + 1] = __uint_as_float((uint32_t)v[k].y);
+                ok[k] = true;
+            } else {
+                all = false;
+            }
+        }
+        if (all) return true;
+        if (__builtin_amdgcn_s_memrealtime() - t0 > wait_ticks) return false;
+        if ((round & 31) == 0 && err_seen(a->ctl)) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 // Block-uniform end of a wait: every thread reaches the barrier; true when
 // the whole block may go on.
 __device__ __forceinline__ bool block_ok(bool mine, int *s_fail, DecodeCtl *ctl) {
@@ -878,7 +918,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 const uint64_t *t_xa = a->t_xa + (long)l * D;
                 uint64_t *t_xb = a->t_xb + (long)l * D;
                 __syncthreads();
-                bool ok = tid >= kPollT || poll_words<5>(a->t_hb + (long)l * H, H, tk.tag, sm.xs, a, tid);
+                bool ok = tid >= kPollT || poll_pairs<3>(a->t_hb + (long)l * H, H, tk.tag, sm.xs, a, tid);
                 if (ok && tid < kRowsH && (b >= blocks_w13 || !in(kStages * l + 3)))   // residual rows not taken in W13
                     ok = poll_words<1>(t_xa + b * kRowsH, min(kRowsH, D - b * kRowsH), tk.tag, sm.xres2, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
