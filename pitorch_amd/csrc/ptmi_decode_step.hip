@@ -592,7 +592,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     const float *x = a->emb + (long)tk.token * D;
                     for (int i = tid; i < D; i += kT) sm.xs[i] = gl(x)[i];
                 } else {
-                    ok = tid >= kPollT || poll_words<5>(a->t_xb + (long)(l - 1) * D, D, tk.tag, sm.xs, a, tid);
+                    ok = tid >= kPollT || poll_pairs<3>(a->t_xb + (long)(l - 1) * D, D, tk.tag, sm.xs, a, tid);
                 }
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, sm.st, 1 + 10 * l);
@@ -835,7 +835,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             const int wb = b - a->wbase;
             if (wb >= 0 && wb < blocks_wo) {
                 __syncthreads();
-                bool ok = tid >= kPollT || poll_words<5>(a->t_att + (long)l * D, D, tk.tag, sm.xs, a, tid);
+                bool ok = tid >= kPollT || poll_pairs<3>(a->t_att + (long)l * D, D, tk.tag, sm.xs, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, sm.st, 5 + 10 * l);
                 // the residual rows came with this layer's QKV input when the
@@ -873,7 +873,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             const int blocks_w13 = (2 * H + kRowsD - 1) / kRowsD, blocks_w2 = (D + kRowsH - 1) / kRowsH;
             if (b < blocks_w13) {
                 __syncthreads();                              // xs and xres2 are free again
-                bool ok = tid >= kPollT || poll_words<5>(a->t_xa + (long)l * D, D, tk.tag, sm.xs, a, tid);
+                bool ok = tid >= kPollT || poll_pairs<3>(a->t_xa + (long)l * D, D, tk.tag, sm.xs, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, sm.st, 7 + 10 * l);
                 // the W2 residual rows are rows of this same input
@@ -984,7 +984,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             float4 wB[ITD], xr[ITD];
             if (b + nb < blocks_cls) load_rows_d(a, wB, a->wcls, a->V, b + nb);
             __syncthreads();
-            bool ok = tid >= kPollT || poll_words<5>(a->t_xb + (long)(a->L - 1) * a->D, a->D, tk.tag, sm.xs, a, tid);
+            bool ok = tid >= kPollT || poll_pairs<3>(a->t_xb + (long)(a->L - 1) * a->D, a->D, tk.tag, sm.xs, a, tid);
             if (!block_ok(ok, &sm.fail, a->ctl)) return;
             stamp(a, sm.st, 1 + 10 * a->L);
             norm_x_d(a, R, sm.xs, xr);
@@ -1061,7 +1061,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
     // ── workgroup 0: the step's argmax, prompt forcing and position
     //    advance (pt.c:267-271, pt_text.c:344-350) ──
     __syncthreads();
-    bool ok = tid >= kPollT || poll_words<3>(a->t_cand, 2 * nb, tk.tag, sm.cand, a, tid);
+    bool ok = tid >= kPollT || poll_pairs<2>(a->t_cand, 2 * nb, tk.tag, sm.cand, a, tid);
     if (!block_ok(ok, &sm.fail, a->ctl)) return;
     stamp(a, sm.st, 3 + 10 * a->L);
     bv = -INFINITY;
