@@ -797,7 +797,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     }
                     bool ok = true;
                     if (nother > 0 && tid < kPollT)
-                        ok = poll_words<2>(head_part + (hd + 2), nother * (hd + 2), tk.tag, sm.part + (hd + 2), a, tid);
+                        ok = poll_pairs<1>(head_part + (hd + 2), nother * (hd + 2), tk.tag, sm.part + (hd + 2), a, tid);
                     if (!block_ok(ok, &sm.fail, a->ctl)) return;
                     if (wave == kWriter) {
                         auto rl = [](float x, int k) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k)); };
