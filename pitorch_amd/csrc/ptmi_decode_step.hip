@@ -342,16 +342,29 @@ __device__ __forceinline__ void load_wo(const PTMI_CONST StepArgs *a, Regs<ITD, 
 #pragma unroll
     for (int it = 0; it < ITD; it++) R.wH[it] = ntload4(row + 4 * min(sub + it * 32, nD4 - 1));
 }
+// The lane's chunks of the stage input xs (LDS), all reads issued before
+// any is used: one wait for the batch instead of one LDS round trip per
+// chunk (the scheduler otherwise interleaves each read with its use).
+template <int N, int STRIDE>
+__device__ __forceinline__ void read_xs(const float *xs, int n4, int sub, float4 (&xr)[N]) {
+#pragma unroll
+    for (int it = 0; it < N; it++) {
+        const int c = sub + it * STRIDE;
+        xr[it] = reinterpret_cast<const float4 *>(xs)[min(c, n4 - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int it = 0; it < N; it++) xr[it] = sel4(sub + it * STRIDE < n4, xr[it]);
+}
+
 template <int ITD, int ITH, int GA>
 __device__ __forceinline__ float dot_wo(const PTMI_CONST StepArgs *a, const Regs<ITD, ITH, GA> &R, const float *xs) {
     const int nD4 = a->D >> 2, sub = sub_d();
+    float4 xr[ITD];
+    read_xs<ITD, 32>(xs, nD4, sub, xr);
     float acc = 0.0f;
 #pragma unroll
-    for (int it = 0; it < ITD; it++) {
-        const int c = sub + it * 32;
-        const float4 x = sel4(c < nD4, reinterpret_cast<const float4 *>(xs)[min(c, nD4 - 1)]);
-        acc = dot4(sel4(c < nD4, R.wH[it]), x, acc);
-    }
+    for (int it = 0; it < ITD; it++) acc = dot4(sel4(sub + it * 32 < nD4, R.wH[it]), xr[it], acc);
     return group_sum<32>(acc);
 }
 
@@ -361,11 +374,7 @@ template <int ITD, int ITH, int GA>
 __device__ __forceinline__ float dot_d(const PTMI_CONST StepArgs *a, const Regs<ITD, ITH, GA> &R, const float *xs, bool norm) {
     const int nD4 = a->D >> 2, sub = sub_d();
     float4 xr[ITD];
-#pragma unroll
-    for (int it = 0; it < ITD; it++) {
-        const int c = sub + it * 32;
-        xr[it] = sel4(c < nD4, reinterpret_cast<const float4 *>(xs)[min(c, nD4 - 1)]);
-    }
+    read_xs<ITD, 32>(xs, nD4, sub, xr);
     if (norm) {                                       // rmsnorm, pt_ops.c:5-12
         float ss = 0.0f;
 #pragma unroll
@@ -395,11 +404,7 @@ template <int ITD, int ITH, int GA>
 __device__ __forceinline__ void norm_x_d(const PTMI_CONST StepArgs *a, const Regs<ITD, ITH, GA> &R, const float *xs,
                                          float4 (&xr)[ITD]) {
     const int nD4 = a->D >> 2, sub = sub_d();
-#pragma unroll
-    for (int it = 0; it < ITD; it++) {
-        const int c = sub + it * 32;
-        xr[it] = sel4(c < nD4, reinterpret_cast<const float4 *>(xs)[min(c, nD4 - 1)]);
-    }
+    read_xs<ITD, 32>(xs, nD4, sub, xr);
     float ss = 0.0f;
 #pragma unroll
     for (int it = 0; it < ITD; it++)
@@ -433,13 +438,11 @@ __device__ __forceinline__ float dot_rows_d(const PTMI_CONST StepArgs *a, const 
 template <int ITD, int ITH, int GA>
 __device__ __forceinline__ float dot_h(const PTMI_CONST StepArgs *a, const Regs<ITD, ITH, GA> &R, const float *xs) {
     const int nH4 = a->H >> 2, sub = opaque((int)threadIdx.x & 63);
+    float4 xr[ITH];
+    read_xs<ITH, 64>(xs, nH4, sub, xr);
     float acc = 0.0f;
 #pragma unroll
-    for (int it = 0; it < ITH; it++) {
-        const int c = sub + it * 64;
-        const bool in = c < nH4;
-        acc = dot4(sel4(in, R.wH[it]), sel4(in, reinterpret_cast<const float4 *>(xs)[min(c, nH4 - 1)]), acc);
-    }
+    for (int it = 0; it < ITH; it++) acc = dot4(sel4(sub + it * 64 < nH4, R.wH[it]), xr[it], acc);
     return group_sum<64>(acc);
 }
 
