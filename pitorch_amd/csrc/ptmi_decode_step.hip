@@ -353,8 +353,26 @@ __device__ __forceinline__ void read_xs(const float *xs, int n4, int sub, float4
         xr[it] = reinterpret_cast<const float4 *>(xs)[min(c, n4 - 1)];
     }
     __builtin_amdgcn_sched_barrier(0);
+    if (n4 < N * STRIDE) {                            // uniform: rows shorter than the lanes' span
 #pragma unroll
-    for (int it = 0; it < N; it++) xr[it] = sel4(sub + it * STRIDE < n4, xr[it]);
+        for (int it = 0; it < N; it++) xr[it] = sel4(sub + it * STRIDE < n4, xr[it]);
+    }
+}
+
+// sum over the lane's chunks of w . x; chunks past the row (clamped
+// re-reads) are dropped, and a row that fills every lane's chunks takes the
+// branch without the selects (the same sums)
+template <int N, int STRIDE>
+__device__ __forceinline__ float dot_chunks(const float4 (&w)[N], const float4 (&x)[N], int n4, int sub) {
+    float acc = 0.0f;
+    if (n4 >= N * STRIDE) {                           // uniform
+#pragma unroll
+        for (int it = 0; it < N; it++) acc = dot4(w[it], x[it], acc);
+    } else {
+#pragma unroll
+        for (int it = 0; it < N; it++) acc = dot4(sel4(sub + it * STRIDE < n4, w[it]), x[it], acc);
+    }
+    return acc;
 }
 
 template <int ITD, int ITH, int GA>
@@ -362,10 +380,10 @@ __device__ __forceinline__ float dot_wo(const PTMI_CONST StepArgs *a, const Regs
     const int nD4 = a->D >> 2, sub = sub_d();
     float4 xr[ITD];
     read_xs<ITD, 32>(xs, nD4, sub, xr);
-    float acc = 0.0f;
+    float4 wr[ITD];
 #pragma unroll
-    for (int it = 0; it < ITD; it++) acc = dot4(sel4(sub + it * 32 < nD4, R.wH[it]), xr[it], acc);
-    return group_sum<32>(acc);
+    for (int it = 0; it < ITD; it++) wr[it] = R.wH[it];
+    return group_sum<32>(dot_chunks<ITD, 32>(wr, xr, nD4, sub));
 }
 
 // The lane's D-row weights against xs (RMSNorm'd when norm): the row's sum
@@ -390,10 +408,7 @@ __device__ __forceinline__ float dot_d(const PTMI_CONST StepArgs *a, const Regs<
             xr[it].w = xr[it].w * inv * R.nw[it].w;
         }
     }
-    float acc = 0.0f;
-#pragma unroll
-    for (int it = 0; it < ITD; it++) acc = dot4(sel4(sub + it * 32 < nD4, R.wD[it]), xr[it], acc);
-    return group_sum<32>(acc);
+    return group_sum<32>(dot_chunks<ITD, 32>(R.wD, xr, nD4, sub));
 }
 
 // The classifier's two halves of dot_d: its rows all take the same
@@ -429,9 +444,7 @@ __device__ __forceinline__ void load_rows_d(const PTMI_CONST StepArgs *a, float4
 template <int ITD>
 __device__ __forceinline__ float dot_rows_d(const PTMI_CONST StepArgs *a, const float4 (&w)[ITD], const float4 (&xr)[ITD]) {
     const int nD4 = a->D >> 2, sub = sub_d();
-    float acc = 0.0f;
-#pragma unroll
-    for (int it = 0; it < ITD; it++) acc = dot4(sel4(sub + it * 32 < nD4, w[it]), xr[it], acc);
+    const float acc = dot_chunks<ITD, 32>(w, xr, nD4, sub);
     return group_sum<32>(acc);
 }
 
@@ -440,10 +453,7 @@ __device__ __forceinline__ float dot_h(const PTMI_CONST StepArgs *a, const Regs<
     const int nH4 = a->H >> 2, sub = opaque((int)threadIdx.x & 63);
     float4 xr[ITH];
     read_xs<ITH, 64>(xs, nH4, sub, xr);
-    float acc = 0.0f;
-#pragma unroll
-    for (int it = 0; it < ITH; it++) acc = dot4(sel4(sub + it * 64 < nH4, R.wH[it]), xr[it], acc);
-    return group_sum<64>(acc);
+    return group_sum<64>(dot_chunks<ITH, 64>(R.wH, xr, nH4, sub));
 }
 
 // K/V rows of attention unit u (head u % NH, chunk u / NH) at positions
