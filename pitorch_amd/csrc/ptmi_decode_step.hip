@@ -397,7 +397,7 @@ __device__ __forceinline__ float dot_d(const PTMI_CONST StepArgs *a, const Regs<
         float ss = 0.0f;
 #pragma unroll
         for (int it = 0; it < ITD; it++)
-            ss += xr[it].x * xr[it].x + xr[it].y * xr[it].y + xr[it].z * xr[it].z + xr[it].w * xr[it].w;
+            ss = dot4(xr[it], xr[it], ss);
         ss = group_sum<32>(ss);
         const float inv = 1.0f / d_sqrtf(ss / (float)a->D + 1e-5f);
 #pragma unroll
@@ -423,7 +423,7 @@ __device__ __forceinline__ void norm_x_d(const PTMI_CONST StepArgs *a, const Reg
     float ss = 0.0f;
 #pragma unroll
     for (int it = 0; it < ITD; it++)
-        ss += xr[it].x * xr[it].x + xr[it].y * xr[it].y + xr[it].z * xr[it].z + xr[it].w * xr[it].w;
+        ss = dot4(xr[it], xr[it], ss);
     ss = group_sum<32>(ss);
     const float inv = 1.0f / d_sqrtf(ss / (float)a->D + 1e-5f);
 #pragma unroll
