@@ -199,26 +199,45 @@ __device__ bool poll_words(const uint64_t *src, int n, uint32_t tag, float *dst,
     }
 }
 
-// poll_words over word pairs: one 16-byte load (volatile: coherent at
-// system scope, so it bypasses the XCD's L2 like the agent-scope loads)
-// brings two tagged words, half the load requests of poll_words for a long
-// vector.  Pair p of thread t is words 2p, 2p+1, p = t, t + kPollT, ...;
+// poll_words over word pairs: one 16-byte load (coherent at system scope,
+// so it bypasses the XCD's L2 like the agent-scope loads) brings two tagged
+// words, half the load requests of poll_words for a long vector.  Pair p of thread t is words 2p, 2p+1, p = t, t + kPollT, ...;
 // src must be 16-byte aligned and n even.
 typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kSysScope = 1 | 16;            // buffer cache policy: sc0 | sc1
 template <int K>
 __device__ bool poll_pairs(const uint64_t *src, int n, uint32_t tag, float *dst, const PTMI_CONST StepArgs *a, int t) {
     t = opaque(t);
     const int np = n >> 1;
-    bool ok[K];
+    bool valid[K], ok[K];
 #pragma unroll
-    for (int k = 0; k < K; k++) ok[k] = t + k * kPollT >= np;
+    for (int k = 0; k < K; k++) ok[k] = !(valid[k] = t + k * kPollT < np);
+    // every round loads all K pairs (past the vector: its last pair again),
+    // so each register set is only ever written by a load.  The loads are
+    // buffer loads with the system-scope cache bits (sc0 sc1: past this
+    // XCD's L2, like a volatile load) but not volatile: a volatile load is
+    // followed by a wait for it, which would serialise a round's loads and
+    // the two rounds.  The offset goes through opaque() at every load, so no
+    // load is taken as loop-invariant.
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, np * 16, 0x00020000);
+    auto pair = [&](int k) {
+        const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, opaque(16 * min(t + k * kPollT, np - 1)), 0, kSysScope);
+        u64x2 v;
+        v.x = (uint64_t)w.x | ((uint64_t)w.y << 32);
+        v.y = (uint64_t)w.z | ((uint64_t)w.w << 32);
+        return v;
+    };
+    // Two rounds in flight: round r + 1's loads go out before round r's
+    // words are checked, so a word that lands is seen about half a round
+    // trip sooner than with one round at a time.  The loop alternates two
+    // register sets (a copy between them would wait for the loads).
+    u64x2 va[K], vb[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) va[k] = pair(k);
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     const uint64_t wait_ticks = a->wait_ticks;
-    for (int round = 1;; round++) {
-        u64x2 v[K];
-#pragma unroll
-        for (int k = 0; k < K; k++)
-            if (!ok[k]) v[k] = *(const volatile PTMI_GLOBAL u64x2 *)(src + 2 * (t + k * kPollT));
+    auto check = [&](const u64x2 (&v)[K]) {
         bool all = true;
 #pragma unroll
         for (int k = 0; k < K; k++) {
@@ -232,9 +251,24 @@ __device__ bool poll_pairs(const uint64_t *src, int n, uint32_t tag, float *dst,
                 all = false;
             }
         }
-        if (all) return true;
+        return all;
+    };
+    // The wave leaves the loop together (a lane that has all its words
+    // keeps loading until every lane has): with per-lane exits the loop's
+    // register sets are copied at its latch, which waits for their loads.
+    asm volatile("" ::: "memory");
+    for (int round = 1;; round += 2) {
+#pragma unroll
+        for (int k = 0; k < K; k++) vb[k] = pair(k);
+        asm volatile("" ::: "memory");
+        if (__all(check(va))) return true;
         if (__builtin_amdgcn_s_memrealtime() - t0 > wait_ticks) return false;
-        if ((round & 31) == 0 && err_seen(a->ctl)) return false;
+        if ((round & 31) == 1 && __any(err_seen(a->ctl))) return false;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int k = 0; k < K; k++) va[k] = pair(k);
+        asm volatile("" ::: "memory");
+        if (__all(check(vb))) return true;
         __builtin_amdgcn_s_sleep(1);
     }
 }
@@ -518,6 +552,8 @@ constexpr int kStages = 5;
 template <int ITD, int ITH, int GA>
 __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, int g1) {
     using Rg = Regs<ITD, ITH, GA>;
+    // word pairs per polling thread of a dim-length and a hidden-length vector
+    constexpr int kPD = (ITD * 64 + kPollT - 1) / kPollT, kPH = (ITH * 128 + kPollT - 1) / kPollT;
     __shared__ Smem sm;
     Rg R;
     float pf_acc = 0.0f;                              // keeps prefetch loads alive
@@ -605,7 +641,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     const float *x = a->emb + (long)tk.token * D;
                     for (int i = tid; i < D; i += kT) sm.xs[i] = gl(x)[i];
                 } else {
-                    ok = tid >= kPollT || poll_pairs<3>(a->t_xb + (long)(l - 1) * D, D, tk.tag, sm.xs, a, tid);
+                    ok = tid >= kPollT || poll_pairs<kPD>(a->t_xb + (long)(l - 1) * D, D, tk.tag, sm.xs, a, tid);
                 }
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, sm.st, 1 + 10 * l);
@@ -848,7 +884,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             const int wb = b - a->wbase;
             if (wb >= 0 && wb < blocks_wo) {
                 __syncthreads();
-                bool ok = tid >= kPollT || poll_pairs<3>(a->t_att + (long)l * D, D, tk.tag, sm.xs, a, tid);
+                bool ok = tid >= kPollT || poll_pairs<kPD>(a->t_att + (long)l * D, D, tk.tag, sm.xs, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, sm.st, 5 + 10 * l);
                 // the residual rows came with this layer's QKV input when the
@@ -886,7 +922,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             const int blocks_w13 = (2 * H + kRowsD - 1) / kRowsD, blocks_w2 = (D + kRowsH - 1) / kRowsH;
             if (b < blocks_w13) {
                 __syncthreads();                              // xs and xres2 are free again
-                bool ok = tid >= kPollT || poll_pairs<3>(a->t_xa + (long)l * D, D, tk.tag, sm.xs, a, tid);
+                bool ok = tid >= kPollT || poll_pairs<kPD>(a->t_xa + (long)l * D, D, tk.tag, sm.xs, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, sm.st, 7 + 10 * l);
                 // the W2 residual rows are rows of this same input
@@ -931,7 +967,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 const uint64_t *t_xa = a->t_xa + (long)l * D;
                 uint64_t *t_xb = a->t_xb + (long)l * D;
                 __syncthreads();
-                bool ok = tid >= kPollT || poll_pairs<3>(a->t_hb + (long)l * H, H, tk.tag, sm.xs, a, tid);
+                bool ok = tid >= kPollT || poll_pairs<kPH>(a->t_hb + (long)l * H, H, tk.tag, sm.xs, a, tid);
                 if (ok && tid < kRowsH && (b >= blocks_w13 || !in(kStages * l + 3)))   // residual rows not taken in W13
                     ok = poll_words<1>(t_xa + b * kRowsH, min(kRowsH, D - b * kRowsH), tk.tag, sm.xres2, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
@@ -997,7 +1033,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             float4 wB[ITD], xr[ITD];
             if (b + nb < blocks_cls) load_rows_d(a, wB, a->wcls, a->V, b + nb);
             __syncthreads();
-            bool ok = tid >= kPollT || poll_pairs<3>(a->t_xb + (long)(a->L - 1) * a->D, a->D, tk.tag, sm.xs, a, tid);
+            bool ok = tid >= kPollT || poll_pairs<kPD>(a->t_xb + (long)(a->L - 1) * a->D, a->D, tk.tag, sm.xs, a, tid);
             if (!block_ok(ok, &sm.fail, a->ctl)) return;
             stamp(a, sm.st, 1 + 10 * a->L);
             norm_x_d(a, R, sm.xs, xr);
