@@ -337,7 +337,7 @@ def pmc_workload(pa, name, positions):
           file=sys.stderr)
 
 
-def step_stamps(pa, name, at):
+def step_stamps(pa, name, at, out=""):
     """The one-kernel decode step's stage timeline (PTMI_DECODE_STEP=1 with
     stage stamps): a greedy decode from position 0; for the step at each
     position in `at`, every workgroup's stamps (the GPU's 100 MHz real-time
@@ -345,7 +345,8 @@ def step_stamps(pa, name, at):
     finishing the previous stage to the last finishing this one; the
     release, from that same point to the median workgroup of this stage
     seeing its input (the hand-off); and the median work after the release.
-    Medians and maxima are over the layers.  Prints markdown on stdout."""
+    Medians and maxima are over the layers.  Prints markdown on stdout;
+    `out` (a .npz path) also keeps every workgroup's raw stamps per position."""
     import numpy as np
     os.environ["PTMI_DECODE_STEP"] = "1"
     os.environ["PTMI_STEP_STAMPS"] = "1"
@@ -360,6 +361,7 @@ def step_stamps(pa, name, at):
           "| work median µs |")
     print("|---:|---|---:|---:|---:|---:|---:|---:|")
     rows = []
+    raw = {}
     tok = int(prompt[0])
     for pos in range(max(at) + 1):
         nxt = m.forward_step(tok)
@@ -367,6 +369,7 @@ def step_stamps(pa, name, at):
         if pos not in at:
             continue
         st = m.step_stamps().astype(np.int64)
+        raw[f"pos{pos}"] = st
         span = {s_: [] for s_ in stages}
         rel = {s_: [] for s_ in stages}
         work = {s_: [] for s_ in stages}
@@ -403,6 +406,8 @@ def step_stamps(pa, name, at):
     print("|---:|---:|---:|---:|---:|---:|---:|---:|")
     for pos, med, mx, total, spread, cls, arel, awork in rows:
         print(f"| {pos} | {med:.2f} | {mx:.2f} | {total:.2f} | {spread:.2f} | {cls:.2f} | {arel:.2f} | {awork:.2f} |")
+    if out:
+        np.savez_compressed(out, **raw)
     m.close()
 
 
@@ -449,6 +454,8 @@ def main():
                     help="counter-profile workload, no timing: POSITIONS decode steps of the --config model "
                          "enqueued without graphs, 8 at a time (rocprofv3 --pmc faults on its host side with "
                          "thousands of dispatches in flight), then the 256 MiB calibration copy")
+    ap.add_argument("--stamps-out", type=str, default="", metavar="NPZ",
+                    help="with --step-stamps: also save every workgroup's raw stamps")
     ap.add_argument("--step-stamps", type=str, default="", metavar="POSITIONS",
                     help="print the one-kernel decode step's stage timeline at these comma-separated positions "
                          "(greedy decode of the --config model from position 0), not the bench line")
@@ -472,7 +479,7 @@ def main():
         pmc_workload(pa, args.config, args.pmc_workload)
         return
     if args.step_stamps:
-        step_stamps(pa, args.config, sorted(int(p) for p in args.step_stamps.split(",")))
+        step_stamps(pa, args.config, sorted(int(p) for p in args.step_stamps.split(",")), args.stamps_out)
         return
 
     name = args.config
