@@ -612,7 +612,8 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 }
             }
             if (k0 <= 2) {
-                if (in(kStages * l + 2) && wb >= 0 && wb < (D + kRowsD - 1) / kRowsD) load_wo(a, R, l, wb);
+                // (a window from QKV loads them after its QKV stage)
+                if (k0 > 0 && in(kStages * l + 2) && wb >= 0 && wb < (D + kRowsD - 1) / kRowsD) load_wo(a, R, l, wb);
             } else if (in(kStages * l + 4) && b < (D + kRowsH - 1) / kRowsH) {
                 load_wH(a, R, a->w2 + (long)l * D * H, D, b);
             }
@@ -697,10 +698,13 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 }
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
             }
-            // after QKV: this layer's w1|w3 rows (used in W13)
+            // after QKV: this layer's w1|w3 rows (used in W13) and Wo rows
+            // (the Wo blocks sit on QKV workgroups: loaded before the QKV
+            // wait, they held it back, since a wave's loads complete in order)
             const int H = a->H;
             if (in(kStages * l + 3) && b < (2 * H + kRowsD - 1) / kRowsD)
                 load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, b, a->rms_ffn + (long)l * D);
+            if (pre_wo) load_wo(a, R, l, wb);
             // Workgroups with no QKV, attention or Wo work wait until the
             // w1|w3 stage: meanwhile they stage this layer's w1|w3 and w2
             // rows in their XCD's L2 (and through it the MALL).
@@ -1003,12 +1007,11 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                                                blocks_w2, nb, pf_acc);
                 }
             }
-            // after W2: the next layer's K/V rows (attention units) and Wo rows
+            // after W2: the next layer's K/V rows (attention units)
             if (!last_layer) {
-                const int u = b - a->ubase, wb = b - a->wbase;
+                const int u = b - a->ubase;
                 if (in(kStages * (l + 1) + 1) && u >= 0 && u < a->NH * a->n_chunks && u / a->NH < tk.nact)
                     load_kv(a, R, tk, l + 1, u);
-                if (in(kStages * (l + 1) + 2) && wb >= 0 && wb < (D + kRowsD - 1) / kRowsD) load_wo(a, R, l + 1, wb);
             }
         }
     }
