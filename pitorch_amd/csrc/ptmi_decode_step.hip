@@ -492,7 +492,7 @@ __device__ __forceinline__ float dot_h(const PTMI_CONST StepArgs *a, const Regs<
 
 // K/V rows of attention unit u (head u % NH, chunk u / NH) at positions
 // below pos (written by earlier tokens' kernels), clamped into the chunk.
-template <int ITD, int ITH, int GA>
+template <int ITD, int ITH, int GA, bool V>
 __device__ __forceinline__ void load_kv(const PTMI_CONST StepArgs *a, Regs<ITD, ITH, GA> &R, const Tok &t, int l, int u) {
     using Rg = Regs<ITD, ITH, GA>;
     const int lane = (int)threadIdx.x & 63, wave = opaque((int)threadIdx.x >> 6);
@@ -506,9 +506,20 @@ __device__ __forceinline__ void load_kv(const PTMI_CONST StepArgs *a, Regs<ITD, 
     for (int q = 0; q < Rg::kU; q++) {
         const int row = t0 + q * (kW * Rg::kRPW) + wave * Rg::kRPW + slot;
         const long o = base + (long)max(t0, min(row, top)) * a->KV;
-        R.kk[q] = ntload4(a->kc + o);
-        R.vv[q] = ntload4(a->vc + o);
+        if constexpr (V) R.vv[q] = ntload4(a->vc + o);
+        else R.kk[q] = ntload4(a->kc + o);
     }
+}
+// The K rows go out a stage ahead; the V rows only once the unit's q, k and
+// v are in (they are first used after the softmax): loaded with the K rows,
+// they held back that wait, since a wave's loads complete in order.
+template <int ITD, int ITH, int GA>
+__device__ __forceinline__ void load_k(const PTMI_CONST StepArgs *a, Regs<ITD, ITH, GA> &R, const Tok &t, int l, int u) {
+    load_kv<ITD, ITH, GA, false>(a, R, t, l, u);
+}
+template <int ITD, int ITH, int GA>
+__device__ __forceinline__ void load_v(const PTMI_CONST StepArgs *a, Regs<ITD, ITH, GA> &R, const Tok &t, int l, int u) {
+    load_kv<ITD, ITH, GA, true>(a, R, t, l, u);
 }
 
 // L2 prefetch by a workgroup that has no work in the current window: row
@@ -618,7 +629,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 load_wH(a, R, a->w2 + (long)l * D * H, D, b);
             }
             if (k0 <= 1 && in(kStages * l + 1) && u >= 0 && u < a->NH * a->n_chunks && u / a->NH < tk.nact)
-                load_kv(a, R, tk, l, u);
+                load_k(a, R, tk, l, u);
         }
         if (g0 == 0) stamp(a, sm.st, 0);
     }
@@ -727,7 +738,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 if (u < 0) continue;                          // uniform
                 const int h = u % NH, c = u / NH;
                 if (c >= tk.nact) continue;                   // uniform: chunk past pos
-                if (u != u0) load_kv(a, R, tk, l, u);
+                if (u != u0) load_k(a, R, tk, l, u);
                 const int t0 = c * a->chunk, t_end = min(t0 + a->chunk, tk.pos + 1), cnt = t_end - t0;
                 const bool has_pos = tk.pos < t_end;
                 const int kvh = h / a->kv_mul;
@@ -743,6 +754,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 }
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, sm.st, 3 + 10 * l);
+                load_v(a, R, tk, l, u);
                 const int slot = lane / GA, sub = lane % GA;
                 const bool has = sub < (hd >> 2);
                 const int sub_c = has ? sub : 0;
@@ -1011,7 +1023,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             if (!last_layer) {
                 const int u = b - a->ubase;
                 if (in(kStages * (l + 1) + 1) && u >= 0 && u < a->NH * a->n_chunks && u / a->NH < tk.nact)
-                    load_kv(a, R, tk, l + 1, u);
+                    load_k(a, R, tk, l + 1, u);
             }
         }
     }
