@@ -206,13 +206,13 @@ __device__ bool poll_words(const uint64_t *src, int n, uint32_t tag, float *dst,
 typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kSysScope = 1 | 16;            // buffer cache policy: sc0 | sc1
-template <int K>
+template <int K, int NT = kPollT>
 __device__ bool poll_pairs(const uint64_t *src, int n, uint32_t tag, float *dst, const PTMI_CONST StepArgs *a, int t) {
     t = opaque(t);
     const int np = n >> 1;
     bool valid[K], ok[K];
 #pragma unroll
-    for (int k = 0; k < K; k++) ok[k] = !(valid[k] = t + k * kPollT < np);
+    for (int k = 0; k < K; k++) ok[k] = !(valid[k] = t + k * NT < np);
     // every round loads all K pairs (past the vector: its last pair again),
     // so each register set is only ever written by a load.  The loads are
     // buffer loads with the system-scope cache bits (sc0 sc1: past this
@@ -222,7 +222,7 @@ __device__ bool poll_pairs(const uint64_t *src, int n, uint32_t tag, float *dst,
     // load is taken as loop-invariant.
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, np * 16, 0x00020000);
     auto pair = [&](int k) {
-        const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, opaque(16 * min(t + k * kPollT, np - 1)), 0, kSysScope);
+        const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, opaque(16 * min(t + k * NT, np - 1)), 0, kSysScope);
         u64x2 v;
         v.x = (uint64_t)w.x | ((uint64_t)w.y << 32);
         v.y = (uint64_t)w.z | ((uint64_t)w.w << 32);
@@ -243,7 +243,7 @@ __device__ bool poll_pairs(const uint64_t *src, int n, uint32_t tag, float *dst,
         for (int k = 0; k < K; k++) {
             if (ok[k]) continue;
             if ((uint32_t)(v[k].x >> 32) == tag && (uint32_t)(v[k].y >> 32) == tag) {
-                const int i = 2 * (t + k * kPollT);
+                const int i = 2 * (t + k * NT);
                 dst[i] = __uint_as_float((uint32_t)v[k].x);
                 dst[i + 1] = __uint_as_float((uint32_t)v[k].y);
                 ok[k] = true;
@@ -564,7 +564,7 @@ template <int ITD, int ITH, int GA>
 __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, int g1) {
     using Rg = Regs<ITD, ITH, GA>;
     // word pairs per polling thread of a dim-length and a hidden-length vector
-    constexpr int kPD = (ITD * 64 + kPollT - 1) / kPollT, kPH = (ITH * 128 + kPollT - 1) / kPollT;
+    constexpr int kPD = (ITD * 64 + kPollT - 1) / kPollT, kPH8 = (ITH * 128 + kT - 1) / kT;
     __shared__ Smem sm;
     Rg R;
     float pf_acc = 0.0f;                              // keeps prefetch loads alive
@@ -983,7 +983,10 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 const uint64_t *t_xa = a->t_xa + (long)l * D;
                 uint64_t *t_xb = a->t_xb + (long)l * D;
                 __syncthreads();
-                bool ok = tid >= kPollT || poll_pairs<kPH>(a->t_hb + (long)l * H, H, tk.tag, sm.xs, a, tid);
+                // every wave polls the hidden vector, the writer wave too
+                // (its hb stores of the stage before are acknowledged about
+                // as soon as the other waves' first round is back)
+                bool ok = poll_pairs<kPH8, kT>(a->t_hb + (long)l * H, H, tk.tag, sm.xs, a, tid);
                 if (ok && tid < kRowsH && (b >= blocks_w13 || !in(kStages * l + 3)))   // residual rows not taken in W13
                     ok = poll_words<1>(t_xa + b * kRowsH, min(kRowsH, D - b * kRowsH), tk.tag, sm.xres2, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
