@@ -264,12 +264,10 @@ __device__ bool poll_pairs(const uint64_t *src, int n, uint32_t tag, float *dst,
         if (__all(check(va))) return true;
         if (__builtin_amdgcn_s_memrealtime() - t0 > wait_ticks) return false;
         if ((round & 31) == 1 && __any(err_seen(a->ctl))) return false;
-        __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int k = 0; k < K; k++) va[k] = pair(k);
         asm volatile("" ::: "memory");
         if (__all(check(vb))) return true;
-        __builtin_amdgcn_s_sleep(1);
     }
 }
 
