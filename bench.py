@@ -329,7 +329,7 @@ def pmc_workload(pa, name, positions):
         m.reset_kv()
         for k in range(0, positions, 8):
             m.decode_async(int(prompt[0]), min(8, positions - k))
-            pa._ffi.check(L.ptmi_sync())
+            m.sync()
         m.close()
     os.environ.pop("PTMI_DECODE_STEP")
     calib_copy(pa)

@@ -185,8 +185,15 @@ int  ptmi_model_pos(const ptmi_model_t *m);
 int  ptmi_model_generate(ptmi_model_t *m, const int *prompt, int n_prompt,
                          int max_tokens, int stop_on_eos, int *out, int *n_out);
 /* Enqueue `n_steps` greedy decode steps from the current position without
- * waiting (benchmark form of the loop above; tokens stay on the device). */
+ * waiting (benchmark form of the loop above; tokens stay on the device).
+ * Its errors are deferred: a wait of the one-kernel step that timed out
+ * makes the rest of the submission do nothing, and is reported by the
+ * next ptmi_model_sync (or forward_step / generate) on this model.      */
 int  ptmi_model_decode_async(ptmi_model_t *m, int first_token, int n_steps);
+/* Wait for the model's enqueued work; PTMI_ERR_STATE when a one-kernel
+ * decode step of it timed out (the model stays usable afterwards).  No
+ * counterpart in the reference (its steps are synchronous, pt.c:267-271). */
+int  ptmi_model_sync(ptmi_model_t *m);
 /* Kernel timing: run `n_steps` decode steps eagerly (no graph) with HIP
  * events around every launch, from the current position.  role_ms[i] is
  * the summed kernel time and role_launches[i] the launch count of role i:
@@ -204,6 +211,23 @@ int  ptmi_model_profile(ptmi_model_t *m, int first_token, int n_steps,
  * classifier's and the final argmax's.  0 where the workgroup had no
  * part in a stage.  out holds n_wg * n_stamps words, workgroup-major.   */
 int  ptmi_model_step_stamps(ptmi_model_t *m, uint64_t *out, size_t n, int *n_stamps, int *n_wg);
+/* Which decode step pt_forward_step (pitorch/pt.c:267-271) runs on.  The
+ * one-kernel step needs a supported shape, one workgroup per compute unit
+ * all resident at once (its workgroups wait for each other's results, so
+ * one that cannot start would stall the others until their wait bound
+ * runs out), and a workgroup of its own for every attention unit.  Pure
+ * host arithmetic, no device call: cfg7 as ptmi_model_config, cus =
+ * compute units, per_cu = workgroups of the step kernel one compute unit
+ * holds at once (its occupancy).  *reason = 0 (one kernel: *grid
+ * workgroups, *units of them attention units), 1 (shape not supported) or
+ * 2 (grid or attention units do not fit): 1 and 2 take the multi-kernel
+ * step.  Returns a status.  No counterpart in the reference (its decode
+ * runs on one core).                                                    */
+int  ptmi_decode_step_plan(const int cfg7[7], int cus, int per_cu, int *reason, int *grid, int *units);
+/* The plan a model's creation took: as above, with the device's own
+ * compute units and occupancy; -1 when PTMI_DECODE_STEP=0 forced the
+ * multi-kernel step.                                                    */
+int  ptmi_model_step_plan(const ptmi_model_t *m);
 /* pt_train_step (pitorch/pt.c:339-364): zero grads, forward (loss),
  * backward, SGD on the device copy of the weights.                     */
 int  ptmi_model_train_step(ptmi_model_t *m, const int *tokens, int T, float lr,

@@ -11,6 +11,7 @@ is no CPU fallback: if the libraries are missing, loading raises.
 from ._ffi import (  # noqa: F401
     PtmiError,
     Model,
+    decode_step_plan,
     lib_dir,
     load_host,
     load_ptmi,

@@ -81,8 +81,11 @@ def load_ptmi():
     _sig(L, "ptmi_model_pos", i, [_vp])
     _sig(L, "ptmi_model_generate", i, [_vp, _c_int_p, i, i, i, _c_int_p, _c_int_p])
     _sig(L, "ptmi_model_decode_async", i, [_vp, i, i])
+    _sig(L, "ptmi_model_sync", i, [_vp])
     _sig(L, "ptmi_model_profile", i, [_vp, i, i, _c_float_p, _c_int_p])
     _sig(L, "ptmi_model_step_stamps", i, [_vp, ctypes.POINTER(ctypes.c_uint64), sz, _c_int_p, _c_int_p])
+    _sig(L, "ptmi_decode_step_plan", i, [_c_int_p, i, i, _c_int_p, _c_int_p, _c_int_p])
+    _sig(L, "ptmi_model_step_plan", i, [_vp])
     _sig(L, "ptmi_model_train_step", i, [_vp, _c_int_p, i, f, _c_float_p])
     _sig(L, "ptmi_model_train_step_trace", i,
          [_vp, _c_int_p, i, f, _c_float_p, ctypes.POINTER(Span), i, ctypes.POINTER(i)])
@@ -148,6 +151,17 @@ def synth_model(cfg, seed, std=0.02):
     if st:
         raise PtmiError(st, "pt_synth_model failed")
     return blob
+
+
+def decode_step_plan(cfg, cus, per_cu):
+    """ptmi_decode_step_plan for a 7-int model shape: (reason, grid, units);
+    reason 0 = one kernel, 1 = shape not supported, 2 = grid not resident."""
+    L = load_ptmi()
+    c = (ctypes.c_int * 7)(*cfg)
+    reason, grid, units = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    check(L.ptmi_decode_step_plan(c, int(cus), int(per_cu), ctypes.byref(reason), ctypes.byref(grid),
+                                  ctypes.byref(units)))
+    return reason.value, grid.value, units.value
 
 
 def seed_tokens(seed, n, vocab):
@@ -234,6 +248,10 @@ class Model:
     def decode_async(self, first_token, n_steps):
         check(self.L.ptmi_model_decode_async(self.h, int(first_token), int(n_steps)))
 
+    def sync(self):
+        """Wait for the model's enqueued steps; raises if one timed out."""
+        check(self.L.ptmi_model_sync(self.h))
+
     ROLES = ("qkv", "attention", "wo", "w13", "w2", "classifier", "argmax", "step")
 
     def profile(self, first_token, n_steps):
@@ -243,6 +261,11 @@ class Model:
         cnt = (ctypes.c_int * 8)()
         check(self.L.ptmi_model_profile(self.h, int(first_token), int(n_steps), ms, cnt))
         return {r: (ms[i], cnt[i]) for i, r in enumerate(self.ROLES)}
+
+    def step_plan(self):
+        """Why this model's decode step runs as one kernel (0) or not: 1 shape
+        not supported, 2 grid not resident at once, -1 multi-kernel forced."""
+        return self.L.ptmi_model_step_plan(self.h)
 
     def step_stamps(self):
         """Stage stamps of the last one-kernel decode step (model created

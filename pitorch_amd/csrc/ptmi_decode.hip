@@ -511,6 +511,16 @@ int ptmi_model_create(const void *blob, size_t bytes, int max_T, ptmi_model_t **
         release_blob(r);
         return st;
     }
+    // Grouped-query attention is refused: the reference's rope() rotates k
+    // over dim floats (pt_ops.c:33-49, called at llama2.c:147) while s->k
+    // holds kv_dim floats (llama2.c:81), so it has no defined result to
+    // match there, and no configuration uses it.
+    if (c.n_kv_heads != c.n_heads) {
+        st = set_error(PTMI_ERR_ARG, "n_kv_heads=%d != n_heads=%d: grouped-query attention is not supported",
+                       c.n_kv_heads, c.n_heads);
+        release_blob(r);
+        return st;
+    }
     if (max_T < 0 || max_T > c.seq_len) {
         st = set_error(PTMI_ERR_ARG, "max_T=%d outside [0, seq_len]", max_T);
         release_blob(r);
@@ -689,6 +699,15 @@ int ptmi_model_decode_async(ptmi_model_t *m, int first_token, int n_steps) {
     if ((st = launch_steps(m, s, n_steps))) return st;
     m->host_pos += n_steps;
     return PTMI_OK;
+}
+
+int ptmi_model_sync(ptmi_model_t *m) {
+    if (!m) return set_error(PTMI_ERR_ARG, "NULL model");
+    hipStream_t s = lib_stream();
+    DecodeCtl h;
+    PTMI_HIP(hipMemcpyAsync(&h, m->ctl, sizeof(h), hipMemcpyDeviceToHost, s));
+    PTMI_HIP(hipStreamSynchronize(s));
+    return check_step_error(m, h);
 }
 
 int ptmi_model_profile(ptmi_model_t *m, int first_token, int n_steps, float role_ms[8], int role_launches[8]) {

@@ -50,7 +50,7 @@ constexpr int kT = 512;                      // threads per workgroup
 constexpr int kW = kT / 64;                  // waves per workgroup
 constexpr int kRowsD = 2 * kW;               // rows per block, D-length rows (32 lanes per row)
 constexpr int kRowsH = kW;                   // rows per block, H-length rows (64 lanes per row)
-constexpr int kMaxChunk = 128;               // attention positions per unit
+constexpr int kAttRows = 128;                // attention positions per unit (at most)
 constexpr int kMaxChunks = 8;                // units per head
 constexpr int kWriter = kW - 1;              // the wave that issues the workgroup's global stores
 constexpr int kPollT = kWriter * 64;         // threads that poll (all other waves)
@@ -314,7 +314,8 @@ struct Smem {
     float qs[128], kp[128], vp[128];   // ATT: q, and k/v of this position
     float red[kW][128];
     float wred[kW];
-    float sc[kMaxChunk];               // ATT: scores -> weights
+    float sc[kAttRows];                // ATT: scores -> weights
+    float wred2[kW];                   // ATT: per-wave sums of e^(s - max)
     float cand[1024];                  // final argmax: (value, index) per workgroup
     float yout[kRowsD];                // results the writer wave stores
     uint64_t st[kStampSlots];          // stage stamps until the workgroup leaves
@@ -327,7 +328,7 @@ struct Smem {
 template <int ITD, int ITH, int GA>
 struct Regs {
     static constexpr int kRPW = 64 / GA;                 // K/V rows per wave load
-    static constexpr int kU = kMaxChunk / (kW * kRPW);   // loads per thread per chunk
+    static constexpr int kU = kAttRows / (kW * kRPW);    // loads per thread per chunk
     float4 wD[ITD], nw[ITD], wH[ITH];
     float4 kk[kU], vv[kU];
 };
@@ -731,12 +732,12 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
         if (in(kStages * l + 1)) {
             const PTMI_CONST StepArgs *a = fresh(ap);
             const int D = a->D, KV = a->KV, hd = a->hd, NH = a->NH, QR = D + 2 * KV;
-            const int n_units = NH * a->n_chunks, u0 = b - a->ubase;
-            for (int u = u0; u < n_units; u += nb) {
-                if (u < 0) continue;                          // uniform
+            // one unit per workgroup: the plan keeps every unit on a
+            // workgroup of its own (ubase + units <= workgroups), so no unit
+            // ever waits behind another unit of the same workgroup
+            const int u = b - a->ubase;
+            if (u >= 0 && u < NH * a->n_chunks && u / NH < tk.nact) {
                 const int h = u % NH, c = u / NH;
-                if (c >= tk.nact) continue;                   // uniform: chunk past pos
-                if (u != u0) load_k(a, R, tk, l, u);
                 const int t0 = c * a->chunk, t_end = min(t0 + a->chunk, tk.pos + 1), cnt = t_end - t0;
                 const bool has_pos = tk.pos < t_end;
                 const int kvh = h / a->kv_mul;
@@ -752,46 +753,80 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 }
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, sm.st, 3 + 10 * l);
+                // the V rows, first used after the softmax: issued once q, k
+                // and v are in (loaded with the K rows a stage ahead, they
+                // held back that wait, since a wave's loads complete in order)
                 load_v(a, R, tk, l, u);
+                // Every row pass of the unit at once, so the passes'
+                // dependency chains (dots, cross-lane sums) overlap instead
+                // of running one after another; rows past the unit's
+                // positions are computed and dropped.  Row pos is this
+                // token's: its key and value come from the polled k and v.
+                const float scale = a->att_scale;
                 const int slot = lane / GA, sub = lane % GA;
                 const bool has = sub < (hd >> 2);
                 const int sub_c = has ? sub : 0;
                 const float4 q4 = sel4(has, reinterpret_cast<const float4 *>(sm.qs)[sub_c]);
                 const float4 kp4 = reinterpret_cast<const float4 *>(sm.kp)[sub_c];
-                const float4 vp4 = reinterpret_cast<const float4 *>(sm.vp)[sub_c];
+                float spos = dot4(kp4, q4, 0.0f);             // q . k of row pos
+                float sv[Rg::kU];
+#pragma unroll
+                for (int q = 0; q < Rg::kU; q++) sv[q] = dot4(R.kk[q], q4, 0.0f);
+                // the row sums over each group of GA lanes, the passes interleaved
+                static_assert(GA == 16, "row sums over rows of 16 lanes");
+                spos = group_sum<GA>(spos);
+#pragma unroll
+                for (int q = 0; q < Rg::kU; q++) sv[q] += dpp_xor1(sv[q]);
+#pragma unroll
+                for (int q = 0; q < Rg::kU; q++) sv[q] += dpp_xor2(sv[q]);
+#pragma unroll
+                for (int q = 0; q < Rg::kU; q++) sv[q] += dpp_hmirror(sv[q]);
+#pragma unroll
+                for (int q = 0; q < Rg::kU; q++) sv[q] += dpp_mirror(sv[q]);
+                // scaled scores to LDS (one lane per row) and the wave's maximum
+                float mx = -INFINITY;
 #pragma unroll
                 for (int q = 0; q < Rg::kU; q++) {
                     const int t = t0 + q * (kW * Rg::kRPW) + wave * Rg::kRPW + slot;
-                    const float4 k4 = sel4(t < t_end, t == tk.pos ? kp4 : R.kk[q]);
-                    float sv = has ? dot4(k4, q4, 0.0f) : 0.0f;
-                    sv = group_sum<GA>(sv);
-                    if (sub == 0 && t < t_end) sm.sc[t - t0] = sv * a->att_scale;
+                    const float scv = (t == tk.pos ? spos : sv[q]) * scale;
+                    if (t < t_end) {
+                        mx = fmaxf(mx, scv);
+                        if (sub == 0) sm.sc[t - t0] = scv;
+                    }
                 }
-                __syncthreads();
-                // chunk softmax statistics: max, then e^(s - max) and their sum
-                float mx = -INFINITY;
-                for (int i = tid; i < cnt; i += kT) mx = fmaxf(mx, sm.sc[i]);
-                mx = group_max<64>(mx);
+                {
+                    const LanePair p16 = pl16(mx);
+                    mx = fmaxf(p16.lo, p16.hi);
+                    const LanePair p32 = pl32(mx);
+                    mx = fmaxf(p32.lo, p32.hi);
+                }
                 if (lane == 0) sm.wred[wave] = mx;
                 __syncthreads();
+                // chunk softmax statistics: the maximum, then e^(s - max)
+                // (one per thread) and their sum
                 mx = sm.wred[0];
 #pragma unroll
                 for (int w = 1; w < kW; w++) mx = fmaxf(mx, sm.wred[w]);
-                __syncthreads();
                 float sum = 0.0f;
-                for (int i = tid; i < cnt; i += kT) {
-                    const float e = d_expf(sm.sc[i] - mx);
-                    sm.sc[i] = e;
-                    sum += e;
+                if (tid < cnt) {
+                    const float e = d_expf(sm.sc[tid] - mx);
+                    sm.sc[tid] = e;
+                    sum = e;
                 }
                 sum = group_sum<64>(sum);
-                if (lane == 0) sm.wred[wave] = sum;
+                if (lane == 0) sm.wred2[wave] = sum;
                 __syncthreads();
+                // e . v over the unit's rows, every pass's weight read before use
+                float ew[Rg::kU];
+#pragma unroll
+                for (int q = 0; q < Rg::kU; q++)
+                    ew[q] = sm.sc[min(q * (kW * Rg::kRPW) + wave * Rg::kRPW + slot, kAttRows - 1)];
+                const float4 vp4 = reinterpret_cast<const float4 *>(sm.vp)[sub_c];
                 float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
                 for (int q = 0; q < Rg::kU; q++) {
                     const int t = t0 + q * (kW * Rg::kRPW) + wave * Rg::kRPW + slot;
-                    const float e = t < t_end ? sm.sc[t - t0] : 0.0f;
+                    const float e = t < t_end ? ew[q] : 0.0f;
                     const float4 v4 = sel4(t < t_end, t == tk.pos ? vp4 : R.vv[q]);
                     acc.x = fmaf(e, v4.x, acc.x);
                     acc.y = fmaf(e, v4.y, acc.y);
@@ -799,14 +834,10 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     acc.w = fmaf(e, v4.w, acc.w);
                 }
                 // sum over the wave's row slots (lanes with equal lane % GA)
-                auto slot_sum = [](float v) {
-                    if constexpr (GA <= 16) v = xsum16(v);
-                    return xsum32(v);
-                };
-                acc.x = slot_sum(acc.x);
-                acc.y = slot_sum(acc.y);
-                acc.z = slot_sum(acc.z);
-                acc.w = slot_sum(acc.w);
+                acc.x = xsum32(xsum16(acc.x));
+                acc.y = xsum32(xsum16(acc.y));
+                acc.z = xsum32(xsum16(acc.z));
+                acc.w = xsum32(xsum16(acc.w));
                 if (slot == 0 && has) {
                     sm.red[wave][4 * sub + 0] = acc.x;
                     sm.red[wave][4 * sub + 1] = acc.y;
@@ -824,7 +855,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 auto rec_l = [&]() {
                     float ls = 0.0f;
 #pragma unroll
-                    for (int w = 0; w < kW; w++) ls += sm.wred[w];
+                    for (int w = 0; w < kW; w++) ls += sm.wred2[w];
                     return ls;
                 };
                 uint64_t *head_part = a->t_part + ((long)l * NH + h) * a->n_chunks * (hd + 2);
@@ -1187,43 +1218,71 @@ const StepKernel kStepKernels[] = {
 
 }  // namespace
 
-// The persistent step for this model's shape, or null.
-static const StepKernel *pick_step(const Config &c, int *chunk, int *n_chunks) {
-    if (c.dim % 4 || c.hidden % 4 || c.head_dim % 4 || (c.dim & 1) || (c.kv_dim & 1)) return nullptr;
-    if (c.dim > 2048 || c.hidden > 2048 || c.head_dim > 128 || c.n_heads > 64) return nullptr;
+// The one-kernel step's launch plan for a model shape, on a device with
+// `cus` compute units of which each holds `per_cu` workgroups of the step
+// kernel at once (its occupancy).  The step runs one workgroup per compute
+// unit, all resident at the same time: the stages hand values to each
+// other through memory and wait for them, so a workgroup that has not
+// started would make its consumers wait until their bound runs out.  Each
+// attention unit needs a workgroup of its own (a head's chunk-0 unit waits
+// for the head's other units; queued behind another unit's wait on the
+// same workgroup, two merges could wait for each other).  Returns kPlanOk,
+// or why the multi-kernel step runs instead.
+enum { kPlanOk = 0, kPlanShape = 1, kPlanResident = 2 };
+struct StepPlan {
+    const StepKernel *k;
+    int chunk, n_chunks;   // attention positions per unit, units per head
+    int nb, units;         // workgroups, attention units
+};
+static int plan_step(const Config &c, int cus, int per_cu, StepPlan *p) {
+    *p = StepPlan{};
+    if (c.dim % 4 || c.hidden % 4 || c.head_dim % 4 || (c.dim & 1) || (c.kv_dim & 1)) return kPlanShape;
+    if (c.dim > 2048 || c.hidden > 2048 || c.head_dim > 128 || c.n_heads > 64) return kPlanShape;
     const int itd = (c.dim / 4 + 31) / 32, ith = (c.hidden / 4 + 63) / 64;
-    const int ga = 16;                                     // lanes per K/V row: head_dim <= 64
-    if (c.head_dim > 4 * ga) return nullptr;
-    // chunk: a multiple of the K/V rows one pass of the block covers, at
-    // most kMaxChunk positions, at most kMaxChunks per head
+    const int ga = 16;                                     // lanes per V row: head_dim <= 64
+    if (c.head_dim > 4 * ga || c.n_heads * c.head_dim != c.dim) return kPlanShape;
+    // chunk: a multiple of the K/V rows one pass of the workgroup covers,
+    // at most kAttRows positions, at most kMaxChunks per head
     const int gran = kW * (64 / ga);
     int ch = (c.seq_len + kMaxChunks - 1) / kMaxChunks;
     ch = (ch + gran - 1) / gran * gran;
-    if (ch > kMaxChunk) return nullptr;
+    if (ch > kAttRows) return kPlanShape;
     const int nc = (c.seq_len + ch - 1) / ch;
-    if (c.n_heads * c.head_dim != c.dim || nc * (c.head_dim + 2) > kPartLds) return nullptr;
+    if (nc * (c.head_dim + 2) > kPartLds) return kPlanShape;
     for (const StepKernel &k : kStepKernels)
         if (k.ga == ga && k.itd >= itd && k.ith >= ith && k.itd <= itd + 1 && k.ith <= ith + 2) {
-            *chunk = ch;
-            *n_chunks = nc;
-            return &k;
+            p->k = &k;
+            break;
         }
-    return nullptr;
+    if (!p->k) return kPlanShape;
+    p->chunk = ch;
+    p->n_chunks = nc;
+    p->nb = std::min(cus, 512);
+    p->units = c.n_heads * nc;
+    if (cus <= 0 || per_cu < 1 || p->units > p->nb) return kPlanResident;
+    return kPlanOk;
 }
 
 int decode_step_create(ptmi_model *m) {
     // PTMI_DECODE_STEP=1 / 0 forces this step / the captured multi-kernel
-    // step.  Unset: this step wherever its shape is supported (measured
-    // faster on stories15M, 42M and 110M).
+    // step.  Unset: this step wherever the plan allows it (measured faster
+    // on stories15M, 42M and 110M).
+    m->step_plan = -1;
     const char *env = getenv("PTMI_DECODE_STEP");
     const bool on = env && env[0] ? env[0] == '1' : true;
     if (!on) return PTMI_OK;
-    int chunk = 0, nc = 0;
-    if (!pick_step(m->c, &chunk, &nc)) return PTMI_OK;       // multi-kernel step
-    int dev = 0, cus = 0;
+    StepPlan plan;
+    if (plan_step(m->c, 1 << 20, 1, &plan) == kPlanShape) {
+        m->step_plan = kPlanShape;
+        return PTMI_OK;                                    // multi-kernel step
+    }
+    int dev = 0, cus = 0, per_cu = 0;
     PTMI_HIP(hipGetDevice(&dev));
     PTMI_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    if (cus <= 0) return PTMI_OK;
+    PTMI_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(plan.k->fn), kT, 0));
+    m->step_plan = plan_step(m->c, cus, per_cu, &plan);
+    if (m->step_plan != kPlanOk) return PTMI_OK;           // multi-kernel step
+    const int chunk = plan.chunk, nc = plan.n_chunks;
     const Config &c = m->c;
     const long L = c.n_layers, D = c.dim, H = c.hidden, KV = c.kv_dim, NH = c.n_heads, hd = c.head_dim;
     const int nb = std::min(cus, 512);
@@ -1267,6 +1326,7 @@ int decode_step_create(ptmi_model *m) {
             a.ubase = NH * nc <= a.qbase ? 0 : (ub_on && a.qbase + blocks_qkv + NH * nc <= nb ? a.qbase + blocks_qkv : 0);
         else
             a.ubase = (ub_on && blocks_qkv + NH * nc <= nb) ? blocks_qkv : 0;
+        // (ubase + units <= nb in every case: the plan has units <= nb)
     }
     a.att_scale = host_att_scale(c.head_dim);
     a.kc = m->kc; a.vc = m->vc; a.logits = m->logits; a.ctl = m->ctl;
@@ -1303,6 +1363,7 @@ int decode_step_create(ptmi_model *m) {
     m->step_mem = reinterpret_cast<uint64_t *>(mem);
     m->step_args = mem + args_off;
     m->step_nb = nb;
+    m->step_fn = reinterpret_cast<const void *>(plan.k->fn);
     m->step_chunk = chunk;
     m->step_chunks = nc;
     m->step_stamps = a.stamps;
@@ -1328,18 +1389,17 @@ void decode_step_destroy(ptmi_model *m) {
     if (m->step_mem) (void)hipFree(m->step_mem);
     m->step_mem = nullptr;
     m->step_args = nullptr;
+    m->step_fn = nullptr;
 }
 
 int decode_step_windows(const ptmi_model *m) { return (int)m->step_cuts.size() - 1; }
 
 int launch_decode_step(ptmi_model *m, int w, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
-    int chunk = 0, nc = 0;
-    const StepKernel *k = pick_step(m->c, &chunk, &nc);
-    if (!k || !m->step_args || chunk != m->step_chunk || nc != m->step_chunks)
-        return set_error(PTMI_ERR_STATE, "decode step kernel not set up for this model");
+    if (!m->step_fn || !m->step_args) return set_error(PTMI_ERR_STATE, "decode step kernel not set up for this model");
     if (w < 0 || w >= decode_step_windows(m)) return set_error(PTMI_ERR_ARG, "decode step window %d out of range", w);
     const StepArgs *args = reinterpret_cast<const StepArgs *>(m->step_args);
-    launch_k(k->fn, dim3(m->step_nb), dim3(kT), 0, s, e0, e1, args, m->step_cuts[w], m->step_cuts[w + 1]);
+    const StepFn fn = reinterpret_cast<StepFn>(const_cast<void *>(m->step_fn));
+    launch_k(fn, dim3(m->step_nb), dim3(kT), 0, s, e0, e1, args, m->step_cuts[w], m->step_cuts[w + 1]);
     PTMI_HIP(hipGetLastError());
     return PTMI_OK;
 }
@@ -1347,6 +1407,25 @@ int launch_decode_step(ptmi_model *m, int w, hipStream_t s, hipEvent_t e0, hipEv
 }  // namespace ptmi
 
 using namespace ptmi;
+
+extern "C" int ptmi_decode_step_plan(const int cfg7[7], int cus, int per_cu, int *reason, int *grid, int *units) {
+    if (!cfg7 || !reason) return set_error(PTMI_ERR_ARG, "ptmi_decode_step_plan: NULL argument");
+    Config c{};
+    c.dim = cfg7[0]; c.hidden = cfg7[1]; c.n_layers = cfg7[2]; c.n_heads = cfg7[3]; c.n_kv_heads = cfg7[4];
+    c.vocab = cfg7[5]; c.seq_len = cfg7[6];
+    if (c.dim <= 0 || c.hidden <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.vocab <= 0 ||
+        c.seq_len <= 0 || c.dim % c.n_heads || c.n_heads % c.n_kv_heads)
+        return set_error(PTMI_ERR_ARG, "ptmi_decode_step_plan: bad shape");
+    c.head_dim = c.dim / c.n_heads;
+    c.kv_dim = c.n_kv_heads * c.head_dim;
+    StepPlan p;
+    *reason = plan_step(c, cus, per_cu, &p);
+    if (grid) *grid = *reason == kPlanShape ? 0 : p.nb;
+    if (units) *units = *reason == kPlanShape ? 0 : p.units;
+    return PTMI_OK;
+}
+
+extern "C" int ptmi_model_step_plan(const ptmi_model_t *m) { return m ? m->step_plan : -1; }
 
 extern "C" int ptmi_model_step_stamps(ptmi_model_t *m, uint64_t *out, size_t n, int *n_stamps, int *n_wg) {
     if (!m || !n_stamps || !n_wg) return set_error(PTMI_ERR_ARG, "NULL argument");

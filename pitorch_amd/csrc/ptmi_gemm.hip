@@ -925,7 +925,10 @@ int ptmi_gemm_dev_noalloc(int op, const float *dA, long lda, const float *dB, lo
                          "ptmi_gemm_dev_noalloc: %dx%dx%d needs %zu floats of split-K partials; the fixed scratch "
                          "holds %zu",
                          M, N, K, need, kNoAllocScratchFloats);
-    return launch_gemm(op, dA, lda, dB, ldb, dC, ldc, M, N, K, accumulate, ws, kNoAllocScratchFloats,
+    // the split is chosen from ptmi_gemm_dev's workspace size, not the
+    // scratch's, so that both take the same number of splits
+    return launch_gemm(op, dA, lda, dB, ldb, dC, ldc, M, N, K, accumulate, ws,
+                       std::min(kNoAllocScratchFloats, gemm_dev_ws_floats(M, N)),
                        stream ? (hipStream_t)stream : lib_stream());
 }
 

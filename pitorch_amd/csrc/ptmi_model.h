@@ -60,7 +60,9 @@ struct ptmi_model {
     // one-kernel decode step (null step_mem: the multi-kernel step)
     uint64_t *step_mem = nullptr;        // its tagged exchange buffers
     void *step_args = nullptr;           // its argument block (device memory)
-    int step_nb = 0;                     // its workgroups
+    int step_nb = 0;                     // its workgroups (matvec and attention)
+    const void *step_fn = nullptr;       // its kernel
+    int step_plan = -1;                  // why it runs or not (plan_step: 0 runs, 1 shape, 2 residency)
     int step_chunk = 0, step_chunks = 0; // attention positions per unit, units per head
     uint64_t *step_stamps = nullptr;     // stage stamps (PTMI_STEP_STAMPS=1)
     int step_n_stamps = 0;

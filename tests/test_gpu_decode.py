@@ -309,9 +309,91 @@ def test_one_kernel_step_timeout_is_reported(monkeypatch):
         assert "timed out" in str(e.value)
     with pytest.raises(pa.PtmiError):
         m.generate(np.array([1, 2, 3], np.int32), 8, stop_on_eos=False)
+    # decode_async defers its errors to the next synchronising call
+    m.reset_kv()
+    m.decode_async(1, 4)
+    with pytest.raises(pa.PtmiError) as e:
+        m.sync()
+    assert "timed out" in str(e.value)
+    m.sync()                                        # reported once, then clear
     m.close()
     monkeypatch.delenv("PTMI_STEP_WAIT_TICKS")
     fx = fixture("stories15M")
     m = pa.Model(model_for("stories15M"))
     assert greedy_tokens(m.forward_step, fx["prompt"], 16) == fx["tokens"][:16]
+    m.close()
+
+
+def _oracle_decode(blob, n, prompt, paths=("0", "1")):
+    """Greedy decode of n positions on each decode path against the oracle:
+    tokens identical, logits within 1e-5 of max |logit| at every position.
+    Returns the models' step plans."""
+    plans = []
+    for path in paths:
+        os.environ["PTMI_DECODE_STEP"] = path
+        try:
+            m = pa.Model(blob)
+        finally:
+            os.environ.pop("PTMI_DECODE_STEP")
+        plans.append(m.step_plan())
+        om = OracleModel(blob.copy())
+        tok = prompt[0]
+        for pos in range(n):
+            a, b = m.forward_step(tok), om.forward_step(tok)
+            lg, ref_lg = m.logits(), om.logits()
+            err = np.max(np.abs(lg - ref_lg)) / np.max(np.abs(ref_lg))
+            assert err < 1e-5 and a == b, (path, pos, err, a, b)
+            tok = prompt[pos + 1] if pos + 1 < len(prompt) else a
+        m.close()
+        om.close()
+    return plans
+
+
+def test_step_kernel_for_dim_256_matches_oracle():
+    """dim 256 with head_dim 64 (4 heads), hidden 512, 64 positions: the
+    shape that selects the one-kernel step's smallest multi-chunk
+    instantiation (2 float4 per lane of a dim row, 2 of a hidden row, 2
+    attention units of 32 positions per head).  Both decode paths, every
+    position, against the oracle."""
+    cfg = (256, 512, 2, 4, 4, 512, 64)
+    blob = pa.synth_model(cfg, 7)
+    prompt = [int(t) for t in pa.seed_tokens(5, 8, cfg[5])]
+    assert _oracle_decode(blob, 64, prompt) == [-1, 0]
+
+
+def test_wrapped_attention_units_take_the_multi_kernel_step():
+    """48 heads of 16 over 1024 positions make 384 attention units, more
+    than the 256 workgroups of the one-kernel step: the plan refuses it (a
+    head's chunk-0 unit could wait behind another merge on its own
+    workgroup), and the model decodes on the multi-kernel step, matching
+    the oracle past position 896 where all eight chunks are active."""
+    cfg = (768, 2048, 1, 48, 48, 512, 1024)
+    blob = pa.synth_model(cfg, 9)
+    prompt = [int(t) for t in pa.seed_tokens(6, 8, cfg[5])]
+    assert pa.decode_step_plan(cfg, 256, 1)[0] == 2
+    assert _oracle_decode(blob, 920, prompt, paths=("1",)) == [2]
+
+
+def test_grouped_query_attention_is_refused():
+    """n_kv_heads < n_heads is refused at model creation: the reference's
+    rope() rotates k over dim floats while s->k holds kv_dim
+    (pitorch/ops/core/pt_ops.c:33-49, pitorch/model/llama2.c:81,147), so
+    it has no defined result to match."""
+    blob = pa.synth_model((256, 512, 1, 4, 2, 512, 64), 3)
+    with pytest.raises(pa.PtmiError) as e:
+        pa.Model(blob)
+    assert "grouped-query" in str(e.value)
+
+
+def test_step_plan_of_the_stories_models(monkeypatch):
+    """On the MI355X every stories model runs the one-kernel step (plan 0);
+    PTMI_DECODE_STEP=0 forces the multi-kernel step (plan -1)."""
+    monkeypatch.delenv("PTMI_DECODE_STEP", raising=False)
+    for name in pa.STORIES:
+        m = pa.Model(model_for(name))
+        assert m.step_plan() == 0, name
+        m.close()
+    monkeypatch.setenv("PTMI_DECODE_STEP", "0")
+    m = pa.Model(model_for("stories15M"))
+    assert m.step_plan() == -1
     m.close()

@@ -39,8 +39,11 @@ def operands(op, M, N, K, seed, integer):
 
 # (op, M, N, K): split K over 64x64 tiles (the 15M classifier's dX: 52
 # splits), split K over 32x32 tiles, and unsplit; each followed by a
-# smaller GEMM of the same form.
+# smaller GEMM of the same form.  64x64x32768 is one tile whose split is
+# bounded by ptmi_gemm_dev's workspace (64 partials of 64x64), not by the
+# larger fixed scratch.
 CASES = [((0, 255, 288, 32000), (0, 100, 96, 8192)),
+         ((0, 64, 64, 32768), (0, 32, 48, 20000)),
          ((0, 100, 70, 3001), (0, 40, 33, 1500)),
          ((1, 288, 768, 255), (1, 64, 96, 100)),
          ((2, 256, 1536, 288), (2, 17, 50, 64))]
