@@ -28,23 +28,46 @@ HBM_PEAK_GBS = 8000.0
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_stories110M_hbm_traffic.md")
 
 
-def committed_traffic(role, workload_tag):
-    """HBM bytes per launch of decode kernel `role`, measured by the two
-    rocprofv3 FETCH_SIZE / WRITE_SIZE passes whose summary is committed in
-    TRAFFIC_PROFILE (rows `| traffic | <tag> | <role> | ... | <bytes> |`),
-    or None when that file holds no row for this role and workload."""
+# The sources of the decode kernels: a traffic figure measured on other
+# sources says nothing about this build.
+DECODE_SOURCES = ["pitorch_amd/csrc/ptmi_decode_step.hip", "pitorch_amd/csrc/ptmi_decode.hip",
+                  "pitorch_amd/csrc/ptmi_matvec.hip", "pitorch_amd/csrc/ptmi_core.hip",
+                  "pitorch_amd/csrc/ptmi_internal.h", "pitorch_amd/csrc/ptmi_model.h"]
+
+
+def decode_sources_hash(root=ROOT):
+    """First 16 hex digits of the SHA-256 over the decode kernels' sources,
+    in DECODE_SOURCES order."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in DECODE_SOURCES:
+        with open(os.path.join(root, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def committed_traffic(role, workload_tag, path=TRAFFIC_PROFILE, sources=None):
+    """(HBM bytes per launch of decode kernel `role`, note): the figure the
+    two rocprofv3 FETCH_SIZE / WRITE_SIZE passes committed in `path` measured
+    (rows `| traffic | <tag> | <role> | <sources hash> | ... | <bytes> |`),
+    when the row was measured on the decode sources of this build (hash
+    `sources`, default: this tree's); otherwise None and why."""
+    sources = sources or decode_sources_hash()
     try:
-        lines = open(TRAFFIC_PROFILE).read().splitlines()
+        lines = open(path).read().splitlines()
     except OSError:
-        return None
+        return None, f"no traffic profile at {os.path.relpath(path, ROOT)}"
     for ln in lines:
         cells = [c.strip() for c in ln.strip().strip("|").split("|")]
-        if len(cells) >= 4 and cells[0] == "traffic" and cells[1] == workload_tag and cells[2] == role:
+        if len(cells) >= 5 and cells[0] == "traffic" and cells[1] == workload_tag and cells[2] == role:
+            if cells[3].strip("`") != sources:
+                return None, (f"the committed traffic row was measured on decode sources {cells[3].strip('`')}, "
+                              f"this build's are {sources}")
             try:
-                return int(cells[-1])
+                return int(cells[-1]), None
             except ValueError:
-                return None
-    return None
+                return None, "unreadable traffic row"
+    return None, f"no traffic row for {workload_tag} {role}"
 
 
 def matvec_bytes(d, n):
@@ -192,11 +215,13 @@ def cpu_model():
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(blob, prompt, budget_s=15.0, max_tokens=512):
+def cpu_baseline(blob, prompt, positions):
     """The reference's own host decode (oracle/_ref: pitorch/pt.c
     pt_forward_step with smatvec_cpu, built -O2 -ffp-contract=off), one
-    thread pinned to one core, on the same 110M blob and prompt: positions
-    0..n-1 of the same greedy decode, as many as fit the time budget."""
+    thread pinned to one core, on the same 110M blob and prompt: the same
+    greedy decode of positions 0..positions-1 as the GPU figure (~1 minute
+    on one core; the cost of a token grows with its position, so a shorter
+    sample would overstate the CPU)."""
     from tests._oracle import P, ref
     R = ref()
     if R is None:
@@ -206,15 +231,15 @@ def cpu_baseline(blob, prompt, budget_s=15.0, max_tokens=512):
     n = 0
     with pinned_to_one_core() as pin:
         t0 = time.perf_counter()
-        while n < max_tokens and time.perf_counter() - t0 < budget_s:
+        while n < positions:
             nxt = R.ref_forward_step(ctx, tok)
             tok = int(prompt[n + 1]) if n + 1 < len(prompt) else nxt
             n += 1
         dt = time.perf_counter() - t0
     R.ref_ctx_free(ctx)
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": 1, "kind": "reference",
-            "sample": f"positions 0..{n - 1} of the stories110M greedy decode (same blob and prompt; the "
-                      f"GPU figure covers 0..1023), 1 thread pinned to core {pin.core} of {cpu_model()}, "
+            "sample": f"positions 0..{n - 1} of the stories110M greedy decode, the GPU figure's workload (same "
+                      f"blob and prompt), {dt:.1f} s, 1 thread pinned to core {pin.core} of {cpu_model()}, "
                       f"host nproc={os.cpu_count()}"}
 
 
@@ -572,12 +597,16 @@ def main():
         print(f"[bench] train {json.dumps({k: v for k, v in train.items() if k != 'by_shape'})}", file=sys.stderr,
               flush=True)
     blob = pa.synth_model(cfg, pa.SEED_MODEL[name])
-    cpu = None if args.no_cpu else cpu_baseline(blob, prompt)
+    cpu = None if args.no_cpu else cpu_baseline(blob, prompt, S)
     del blob
     cpu_more = None if args.no_cpu else cpu_extra()
     # measured HBM bytes per launch of the dominant kernel (fetch + write,
-    # counter-calibrated), from the committed passes over all S positions
-    traffic = committed_traffic(dominant, name) if n_prof == S else None
+    # counter-calibrated), from the committed passes over all S positions,
+    # when they were measured on this build's decode sources
+    if n_prof == S:
+        traffic, traffic_note = committed_traffic(dominant, name)
+    else:
+        traffic, traffic_note = None, f"traffic was measured over positions 0..{S - 1}, this run profiles {n_prof}"
 
     line = {
         "metric": "decode tok/s + matvec HBM GB/s (% peak), stories110M-shape fp32, 1 GPU",
@@ -599,7 +628,9 @@ def main():
                    "positions": f"0..{S - 1}", "tokens_timed": n_tok, "batch": 1},
         "roofline": {"bound": "hbm", "kernel": f"decode[{dominant}]", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "bytes_per_launch": dom["bytes_per_launch"], "avg_us": dom["avg_us"]},
+                     "traffic": traffic, "traffic_sources": decode_sources_hash(),
+                     **({"traffic_note": traffic_note} if traffic_note else {}),
+                     "bytes_per_launch": dom["bytes_per_launch"], "avg_us": dom["avg_us"]},
         "step_roofline": {"bytes_per_token": int(step_bytes), "achieved_GBps": round(step_gbs, 1),
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4), "kernel_ms_per_token": round(kernel_ms, 4)},
         "matvec_sweep": sweep,
