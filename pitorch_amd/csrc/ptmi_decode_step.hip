@@ -894,10 +894,13 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     // record in the writer wave's registers, the others'
                     // polled into LDS, then w_c = e^(m_c - M) / sum_c' l_c'
                     // e^(m_c' - M) and out = sum_c w_c o_c, published for
-                    // the WO stage.  The writer wave does the merge alone,
-                    // lane c holding chunk c's statistics, so no thread
-                    // walks the records serially through LDS; the sums keep
-                    // the chunk order of one fmaf chain each.
+                    // the WO stage.  The writer wave does the merge alone:
+                    // lane c (< 8) holds chunk c's statistics, M and the sum
+                    // over c come from three cross-lane steps within the
+                    // lane's 8-lane group, and the output sums keep the chunk
+                    // order.  One chunk is o / l, which is what the general
+                    // arithmetic gives there (M = m, e^0 = 1).
+                    static_assert(kMaxChunks == 8, "chunk statistics reduce over 8-lane groups");
                     const int nact = tk.nact, nother = nact - 1;
                     float o0 = 0.0f, m0 = 0.0f, l0 = 0.0f;
                     if (wave == kWriter) {
@@ -910,22 +913,27 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                         ok = poll_pairs<1>(head_part + (hd + 2), nother * (hd + 2), tk.tag, sm.part + (hd + 2), a, tid);
                     if (!block_ok(ok, &sm.fail, a->ctl)) return;
                     if (wave == kWriter) {
-                        auto rl = [](float x, int k) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k)); };
-                        const float *pc = sm.part + min(lane, kMaxChunks - 1) * (hd + 2);
-                        const bool act = lane < nact;
-                        const float mc = lane == 0 ? m0 : pc[hd], lc = lane == 0 ? l0 : pc[hd + 1];
-                        const float M = group_max<64>(act ? mc : -INFINITY);
-                        const float f = act ? d_expf(mc - M) : 0.0f;
-                        float Ls = 0.0f;
-#pragma unroll
-                        for (int k = 0; k < kMaxChunks; k++) Ls = k < nact ? fmaf(rl(lc, k), rl(f, k), Ls) : Ls;
-                        const float inv = 1.0f / Ls;
-                        const int d = min(lane, hd - 1);
-                        float v = 0.0f;
-#pragma unroll
-                        for (int k = 0; k < kMaxChunks; k++) {
-                            const float ok_ = k == 0 ? o0 : sm.part[k * (hd + 2) + d];
-                            v = k < nact ? fmaf(ok_, rl(f, k) * inv, v) : v;
+                        float v;
+                        if (nact == 1) {
+                            v = o0 * (1.0f / l0);
+                        } else {
+                            const float *pc = sm.part + (lane & 7) * (hd + 2);
+                            const bool act = (lane & 7) < nact;
+                            const float mc = (lane & 7) == 0 ? m0 : pc[hd], lc = (lane & 7) == 0 ? l0 : pc[hd + 1];
+                            float M = act ? mc : -INFINITY;
+                            M = fmaxf(M, dpp_xor1(M));
+                            M = fmaxf(M, dpp_xor2(M));
+                            M = fmaxf(M, dpp_hmirror(M));
+                            const float f = act ? d_expf(mc - M) : 0.0f;
+                            float Ls = lc * f;
+                            Ls += dpp_xor1(Ls);
+                            Ls += dpp_xor2(Ls);
+                            Ls += dpp_hmirror(Ls);
+                            const float w = f * (1.0f / Ls);
+                            const int d = min(lane, hd - 1);
+                            v = o0 * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 0));
+                            for (int k = 1; k < nact; k++)
+                                v = fmaf(sm.part[k * (hd + 2) + d], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), k)), v);
                         }
                         if (lane < hd) tstore(a->t_att + (long)l * D + h * hd + lane, v, tk.tag);
                     }
