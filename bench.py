@@ -26,6 +26,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_stories110M_hbm_traffic.md")
+TRAIN_PROFILE = os.path.join(ROOT, "profiles", "train_stories15M_T256_kernel_stats.md")
 
 
 # The sources of the decode kernels: a traffic figure measured on other
@@ -35,15 +36,48 @@ DECODE_SOURCES = ["pitorch_amd/csrc/ptmi_decode_step.hip", "pitorch_amd/csrc/ptm
                   "pitorch_amd/csrc/ptmi_internal.h", "pitorch_amd/csrc/ptmi_model.h"]
 
 
-def decode_sources_hash(root=ROOT):
-    """First 16 hex digits of the SHA-256 over the decode kernels' sources,
-    in DECODE_SOURCES order."""
+def sources_hash(files, root=ROOT):
+    """First 16 hex digits of the SHA-256 over the given sources, in order."""
     import hashlib
     h = hashlib.sha256()
-    for rel in DECODE_SOURCES:
+    for rel in files:
         with open(os.path.join(root, rel), "rb") as f:
             h.update(f.read())
     return h.hexdigest()[:16]
+
+
+def decode_sources_hash(root=ROOT):
+    """sources_hash of the decode kernels' sources (DECODE_SOURCES)."""
+    return sources_hash(DECODE_SOURCES, root)
+
+
+# The sources of the training step's kernels (for the in-step kernel times
+# a committed kernel trace measured).
+TRAIN_SOURCES = ["pitorch_amd/csrc/ptmi_train.hip", "pitorch_amd/csrc/ptmi_gemm.hip",
+                 "pitorch_amd/csrc/ptmi_internal.h", "pitorch_amd/csrc/ptmi_model.h"]
+
+
+def train_sources_hash(root=ROOT):
+    """sources_hash of the training kernels' sources (TRAIN_SOURCES)."""
+    return sources_hash(TRAIN_SOURCES, root)
+
+
+def _profile_row(kind, tag, role, path, sources):
+    """(cells, note) of the committed profile row `| kind | tag | role |
+    <sources hash> | ... |` in `path`: the row's cells when it was measured
+    on the sources with hash `sources`; otherwise None and why."""
+    try:
+        lines = open(path).read().splitlines()
+    except OSError:
+        return None, f"no profile at {os.path.relpath(path, ROOT)}"
+    for ln in lines:
+        cells = [c.strip() for c in ln.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] == kind and cells[1] == tag and cells[2] == role:
+            if cells[3].strip("`") != sources:
+                return None, (f"the committed {kind} row was measured on sources {cells[3].strip('`')}, "
+                              f"this build's are {sources}")
+            return cells, None
+    return None, f"no {kind} row for {tag} {role}"
 
 
 def committed_traffic(role, workload_tag, path=TRAFFIC_PROFILE, sources=None):
@@ -52,22 +86,29 @@ def committed_traffic(role, workload_tag, path=TRAFFIC_PROFILE, sources=None):
     (rows `| traffic | <tag> | <role> | <sources hash> | ... | <bytes> |`),
     when the row was measured on the decode sources of this build (hash
     `sources`, default: this tree's); otherwise None and why."""
-    sources = sources or decode_sources_hash()
+    cells, note = _profile_row("traffic", workload_tag, role, path, sources or decode_sources_hash())
+    if cells is None:
+        return None, note
     try:
-        lines = open(path).read().splitlines()
-    except OSError:
-        return None, f"no traffic profile at {os.path.relpath(path, ROOT)}"
-    for ln in lines:
-        cells = [c.strip() for c in ln.strip().strip("|").split("|")]
-        if len(cells) >= 5 and cells[0] == "traffic" and cells[1] == workload_tag and cells[2] == role:
-            if cells[3].strip("`") != sources:
-                return None, (f"the committed traffic row was measured on decode sources {cells[3].strip('`')}, "
-                              f"this build's are {sources}")
-            try:
-                return int(cells[-1]), None
-            except ValueError:
-                return None, "unreadable traffic row"
-    return None, f"no traffic row for {workload_tag} {role}"
+        return int(cells[-1]), None
+    except ValueError:
+        return None, "unreadable traffic row"
+
+
+def committed_in_step(path=TRAIN_PROFILE, sources=None):
+    """({"steps", "gemm_ms", "kernels_ms"}, note): the training step's summed
+    kernel durations per step, of its GEMM kernels and of all its kernels,
+    from the eager kernel trace committed in `path` (row `| in-step |
+    stories15M T256 | step | <sources hash> | <steps> | <GEMM µs> | <all µs>
+    |`), when it was measured on this build's training sources; otherwise
+    None and why."""
+    cells, note = _profile_row("in-step", "stories15M T256", "step", path, sources or train_sources_hash())
+    if cells is None:
+        return None, note
+    try:
+        return {"steps": int(cells[4]), "gemm_ms": float(cells[5]) / 1e3, "kernels_ms": float(cells[6]) / 1e3}, None
+    except (ValueError, IndexError):
+        return None, "unreadable in-step row"
 
 
 def matvec_bytes(d, n):
@@ -319,11 +360,26 @@ def bench_train(pa, reps=20):
     for a in (A, B, C):
         a.free()
     tflops = total_flop / (total_ms * 1e-3) / 1e12
-    return {"workload": "stories15M training step, T=256, lr=1e-3 (config 5)", "ms_per_step": round(step_ms, 3),
-            "losses_first_last": [round(losses[0], 6), round(losses[-1], 6)],
-            "gemm_gflop_per_step": round(total_flop / 1e9, 3), "gemm_ms_per_step": round(total_ms, 4),
-            "gemm_tflops": round(tflops, 2), "gemm_frac_fp32_mfma": round(tflops / MFMA_FP32_PEAK_TFLOPS, 4),
-            "by_shape": rows}
+    out = {"workload": "stories15M training step, T=256, lr=1e-3 (config 5)", "ms_per_step": round(step_ms, 3),
+           "losses_first_last": [round(losses[0], 6), round(losses[-1], 6)],
+           "losses_steps": "steps 4 and 21 of 21 consecutive SGD steps on one token sequence "
+                           "(the first 3 untimed; the timed ms_per_step covers steps 4..21)",
+           "gemm_gflop_per_step": round(total_flop / 1e9, 3), "gemm_ms_per_step": round(total_ms, 4),
+           "gemm_ms_per_step_basis": "sum over the step's GEMM shapes of isolated graph-replayed launches",
+           "gemm_tflops": round(tflops, 2), "gemm_frac_fp32_mfma": round(tflops / MFMA_FP32_PEAK_TFLOPS, 4)}
+    # the same GEMMs inside the step: summed kernel durations per step from
+    # the committed eager kernel trace (bench.py --train-trace-workload)
+    ins, note = committed_in_step()
+    out["in_step"] = (None if ins is None else
+                      {"gemm_ms": round(ins["gemm_ms"], 4), "kernels_ms": round(ins["kernels_ms"], 4),
+                       "gemm_tflops": round(total_flop / ins["gemm_ms"] / 1e9, 2),
+                       "gemm_frac_fp32_mfma": round(total_flop / ins["gemm_ms"] / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
+                       "basis": f"rocprofv3 kernel trace of {ins['steps']} eager steps "
+                                f"({os.path.relpath(TRAIN_PROFILE, ROOT)}, sources {train_sources_hash()})"})
+    if note:
+        out["in_step_note"] = note
+    out["by_shape"] = rows
+    return out
 
 
 def calib_copy(pa, mb=256):
@@ -436,6 +492,21 @@ def step_stamps(pa, name, at, out=""):
     m.close()
 
 
+def train_trace_workload(pa, steps):
+    """Kernel-trace workload of the training step, no timing: `steps`
+    training steps of stories15M at T=256 enqueued eagerly (no graph), each
+    waited for (the step returns its loss)."""
+    os.environ["PTMI_TRAIN_EAGER"] = "1"
+    name, T, lr = "stories15M", 256, 1e-3
+    cfg = pa.STORIES[name]
+    m = pa.Model(pa.synth_model(cfg, pa.SEED_MODEL[name]), max_T=T)
+    tokens = pa.seed_tokens(pa.SEED_TRAIN, T, cfg[5])
+    for i in range(steps):
+        m.train_step(tokens, lr)
+    m.close()
+    print(f"[bench] train trace workload: {steps} eager stories15M T=256 steps", file=sys.stderr)
+
+
 def pmc_gemm(pa, reps):
     """Every training GEMM shape of stories15M at T=256, `reps` launches
     each, enqueued directly (no graph) with one synchronisation per shape:
@@ -479,6 +550,9 @@ def main():
                     help="counter-profile workload, no timing: POSITIONS decode steps of the --config model "
                          "enqueued without graphs, 8 at a time (rocprofv3 --pmc faults on its host side with "
                          "thousands of dispatches in flight), then the 256 MiB calibration copy")
+    ap.add_argument("--train-trace-workload", type=int, default=0, metavar="STEPS",
+                    help="kernel-trace workload, no timing: STEPS eager training steps (no graph launches), "
+                         "print nothing on stdout")
     ap.add_argument("--stamps-out", type=str, default="", metavar="NPZ",
                     help="with --step-stamps: also save every workgroup's raw stamps")
     ap.add_argument("--step-stamps", type=str, default="", metavar="POSITIONS",
@@ -502,6 +576,9 @@ def main():
         return
     if args.pmc_workload:
         pmc_workload(pa, args.config, args.pmc_workload)
+        return
+    if args.train_trace_workload:
+        train_trace_workload(pa, args.train_trace_workload)
         return
     if args.step_stamps:
         step_stamps(pa, args.config, sorted(int(p) for p in args.step_stamps.split(",")), args.stamps_out)

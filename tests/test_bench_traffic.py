@@ -1,7 +1,8 @@
-"""bench.py's roofline.traffic provenance (CPU only): the committed
-FETCH_SIZE / WRITE_SIZE figure is used only when the profile row was
-measured on this build's decode sources; otherwise the field is null and
-the line says why."""
+"""Provenance of the committed profile figures bench.py reports (CPU only):
+roofline.traffic (the FETCH_SIZE / WRITE_SIZE figure) and the training
+leg's in-step kernel times are used only when the profile row was measured
+on this build's sources (decode kernels, training kernels); otherwise the
+field is null and the line says why."""
 import os
 import sys
 
@@ -36,3 +37,28 @@ def test_missing_row_or_file_gives_null(tmp_path):
     p.write_text(ROW.format(h=bench.decode_sources_hash()))
     assert bench.committed_traffic("wo", "stories110M", path=str(p))[0] is None
     assert bench.committed_traffic("step", "stories110M", path=str(tmp_path / "none.md"))[0] is None
+
+
+# The training step's in-step kernel times follow the same rule, keyed by
+# the training kernels' sources.
+IN_STEP = "| in-step | stories15M T256 | step | `{h}` | 18 | 612.5 | 802.4 |\n"
+
+
+def test_in_step_times_need_the_training_sources():
+    assert "pitorch_amd/csrc/ptmi_train.hip" in bench.TRAIN_SOURCES
+    assert "pitorch_amd/csrc/ptmi_gemm.hip" in bench.TRAIN_SOURCES
+
+
+def test_in_step_row_on_matching_sources(tmp_path):
+    p = tmp_path / "train.md"
+    p.write_text("# profile\n\n" + IN_STEP.format(h=bench.train_sources_hash()))
+    got, note = bench.committed_in_step(path=str(p))
+    assert note is None and got == {"steps": 18, "gemm_ms": 0.6125, "kernels_ms": 0.8024}
+
+
+def test_in_step_row_on_other_sources_is_null(tmp_path):
+    p = tmp_path / "train.md"
+    p.write_text(IN_STEP.format(h="fedcba9876543210"))
+    got, note = bench.committed_in_step(path=str(p))
+    assert got is None and "fedcba9876543210" in note and bench.train_sources_hash() in note
+    assert bench.committed_in_step(path=str(tmp_path / "none.md"))[0] is None
