@@ -452,7 +452,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
 // s and waited for (vmcnt, in order) at the next step's barrier.
 // Measured on the MI355X against the register-ring kernel (launches back to
 // back, same inputs, same bits): NT 256x32000x288 with 256x128 tiles, 47.2
-// vs 51.3 us; TN 32000x288x255 with 64x96 tiles, 55.5 vs 58.7 us.  Deeper
+// vs 51.3 us; TN 32000x288x255 with 64x96 tiles, 55.5 vs 58.7 us, and with
+// 128x96 tiles on 8 waves (4x2) 51.1-52.9 vs 53.6-55.1 us (graph-replayed,
+// same output bits; 128x96 on 4 or 8x1 waves, 256x96, 64x96 on 8 waves,
+// 64x288 and 128x288 were slower).  NT 256x128 on 8x1 or 2x4 waves and
+// 256x64 tiles were no faster than 4x2.  Deeper
 // stage rings, 64-k stages, and loads interleaved one per MFMA k step were
 // all slower; so were these tiles on the per-layer shapes (5-16 us against
 // 5-10 us) and on the long-K NN (split K, 68 vs 60 us).
@@ -794,8 +798,9 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
             fn = k_gemm_dl<false, false, 256, 128, 4, 2>;
             threads = 512;
         } else if (op == 1) {
-            grid = dim3((unsigned)((N + 95) / 96), (unsigned)((M + 63) / 64), 1);
-            fn = k_gemm_dl<true, true, 64, 96, 2, 2>;
+            grid = dim3((unsigned)((N + 95) / 96), (unsigned)((M + 127) / 128), 1);
+            fn = k_gemm_dl<true, true, 128, 96, 4, 2>;
+            threads = 512;
         }
     }
     hipLaunchKernelGGL(fn, grid, dim3(threads), 0, s, g);
