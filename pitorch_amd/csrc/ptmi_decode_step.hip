@@ -88,6 +88,7 @@ struct StepArgs {
     int n_stamps;                            // 1 + 10 L + 4
     uint64_t wait_ticks;                     // bound of every wait (100 MHz ticks)
     int l2pf;                                // L2 staging by idle workgroups: 1 w1|w3 + w2, 2 next QKV + Wo
+    int cls_pf;                              // classifier row blocks each w2-idle workgroup stages in the last layer
 };
 
 
@@ -564,6 +565,24 @@ __device__ __forceinline__ float prefetch_rows(const float *W, int rows, int n, 
 #pragma unroll
             for (int u = 0; u < 8; u++) acc += v[u].x;
         }
+    }
+    return acc;
+}
+
+// Row block rb (R rows of n floats) read into this XCD's L2 by the whole
+// workgroup; the values go into acc, which the kernel keeps.
+__device__ __forceinline__ float prefetch_block(const float *W, int rows, int n, int R, int rb, float acc) {
+    const int r0 = rb * R, r1 = min(r0 + R, rows);
+    if (r0 >= r1) return acc;
+    const long n4 = (long)(r1 - r0) * n / 4;
+    const float *base = W + (long)r0 * n;
+    const int t = opaque((int)threadIdx.x);
+    for (long i = t; i < n4; i += 8L * kT) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = load4(base + 4 * min(i + (long)u * kT, n4 - 1));
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc += v[u].x;
     }
     return acc;
 }
@@ -1073,6 +1092,11 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     if (a->wbase == 0)
                         pf_acc = prefetch_rows(a->wo + (long)(l + 1) * D * D, D, D, kRowsD, (D + kRowsD - 1) / kRowsD,
                                                blocks_w2, nb, pf_acc);
+                } else if (last_layer && in(kStages * L)) {
+                    // the last layer: this workgroup's classifier row blocks
+                    // after the two the classifier starts with
+                    for (int j = 0; j < a->cls_pf; j++)
+                        pf_acc = prefetch_block(a->wcls, a->V, D, kRowsD, b + (2 + j) * nb, pf_acc);
                 }
             }
             // after W2: the next layer's K/V rows (attention units)
@@ -1379,6 +1403,10 @@ int decode_step_create(ptmi_model *m) {
         const int first_idle = std::max(std::max(a.qbase + blocks_qkv, a.wbase + blocks_wo), a.ubase + (int)(NH * nc));
         const char *pf = getenv("PTMI_STEP_L2PF");
         a.l2pf = pf ? atoi(pf) & 3 : (nb - first_idle >= 64 ? 3 : 2);
+        // In the last layer the workgroups idle during w2 also stage the
+        // classifier row block they take third (PTMI_STEP_CLSPF: 0-4 blocks)
+        const char *cp = getenv("PTMI_STEP_CLSPF");
+        a.cls_pf = cp ? std::max(0, std::min(4, atoi(cp))) : 1;
     }
     hipError_t e = hipMemsetAsync(mem, 0, total, lib_stream());
     if (e == hipSuccess) e = hipMemcpyAsync(mem + args_off, &a, sizeof(a), hipMemcpyHostToDevice, lib_stream());
