@@ -89,6 +89,7 @@ struct StepArgs {
     uint64_t wait_ticks;                     // bound of every wait (100 MHz ticks)
     int l2pf;                                // L2 staging by idle workgroups: 1 w1|w3 + w2, 2 next QKV + Wo
     int cls_pf;                              // classifier row blocks each w2-idle workgroup stages in the last layer
+    int poison;                              // test only: chunk-record LDS starts as NaN (PTMI_STEP_POISON_LDS=1)
 };
 
 
@@ -623,6 +624,9 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
         tk.nact = tk.pos / a->chunk + 1;
         L = a->L;
         if (tid == 0) sm.fail = 0;
+        // (a test's check that no chunk merge reads a record it did not poll)
+        if (a->poison)
+            for (int i = tid; i < kPartLds; i += kT) sm.part[i] = __int_as_float(0x7fc00000);
         // RoPE angle of pair (i, i+1) depends on i % head_dim and pos only
         // (pt_ops.c:33-40): one table per token serves q and k of every layer
         if (tid < (a->hd >> 1)) {
@@ -944,7 +948,10 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                             M = fmaxf(M, dpp_xor2(M));
                             M = fmaxf(M, dpp_hmirror(M));
                             const float f = act ? d_expf(mc - M) : 0.0f;
-                            float Ls = lc * f;
+                            // (inactive chunks' LDS records were not written
+                            // this token: their values, possibly not finite,
+                            // stay out of the sum)
+                            float Ls = act ? lc * f : 0.0f;
                             Ls += dpp_xor1(Ls);
                             Ls += dpp_xor2(Ls);
                             Ls += dpp_hmirror(Ls);
@@ -1407,6 +1414,8 @@ int decode_step_create(ptmi_model *m) {
         // classifier row block they take third (PTMI_STEP_CLSPF: 0-4 blocks)
         const char *cp = getenv("PTMI_STEP_CLSPF");
         a.cls_pf = cp ? std::max(0, std::min(4, atoi(cp))) : 1;
+        const char *pz = getenv("PTMI_STEP_POISON_LDS");
+        a.poison = pz && pz[0] == '1';
     }
     hipError_t e = hipMemsetAsync(mem, 0, total, lib_stream());
     if (e == hipSuccess) e = hipMemcpyAsync(mem + args_off, &a, sizeof(a), hipMemcpyHostToDevice, lib_stream());

@@ -361,6 +361,24 @@ def test_step_kernel_for_dim_256_matches_oracle():
     assert _oracle_decode(blob, 64, prompt) == [-1, 0]
 
 
+def test_step_merge_reads_only_the_records_it_polled():
+    """A head's chunk-0 merge takes the statistics of the head's active
+    chunks only.  With PTMI_STEP_POISON_LDS=1 every workgroup starts with
+    its chunk-record LDS full of NaN, so a merge that let an inactive
+    chunk's (unpolled) record into its sums would give NaN logits.
+    stories15M shape, all 256 positions (8 units of 32 per head, 1 to 8
+    active), against the oracle."""
+    name = "stories15M"
+    cfg = pa.STORIES[name]
+    blob = pa.synth_model(cfg, pa.SEED_MODEL[name])
+    prompt = [int(t) for t in pa.seed_tokens(pa.SEED_PROMPT, pa.N_PROMPT, cfg[5])]
+    os.environ["PTMI_STEP_POISON_LDS"] = "1"
+    try:
+        assert _oracle_decode(blob, 256, prompt, paths=("1",)) == [0]
+    finally:
+        os.environ.pop("PTMI_STEP_POISON_LDS")
+
+
 def test_wrapped_attention_units_take_the_multi_kernel_step():
     """48 heads of 16 over 1024 positions make 384 attention units, more
     than the 256 workgroups of the one-kernel step: the plan refuses it (a
