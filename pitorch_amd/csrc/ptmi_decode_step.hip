@@ -312,6 +312,7 @@ struct Smem {
     float xres[kRowsD];                // WO: residual rows of this block
     float xres2[kRowsH];               // W2: residual rows of this block
     float rope_c[64], rope_s[64];      // RoPE cos/sin of this position, pair i = 2*k (all layers)
+    int rope_k[kRowsD];                // QKV: the RoPE pair of each row of this workgroup's first block
     float ybuf[kW][2];                 // argmax per wave
     float qs[128], kp[128], vp[128];   // ATT: q, and k/v of this position
     float red[kW][128];
@@ -635,6 +636,12 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             sm.rope_c[tid] = c;
             sm.rope_s[tid] = sn;
         }
+        // the pair of each q/k row of the first QKV block (the same rows in
+        // every layer): pair k = (position of the row in its head) / 2
+        if (tid >= 64 && tid < 64 + kRowsD) {
+            const int r0 = ((b - a->qbase) * kRowsD + tid - 64) & ~1;
+            sm.rope_k[tid - 64] = ((r0 < a->D ? r0 : r0 - a->D) % a->hd) >> 1;
+        }
         // Each register set is loaded at one point: after the stage that
         // last read it, a stage or more ahead of its use (w1|w3 rows after
         // QKV, w2 rows after Wo, the next QKV or classifier rows after
@@ -711,7 +718,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                         const int r0 = r & ~1;
                         float out;
                         if (r0 < D + KV) {
-                            const int k = ((r0 < D ? r0 : r0 - D) % a->hd) >> 1;
+                            const int k = rb == qb ? sm.rope_k[slot_d()] : ((r0 < D ? r0 : r0 - D) % a->hd) >> 1;
                             const float c = sm.rope_c[k], sn = sm.rope_s[k];
                             out = (r & 1) ? pr.lo * sn + pr.hi * c : pr.lo * c - pr.hi * sn;
                         } else {
