@@ -450,6 +450,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
 // step s -> k = 4g + s), so every product pairs the same k.
 // Two LDS stages: the loads of tile s+1 are issued before the MFMAs of tile
 // s and waited for (vmcnt, in order) at the next step's barrier.
+// The classifier's weight gradient (TN) runs on these tiles, its forward
+// (NT) on the 32x32x2 form below (gemm_tile_dl32).
 // Measured on the MI355X against the register-ring kernel (launches back to
 // back, same inputs, same bits): NT 256x32000x288 with 256x128 tiles, 47.2
 // vs 51.3 us; TN 32000x288x255 with 64x96 tiles, 55.5 vs 58.7 us, and with
@@ -593,6 +595,144 @@ __device__ __forceinline__ void gemm_tile_dl(const GemmArgs &g, int m0, int n0, 
     gemm_store<EPI, FM, FN>(g, acc, m0 + wm * (TM / WM), n0 + wn * (TN / WN), z, li, lk);
 }
 
+// The NT direct-to-LDS tile on v_mfma_f32_32x32x2_f32 (the classifier's
+// forward: both operands k-contiguous, same LDS layout and DMA loads as
+// gemm_tile_dl).  In 8-k block q, lane half h = l/32 of a 32-lane group
+// reads chunk 2q + h of its row as one b128, so step s pairs k = 8q + s
+// (h = 0) with k = 8q + 4 + s (h = 1); A and B use the same order.  The 8
+// lanes of a b128 access phase hit 8 distinct chunk slots, as in
+// gemm_tile_dl.  C[(v/4)*8 + 4h + v%4][l%32] is component v of the lane's
+// 16 sums; the tile goes out through LDS as whole rows, a float4 per lane.
+// Measured on the MI355X for the 15M classifier (256 x 32000 x 288,
+// interleaved launches): 44.5-49.9 us against 45.7-51.4 us for the 16x16x4
+// tile, the same bits on integer-valued operands.  Four waves per SIMD
+// (16-wave 256x128 tiles, or two 128x128 workgroups per CU) and a third LDS
+// stage gave no further gain: each 32-k step costs ~4.0 us in every form,
+// the rate of one wave's MFMA issue.
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+template <int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void gemm_tile_dl32(const GemmArgs &g, int m0, int n0, int z) {
+    constexpr int NW = WM * WN, NS = kDlStages, CPI = BK / 4;
+    constexpr int FM = TM / WM / 32, FN = TN / WN / 32;
+    static_assert(FM * WM * 32 == TM && FN * WN * 32 == TN, "tile");
+    constexpr int STAGE = (TM + TN) * BK;
+    __shared__ __align__(16) float smem[NS * STAGE + 256];
+    float *junk = smem + NS * STAGE;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int li = lane & 31, lh = lane >> 5;
+    const int kb = z * g.k_per_split;
+    const int kend = min(g.K, kb + g.k_per_split);
+    const int nk = kb < kend ? (kend - kb + BK - 1) / BK : 0;
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
+
+    auto issue = [&](int t) {
+        float *st = smem + (t % NS) * STAGE;
+        const int k0 = kb + t * BK;
+        dl_issue<false, TM, NW>(g.A, g.lda, g.M, m0, k0, kend, st, junk, wave, lane);
+        dl_issue<false, TN, NW>(g.B, g.ldb, g.N, n0, k0, kend, st + TM * BK, junk, wave, lane);
+    };
+    // row i of a k-contiguous tile, k = 8q + 4h + s in component s
+    auto rd = [&](const float *base, int i, int q) {
+        return *reinterpret_cast<const floatx4 *>(base + (i * CPI + ((2 * q + lh) ^ (i & 7))) * 4);
+    };
+
+    if (nk > 0) issue(0);
+    for (int s = 0; s < nk; s++) {
+        // as gemm_tile_dl: tile s is in once this wave's loads are done and
+        // every wave is past the barrier, which also ends the reads of the
+        // stage that tile s+1 overwrites
+        wait_vmcnt<0>();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (s + 1 < nk) issue(s + 1);
+        const float *st = smem + (s % NS) * STAGE, *sb = st + TM * BK;
+        floatx4 a[4][FM], b[4][FN];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+#pragma unroll
+            for (int f = 0; f < FM; f++) a[q][f] = rd(st, wm * (TM / WM) + f * 32 + li, q);
+#pragma unroll
+            for (int h = 0; h < FN; h++) b[q][h] = rd(sb, wn * (TN / WN) + h * 32 + li, q);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int ss = 0; ss < 4; ss++)
+#pragma unroll
+                for (int f = 0; f < FM; f++)
+#pragma unroll
+                    for (int h = 0; h < FN; h++)
+                        acc[f][h] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q][f][ss], b[q][h][ss], acc[f][h], 0, 0, 0);
+    }
+    // C, or this split's partial product (partial + z*M*N, ld N)
+    const int mb = m0 + wm * (TM / WM), nb = n0 + wn * (TN / WN);
+    const bool part = g.partial != nullptr, accum = !part && g.accumulate;
+    float *const out = part ? g.partial + (long)z * g.M * g.N : g.C;
+    const long ldo = part ? (long)g.N : g.ldc;
+    if (!(ldo & 3) && !((uintptr_t)out & 15) && (!accum || !((uintptr_t)g.Cin & 15))) {
+        // Each wave stages RP rows x W columns at a time in its own LDS
+        // region (the stage buffers are free once every wave is past the
+        // loop) and stores whole rows, a float4 per lane.
+        constexpr int W = FN * 32, P = W + 4, RP = NW * 32 * P <= NS * STAGE ? 32 : 16;
+        static_assert(NW * RP * P <= NS * STAGE, "store staging");
+        __syncthreads();
+        float *T = smem + wave * RP * P;
+#pragma unroll
+        for (int f = 0; f < FM; f++) {
+#pragma unroll
+            for (int p = 0; p < 32 / RP; p++) {
+                // components v of rows [p*RP, p*RP + RP) (a wave's LDS
+                // operations complete in order, so this pass's reads are
+                // done before the next pass overwrites the region)
+#pragma unroll
+                for (int h = 0; h < FN; h++)
+#pragma unroll
+                    for (int v = p * RP / 2; v < (p + 1) * RP / 2; v++)
+                        T[((v >> 2) * 8 + 4 * lh + (v & 3) - p * RP) * P + h * 32 + li] = acc[f][h][v];
+                for (int e4 = lane; e4 < RP * W / 4; e4 += 64) {
+                    const int r = e4 / (W / 4), c = 4 * (e4 % (W / 4));
+                    const floatx4 val = *reinterpret_cast<const floatx4 *>(T + r * P + c);
+                    const int m = mb + f * 32 + p * RP + r, n = nb + c;
+                    if (m >= g.M) continue;
+                    const long o = (long)m * ldo + n;
+                    if (n + 3 < g.N) {
+                        floatx4 cv = val;
+                        if (accum) cv += *reinterpret_cast<const floatx4 *>(g.Cin + o);
+                        *reinterpret_cast<floatx4 *>(out + o) = cv;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            if (n + e < g.N) out[o + e] = accum ? g.Cin[o + e] + val[e] : val[e];
+                    }
+                }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int f = 0; f < FM; f++)
+#pragma unroll
+        for (int h = 0; h < FN; h++) {
+            const int n = nb + h * 32 + li;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int m = mb + f * 32 + (v >> 2) * 8 + 4 * lh + (v & 3);
+                if (n >= g.N || m >= g.M) continue;
+                const long o = (long)m * ldo + n;
+                out[o] = accum ? g.Cin[o] + acc[f][h][v] : acc[f][h][v];
+            }
+        }
+}
+
 // Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its
 // own L2.  Block b runs tile xcd_tile(b): XCD c gets the c-th contiguous
 // range of the tiles, in order, so tiles that read the same operand tile
@@ -633,6 +773,21 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_dl(GemmArgs g) {
         else n = u / gy, m = u - n * gy;
     }
     gemm_tile_dl<AK, BKM, TM, TN, WM, WN>(g, m * TM, n * TN, z);
+}
+
+// The classifier's NT forward on the 32x32x2 tiles (grid and tile order as k_gemm).
+template <int TM, int TN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void k_gemm_dl32(GemmArgs g) {
+    const int gx = gridDim.x, gy = gridDim.y, per_z = gx * gy, total = per_z * gridDim.z;
+    int m = blockIdx.y, n = blockIdx.x, z = blockIdx.z;
+    if (total >= kXcdGrid) {                                        // uniform
+        const int t = xcd_tile(blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z), total);
+        z = t / per_z;
+        const int u = t - z * per_z;
+        if (g.M > g.N) m = u / gx, n = u - m * gx;
+        else n = u / gy, m = u - n * gy;
+    }
+    gemm_tile_dl32<TM, TN, WM, WN>(g, m * TM, n * TN, z);
 }
 
 // Grouped TN GEMMs (32x32 tiles, whole K): block b runs tile
@@ -795,7 +950,7 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
     if (vec && ek == GEMM_EPI_NONE && splits == 1 && (long)M * N >= (4L << 20)) {
         if (op == 2 && M >= 192) {
             grid = dim3((unsigned)((N + 127) / 128), (unsigned)((M + 255) / 256), 1);
-            fn = k_gemm_dl<false, false, 256, 128, 4, 2>;
+            fn = k_gemm_dl32<256, 128, 4, 2>;
             threads = 512;
         } else if (op == 1) {
             grid = dim3((unsigned)((N + 95) / 96), (unsigned)((M + 127) / 128), 1);
