@@ -439,10 +439,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
 // Each operand tile keeps its global layout in LDS, permuted in whole
 // 16-byte chunks (the only granularity a DMA load can place):
 //  * k-contiguous operands ([i][k]: A of NN/NT, B^T of NT): rows of BK=32
-//    floats, chunk c of row i at slot c ^ (i & 7).  A lane reads the 4 k of
-//    its row for 4 MFMA steps as one b128 (lane group g takes k = 4g..4g+3 of
-//    each 16-k group): the 8 lanes of an access phase hit 8 distinct chunk
-//    slots, so there are no bank conflicts;
+//    floats (128 bytes), chunk c of row i at slot c ^ kc_swz(i).  A lane
+//    reads the 4 k of its row for 4 MFMA steps as one b128 (lane group g
+//    takes k = 4g..4g+3 of each 16-k group).  A b128 read serves 16 lanes
+//    (16 rows) at a time across the 64 banks, where rows i and i+8 start on
+//    the same bank; kc_swz gives the 16 rows 16 distinct bank groups.  With
+//    c ^ (i & 7) alone the 32x32x2 NT tile measured 45.5% LDS conflict
+//    cycles (SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE), with kc_swz 7.7%
+//    (one cycle per 64-lane b32 write of its store staging), at the same
+//    speed and bits;
 //  * k-major operands ([k][i]: A^T of TN, B of NN/TN): rows of TI floats,
 //    the column XOR-ed with 16 in rows whose bit 2 of k is set; the two k
 //    rows a half-wave reads (g = 0, 1) then sit 16 banks apart.
@@ -463,6 +468,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0, int
 // all slower; so were these tiles on the per-layer shapes (5-16 us against
 // 5-10 us) and on the long-K NN (split K, 68 vs 60 us).
 constexpr int kDlStages = 2;
+
+// Chunk-slot swizzle of row i of a k-contiguous tile: i & 7 spreads 8
+// consecutive rows over the 8 slots; bit 3 of i moves rows i and i+8 to
+// different slots.
+__device__ __forceinline__ int kc_swz(int i) { return (i & 7) ^ ((i >> 3) & 1); }
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {                   // s_waitcnt vmcnt(N), other counters untouched
@@ -492,7 +502,7 @@ __device__ __forceinline__ void dl_issue(const float *P, long ld, int ilim, int 
             if (real && kk < kend && i < ilim) src = P + (long)kk * ld + i;
         } else {
             const int i = S / CPI, t = S % CPI;
-            const int ii = i0 + i, kk = k0 + 4 * (t ^ (i & 7));
+            const int ii = i0 + i, kk = k0 + 4 * (t ^ kc_swz(i));
             if (real && ii < ilim && kk < kend) src = P + (long)ii * ld + kk;
         }
         typedef const void __attribute__((address_space(1))) *gptr;
@@ -545,7 +555,7 @@ __device__ __forceinline__ void gemm_tile_dl(const GemmArgs &g, int m0, int n0, 
                     a[f][s] = st[k * TM + (i ^ (((k >> 2) & 1) << 4))];
                 }
             } else {
-                a[f] = *reinterpret_cast<const floatx4 *>(st + (i * CPI + ((4 * q + lk) ^ (i & 7))) * 4);
+                a[f] = *reinterpret_cast<const floatx4 *>(st + (i * CPI + ((4 * q + lk) ^ kc_swz(i))) * 4);
             }
         }
     };
@@ -561,7 +571,7 @@ __device__ __forceinline__ void gemm_tile_dl(const GemmArgs &g, int m0, int n0, 
                     b[h][s] = sb[k * TN + (i ^ (((k >> 2) & 1) << 4))];
                 }
             } else {
-                b[h] = *reinterpret_cast<const floatx4 *>(sb + (i * CPI + ((4 * q + lk) ^ (i & 7))) * 4);
+                b[h] = *reinterpret_cast<const floatx4 *>(sb + (i * CPI + ((4 * q + lk) ^ kc_swz(i))) * 4);
             }
         }
     };
@@ -641,7 +651,7 @@ __device__ __forceinline__ void gemm_tile_dl32(const GemmArgs &g, int m0, int n0
     };
     // row i of a k-contiguous tile, k = 8q + 4h + s in component s
     auto rd = [&](const float *base, int i, int q) {
-        return *reinterpret_cast<const floatx4 *>(base + (i * CPI + ((2 * q + lh) ^ (i & 7))) * 4);
+        return *reinterpret_cast<const floatx4 *>(base + (i * CPI + ((2 * q + lh) ^ kc_swz(i))) * 4);
     };
 
     if (nk > 0) issue(0);
