@@ -315,6 +315,7 @@ struct Smem {
     int rope_k[kRowsD];                // QKV: the RoPE pair of each row of this workgroup's first block
     float ybuf[kW][2];                 // argmax per wave
     float qs[128], kp[128], vp[128];   // ATT: q, and k/v of this position
+    float mrg[kMaxHd];                 // ATT, chunk 0: the merged head output
     float red[kW][128];
     float wred[kW];
     float sc[kAttRows];                // ATT: scores -> weights
@@ -921,54 +922,63 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     }
                 } else {
                     // chunk 0 merges the head's active chunks: its own
-                    // record in the writer wave's registers, the others'
-                    // polled into LDS, then w_c = e^(m_c - M) / sum_c' l_c'
-                    // e^(m_c' - M) and out = sum_c w_c o_c, published for
-                    // the WO stage.  The writer wave does the merge alone:
-                    // lane c (< 8) holds chunk c's statistics, M and the sum
-                    // over c come from three cross-lane steps within the
-                    // lane's 8-lane group, and the output sums keep the chunk
-                    // order.  One chunk is o / l, which is what the general
-                    // arithmetic gives there (M = m, e^0 = 1).
+                    // record (put in LDS slot 0 by the writer wave) and the
+                    // others' (polled into slots 1..), then w_c =
+                    // e^(m_c - M) / sum_c' l_c' e^(m_c' - M) and out =
+                    // sum_c w_c o_c, published for the WO stage.  One chunk
+                    // is o / l, which is what the general arithmetic gives
+                    // there (M = m, e^0 = 1); the writer wave stores it
+                    // directly.  With several, all eight waves merge (the
+                    // writer wave alone took 0.84-0.90 us at long context,
+                    // a chain of per-chunk LDS reads and broadcasts).
                     static_assert(kMaxChunks == 8, "chunk statistics reduce over 8-lane groups");
                     const int nact = tk.nact, nother = nact - 1;
-                    float o0 = 0.0f, m0 = 0.0f, l0 = 0.0f;
+                    float o0 = 0.0f, l0 = 0.0f;
                     if (wave == kWriter) {
                         o0 = rec_o(min(lane, hd - 1));
-                        m0 = mx;
                         l0 = rec_l();
+                        if (nact > 1) {
+                            // its own record into slot 0, beside the polled ones
+                            if (lane < hd) sm.part[lane] = o0;
+                            if (lane == 0) sm.part[hd] = mx;
+                            if (lane == 1) sm.part[hd + 1] = l0;
+                        }
                     }
                     bool ok = true;
                     if (nother > 0 && tid < kPollT)
                         ok = poll_pairs<1>(head_part + (hd + 2), nother * (hd + 2), tk.tag, sm.part + (hd + 2), a, tid);
                     if (!block_ok(ok, &sm.fail, a->ctl)) return;
-                    if (wave == kWriter) {
-                        float v;
-                        if (nact == 1) {
-                            v = o0 * (1.0f / l0);
-                        } else {
-                            const float *pc = sm.part + (lane & 7) * (hd + 2);
-                            const bool act = (lane & 7) < nact;
-                            const float mc = (lane & 7) == 0 ? m0 : pc[hd], lc = (lane & 7) == 0 ? l0 : pc[hd + 1];
-                            float M = act ? mc : -INFINITY;
-                            M = fmaxf(M, dpp_xor1(M));
-                            M = fmaxf(M, dpp_xor2(M));
-                            M = fmaxf(M, dpp_hmirror(M));
-                            const float f = act ? d_expf(mc - M) : 0.0f;
-                            // (inactive chunks' LDS records were not written
-                            // this token: their values, possibly not finite,
-                            // stay out of the sum)
-                            float Ls = act ? lc * f : 0.0f;
-                            Ls += dpp_xor1(Ls);
-                            Ls += dpp_xor2(Ls);
-                            Ls += dpp_hmirror(Ls);
-                            const float w = f * (1.0f / Ls);
-                            const int d = min(lane, hd - 1);
-                            v = o0 * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 0));
-                            for (int k = 1; k < nact; k++)
-                                v = fmaf(sm.part[k * (hd + 2) + d], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), k)), v);
-                        }
-                        if (lane < hd) tstore(a->t_att + (long)l * D + h * hd + lane, v, tk.tag);
+                    if (nact == 1) {
+                        if (wave == kWriter && lane < hd)
+                            tstore(a->t_att + (long)l * D + h * hd + lane, o0 * (1.0f / l0), tk.tag);
+                    } else {
+                        // every wave merges 8 of the head's outputs: lane 8g + k
+                        // takes output wave*8 + g of chunk k; the chunk
+                        // statistics and the weighted sum reduce over the
+                        // lane's 8-lane group (three cross-lane steps each)
+                        const int k = lane & 7, dq = wave * 8 + (lane >> 3), dd = min(dq, hd - 1);
+                        const bool act = k < nact;
+                        const float *pc = sm.part + k * (hd + 2);
+                        const float mc = pc[hd], lc = pc[hd + 1], oc = pc[dd];
+                        // (inactive chunks' LDS records were not written this
+                        // token: their values, possibly not finite, are
+                        // selected out, never multiplied by zero)
+                        float M = act ? mc : -INFINITY;
+                        M = fmaxf(M, dpp_xor1(M));
+                        M = fmaxf(M, dpp_xor2(M));
+                        M = fmaxf(M, dpp_hmirror(M));
+                        const float f = act ? d_expf(mc - M) : 0.0f;
+                        float Ls = act ? lc * f : 0.0f;
+                        Ls += dpp_xor1(Ls);
+                        Ls += dpp_xor2(Ls);
+                        Ls += dpp_hmirror(Ls);
+                        float pv = act ? oc * (f * (1.0f / Ls)) : 0.0f;
+                        pv += dpp_xor1(pv);
+                        pv += dpp_xor2(pv);
+                        pv += dpp_hmirror(pv);
+                        if (k == 0 && dq < hd) sm.mrg[dq] = pv;
+                        __syncthreads();
+                        if (wave == kWriter && lane < hd) tstore(a->t_att + (long)l * D + h * hd + lane, sm.mrg[lane], tk.tag);
                     }
                 }
                 stamp(a, sm.st, 4 + 10 * l);
