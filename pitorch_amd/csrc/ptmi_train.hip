@@ -658,6 +658,14 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_cols(const float *qkv
 // so a lane's four weights are one float4 in LDS.  Sums therefore run in a
 // different order from the reference's sequential loops.
 constexpr int kMW = 8, kMT = 64 * kMW;
+// Rows per block of the forward and row-backward kernels.  Their MFMA tiles
+// still span 16 rows (the 8 rows after the block's own are computed and
+// dropped), but each wave's per-row softmax work covers one row instead of
+// two.  The slowest block (the last rows, every key) sets the launch time,
+// so halving its softmax share pays for the doubled MFMA work: step 0.808-
+// 0.813 -> 0.790-0.797 ms (stories15M T=256, same-box A/B).
+constexpr int kAttnRows = 8;
+static_assert(kAttnRows % kMW == 0 && kAttnRows <= 16, "rows per wave");
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
@@ -797,7 +805,9 @@ __device__ __forceinline__ void attn_reduce(const f4v (&acc)[HQ], float *red, F 
 }
 
 // Causal attention forward (pt_train.c:224-255) for positions
-// [16*blockIdx.x, +16) of head blockIdx.y: scores into LDS, a softmax per
+// [RT*blockIdx.x, +RT) of head blockIdx.y (RT = kAttnRows; the 16-row MFMA
+// tiles also cover the next 16 - RT rows, whose results are dropped):
+// scores into LDS, a softmax per
 // row (one wave per row; max, then e^(s - max) and its sum, then the 1/sum
 // scaling, as the reference), the probabilities to att (zeros past the
 // diagonal), then att_out = P.V.  Dynamic LDS: max(16*pitch, kMW*16*hd)
@@ -807,8 +817,9 @@ __global__ __launch_bounds__(kMT) void k_attn_fwd_mfma(const float *qkv, float *
                                                       int QS, float scale, int pitch) {
     extern __shared__ float lds[];
     constexpr int HD = 16 * HQ;
-    const int r0 = blockIdx.x * 16, h = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nkb = (min(r0 + 16, T) + 15) / 16, kw = nkb * 16;
+    constexpr int RT = kAttnRows;
+    const int r0 = blockIdx.x * RT, h = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nkb = (min(r0 + RT, T) + 15) / 16, kw = nkb * 16;
     const float *q = qkv + h * HD, *k = qkv + D + h * HD, *v = qkv + 2 * D + h * HD;
     attn_dots<HQ>(q, QS, r0, T, k, QS, T, nkb, scale, lds, pitch);
     AttnWsum<HQ> ws;
@@ -816,7 +827,7 @@ __global__ __launch_bounds__(kMT) void k_attn_fwd_mfma(const float *qkv, float *
     __syncthreads();
     // the wave's rows i = wave + w*kMW, in lockstep (rows past T compute
     // unused values and store nothing)
-    constexpr int RW = 16 / kMW;
+    constexpr int RW = RT / kMW;
     float4 x[RW][kAttnChunks];
     float mx[RW], sum[RW];
 #pragma unroll
@@ -876,19 +887,21 @@ __global__ __launch_bounds__(kMT) void k_attn_fwd_mfma(const float *qkv, float *
     f4v acc[HQ];
     ws.run(lds, pitch, v, QS, T, nkb, acc);
     attn_reduce<HQ>(acc, lds, [&](int i, int c, float o, float) {
-        if (r0 + i < T) att_out[(long)(r0 + i) * D + h * HD + c] = o;
+        if (i < RT && r0 + i < T) att_out[(long)(r0 + i) * D + h * HD + c] = o;
     });
 }
 
 // Attention backward, row half (pt_train.c:780-811) for rows t < R in
-// [16*blockIdx.x, +16) of head blockIdx.y: d_att = d_aout.V^T into LDS, per
+// [RT*blockIdx.x, +RT) of head blockIdx.y (RT = kAttnRows, 16-row MFMA tiles
+// as in the forward; the extra rows' d_aout is read back as another block
+// leaves it and only feeds dropped results): d_att = d_aout.V^T into LDS, per
 // row the softmax backward dot and ds = att*(d_att - dot)*scale (kept for
 // the column half), then d_q = ds.K, stored after rope_backward into the q
 // columns of the fused [dq | dk | dv] row d_qkv.  LDS as k_attn_fwd_mfma.
 template <int HQ>
 // With d_res non-null (D a multiple of 4*kMW), the block first computes its
 // own tile of d_aout = d_res . Wo (backward_input of the Wo projection,
-// pt_train.c:729-730: rows [r0, r0+16), head h's columns), each wave over
+// pt_train.c:729-730: rows [r0, r0+RT), head h's columns), each wave over
 // a D/kMW slice of the contraction summed in wave order, and writes it for
 // the column kernel; the first dot product below reads it back.
 __global__ __launch_bounds__(kMT) void k_attn_bwd_rows_mfma(const float *qkv, const float *att, float *d_aout,
@@ -896,9 +909,9 @@ __global__ __launch_bounds__(kMT) void k_attn_bwd_rows_mfma(const float *qkv, co
                                                            float *d_qkv, int T, int R, int D, int QS, float scale,
                                                            int pitch) {
     extern __shared__ float lds[];
-    constexpr int HD = 16 * HQ, RW = 16 / kMW;             // rows per wave
-    const int r0 = blockIdx.x * 16, h = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nkb = (min(r0 + 16, R) + 15) / 16, kw = nkb * 16;
+    constexpr int RT = kAttnRows, HD = 16 * HQ, RW = RT / kMW;   // rows per wave
+    const int r0 = blockIdx.x * RT, h = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nkb = (min(r0 + RT, R) + 15) / 16, kw = nkb * 16;
     const float *k = qkv + D + h * HD, *v = qkv + 2 * D + h * HD;
     if (d_res) {                                            // uniform
         const int li = lane & 15, g = lane >> 4, ks = D / kMW, k0 = wave * ks;
@@ -913,7 +926,7 @@ __global__ __launch_bounds__(kMT) void k_attn_bwd_rows_mfma(const float *qkv, co
             for (int cb = 0; cb < HQ; cb++) acc[cb] = mfma4(a, bp[(long)s * D + cb * 16], acc[cb]);
         }
         attn_reduce<HQ>(acc, lds, [&](int i, int c, float o, float) {
-            if (r0 + i < R) d_aout[(long)(r0 + i) * D + h * HD + c] = o;
+            if (i < RT && r0 + i < R) d_aout[(long)(r0 + i) * D + h * HD + c] = o;
         });
         __syncthreads();                                   // the tile is written; lds is free again
     }
@@ -975,7 +988,7 @@ __global__ __launch_bounds__(kMT) void k_attn_bwd_rows_mfma(const float *qkv, co
     ws.run(lds, pitch, k, QS, T, nkb, acc);
     attn_reduce<HQ>(acc, lds, [&](int i, int c, float o, float po) {
         const int t = r0 + i;
-        if (t < R) d_qkv[(long)t * QS + h * HD + c] = rope_bwd_elem(o, po, h * HD + c, HD, t);
+        if (i < RT && t < R) d_qkv[(long)t * QS + h * HD + c] = rope_bwd_elem(o, po, h * HD + c, HD, t);
     });
 }
 
@@ -1411,8 +1424,8 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr
         SPAN_END();
         SPAN("attention", "fwd", l);
         if (mfma_attn)
-            hipLaunchKernelGGL(mf_fwd[HQ - 1], dim3((T + 15) / 16, NH), dim3(kMT), mf_lds, s, qkv, att, ao, T, D, QS,
-                               scale, pitch);
+            hipLaunchKernelGGL(mf_fwd[HQ - 1], dim3((T + kAttnRows - 1) / kAttnRows, NH), dim3(kMT), mf_lds, s, qkv, att,
+                               ao, T, D, QS, scale, pitch);
         else
             hipLaunchKernelGGL(attn_fwd, dim3(T, NH), dim3(kAttnThreads), att_lds, s, qkv, att, ao, T, D, QS, KV, hd,
                                kv_mul, scale);
@@ -1521,8 +1534,8 @@ int enqueue_train(ptmi_model *m, int T, hipStream_t s, TrainTracer *tr = nullptr
         // attention
         SPAN("attention", "bwd", l);
         if (mfma_attn) {
-            hipLaunchKernelGGL(mf_rows[HQ - 1], dim3((R + 15) / 16, NH), dim3(kMT), mf_lds, s, qkv, att, ts->d_aout,
-                               wo_fused ? dres(v) : nullptr, wo, ts->ds, dqkv, T, R, D, QS, scale, pitch);
+            hipLaunchKernelGGL(mf_rows[HQ - 1], dim3((R + kAttnRows - 1) / kAttnRows, NH), dim3(kMT), mf_lds, s, qkv,
+                               att, ts->d_aout, wo_fused ? dres(v) : nullptr, wo, ts->ds, dqkv, T, R, D, QS, scale, pitch);
             hipLaunchKernelGGL(mf_cols[HQ - 1], dim3((R + 15) / 16, NH), dim3(kMT), mc_lds, s, qkv, att, ts->ds,
                                ts->d_aout, dqkv, T, R, D, QS);
         } else {
