@@ -52,7 +52,7 @@ constexpr int kRowsD = 2 * kW;               // rows per block, D-length rows (3
 constexpr int kRowsH = kW;                   // rows per block, H-length rows (64 lanes per row)
 constexpr int kAttRows = 128;                // attention positions per unit (at most)
 constexpr int kMaxChunks = 8;                // units per head
-constexpr int kWriter = kW - 1;              // the wave that issues the workgroup's global stores
+constexpr int kWriter = kW - 1;              // the wave that issues the workgroup's global stores (w1|w3 and w2 excepted)
 constexpr int kPollT = kWriter * 64;         // threads that poll (all other waves)
 constexpr int kMaxHd = 64;                   // head_dim of the instantiated kernels (16 lanes x float4)
 constexpr int kPartLds = kMaxChunks * (kMaxHd + 2);  // floats of one head's chunk records
@@ -1042,19 +1042,27 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 uint64_t *t_hb = a->t_hb + (long)l * H;
                 for (int rb = b; rb < blocks_w13; rb += nb) {
                     if (rb != b) {
-                        __syncthreads();                      // the writer wave is done with yout
+                        __syncthreads();                      // every wave is done with the block before
                         load_wD(a, R, a->w13 + (long)l * 2 * H * D, 2 * H, rb, a->rms_ffn + (long)l * D);
                     }
                     const float acc = dot_d(a, R, sm.xs, true);
                     const LanePair pr = pl32(acc);
-                    if (lane == 0) {
+                    // Each wave stores its own output (no barrier, no writer
+                    // wave): the waves' next poll (w2's, right after) may wait
+                    // for the acknowledgement of these stores, but it cannot
+                    // complete before the last w1|w3 workgroup's words land
+                    // anyway (6083-6092 against 5963-5967 tok/s with the
+                    // same for w2, same box).  Storing Wo's outputs this way
+                    // delayed the w1|w3 release by 1.5 us (Wo's 16 words
+                    // per block from 16 single-lane stores, polled by every
+                    // workgroup), and QKV's added the cache-row work to the
+                    // storing lanes; both keep the writer wave.
+                    const int i = rb * (kRowsD / 2) + wave;       // hb index of this wave's row pair
+                    if (lane == 0 && 2 * i < 2 * H) {
                         const float h1 = pr.lo, h3 = pr.hi;
                         const float sg = h1 / (1.0f + d_expf(-h1));
-                        sm.yout[wave] = sg * h3;
+                        tstore(t_hb + i, sg * h3, tk.tag);
                     }
-                    __syncthreads();
-                    const int i = rb * (kRowsD / 2) + lane;       // hb index of row pair `lane`
-                    if (wave == kWriter && lane < kRowsD / 2 && 2 * i < 2 * H) tstore(t_hb + i, sm.yout[lane], tk.tag);
                 }
                 stamp(a, sm.st, 8 + 10 * l);
             }
@@ -1089,7 +1097,7 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                 stamp(a, sm.st, 9 + 10 * l);
                 for (int rb = b; rb < blocks_w2; rb += nb) {
                     if (rb != b) {
-                        __syncthreads();                      // the writer wave is done with yout
+                        __syncthreads();                      // every wave is done with the block before
                         load_wH(a, R, a->w2 + (long)l * D * H, D, rb);
                         bool ok2 = true;
                         if (tid < kRowsH)
@@ -1097,10 +1105,8 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                         if (!block_ok(ok2, &sm.fail, a->ctl)) return;
                     }
                     const float acc = dot_h(a, R, sm.xs);
-                    if (lane == 0) sm.yout[wave] = sm.xres2[wave] + acc;
-                    __syncthreads();
-                    if (wave == kWriter && lane < kRowsH && rb * kRowsH + lane < D)
-                        tstore(t_xb + rb * kRowsH + lane, sm.yout[lane], tk.tag);
+                    // each wave stores its own row, as in w1|w3
+                    if (lane == 0 && rb * kRowsH + wave < D) tstore(t_xb + rb * kRowsH + wave, sm.xres2[wave] + acc, tk.tag);
                 }
                 stamp(a, sm.st, 10 + 10 * l);
             } else {
