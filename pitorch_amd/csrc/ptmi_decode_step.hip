@@ -52,7 +52,7 @@ constexpr int kRowsD = 2 * kW;               // rows per block, D-length rows (3
 constexpr int kRowsH = kW;                   // rows per block, H-length rows (64 lanes per row)
 constexpr int kAttRows = 128;                // attention positions per unit (at most)
 constexpr int kMaxChunks = 8;                // units per head
-constexpr int kWriter = kW - 1;              // the wave that issues the workgroup's global stores (w1|w3 and w2 excepted)
+constexpr int kWriter = kW - 1;              // the wave that issues the workgroup's global stores (not w1|w3's, nor w2's at dim 768)
 constexpr int kPollT = kWriter * 64;         // threads that poll (all other waves)
 constexpr int kMaxHd = 64;                   // head_dim of the instantiated kernels (16 lanes x float4)
 constexpr int kPartLds = kMaxChunks * (kMaxHd + 2);  // floats of one head's chunk records
@@ -600,6 +600,12 @@ constexpr int kStages = 5;
 template <int ITD, int ITH, int GA>
 __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, int g1) {
     using Rg = Regs<ITD, ITH, GA>;
+    // w2's waves store their own rows on the dim-768 instantiation, and
+    // hand them to the writer wave on the smaller ones.  Same-box tok/s,
+    // writer wave / own stores (w1|w3 storing its own in both): stories110M
+    // 6009 / 6075, stories42M 9392 / 8802, stories15M 13043 / 12589.  (A
+    // run-time switch between the two cost 0.5-1.2% on every shape.)
+    constexpr bool kW2Direct = ITD >= 6;
     // word pairs per polling thread of a dim-length and a hidden-length vector
     constexpr int kPD = (ITD * 64 + kPollT - 1) / kPollT, kPH8 = (ITH * 128 + kT - 1) / kT;
     __shared__ Smem sm;
@@ -1051,12 +1057,14 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     // wave): the waves' next poll (w2's, right after) may wait
                     // for the acknowledgement of these stores, but it cannot
                     // complete before the last w1|w3 workgroup's words land
-                    // anyway (6083-6092 against 5963-5967 tok/s with the
-                    // same for w2, same box).  Storing Wo's outputs this way
-                    // delayed the w1|w3 release by 1.5 us (Wo's 16 words
-                    // per block from 16 single-lane stores, polled by every
-                    // workgroup), and QKV's added the cache-row work to the
-                    // storing lanes; both keep the writer wave.
+                    // anyway (stories110M 6009 against 5949 tok/s, 6075 with
+                    // w2 storing its own too; stories42M 9392 against 9373;
+                    // same box).  Storing Wo's outputs this way delayed the
+                    // w1|w3 release by 1.5 us (Wo's 16 words per block from
+                    // 16 single-lane stores, polled by every workgroup), the
+                    // merged head outputs likewise Wo's release by 0.25 us,
+                    // and QKV's added the cache-row work to the storing
+                    // lanes; those keep the writer wave.
                     const int i = rb * (kRowsD / 2) + wave;       // hb index of this wave's row pair
                     if (lane == 0 && 2 * i < 2 * H) {
                         const float h1 = pr.lo, h3 = pr.hi;
@@ -1105,8 +1113,15 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                         if (!block_ok(ok2, &sm.fail, a->ctl)) return;
                     }
                     const float acc = dot_h(a, R, sm.xs);
-                    // each wave stores its own row, as in w1|w3
-                    if (lane == 0 && rb * kRowsH + wave < D) tstore(t_xb + rb * kRowsH + wave, sm.xres2[wave] + acc, tk.tag);
+                    if constexpr (kW2Direct) {                // each wave stores its own row
+                        if (lane == 0 && rb * kRowsH + wave < D)
+                            tstore(t_xb + rb * kRowsH + wave, sm.xres2[wave] + acc, tk.tag);
+                    } else {
+                        if (lane == 0) sm.yout[wave] = sm.xres2[wave] + acc;
+                        __syncthreads();
+                        if (wave == kWriter && lane < kRowsH && rb * kRowsH + lane < D)
+                            tstore(t_xb + rb * kRowsH + lane, sm.yout[lane], tk.tag);
+                    }
                 }
                 stamp(a, sm.st, 10 + 10 * l);
             } else {
