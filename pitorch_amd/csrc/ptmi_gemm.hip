@@ -22,6 +22,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <utility>
 
 namespace ptmi {
 
@@ -605,6 +606,77 @@ __device__ __forceinline__ void gemm_tile_dl(const GemmArgs &g, int m0, int n0, 
     gemm_store<EPI, FM, FN>(g, acc, m0 + wm * (TM / WM), n0 + wn * (TN / WN), z, li, lk);
 }
 
+// The per-layer GEMMs' 32x32 tile with every K tile of its split in flight
+// at once: the block issues the DMA loads of all NSK tiles (each into its
+// own LDS stage; tiles past the split's K range load zeros) before its first
+// MFMA, and starts tile s once the loads behind it are the only ones left
+// (vmcnt counts them).  The register ring holds one or two tiles ahead, so
+// each of its K steps waits about one load latency; here the block waits
+// for about one.  Operand layout, MFMA k order and epilogue as
+// gemm_tile_dl with 2 x 2 waves of 16 x 16.  NT (B^T k-contiguous) or NN
+// (BKM: B stored [K][N]).
+// f(integral_constant<int, s>) for s = S...
+template <typename F, int... S>
+__device__ __forceinline__ void unrolled(F &f, std::integer_sequence<int, S...>) {
+    (f(std::integral_constant<int, S>{}), ...);
+}
+
+template <bool BKM, int NSK, int EPI>
+__device__ __forceinline__ void gemm_tile_panel(const GemmArgs &g, int m0, int n0, int z) {
+    constexpr int TM = 32, TN = 32, WN = 2, NW = 4, CPI = BK / 4;
+    constexpr int STAGE = (TM + TN) * BK;
+    constexpr int LPT = (TM * CPI / 64 + NW - 1) / NW + (TN * CPI / 64 + NW - 1) / NW;
+    static_assert((NSK - 1) * LPT < 64, "vmcnt");
+    __shared__ __align__(16) float smem[NSK * STAGE + 256];
+    float *junk = smem + NSK * STAGE;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int li = lane & 15, lk = lane >> 4;
+    const int kb = z * g.k_per_split;
+    const int kend = min(g.K, kb + g.k_per_split);
+    const int nk = kb < kend ? (kend - kb + BK - 1) / BK : 0;
+#pragma unroll
+    for (int t = 0; t < NSK; t++) {
+        float *st = smem + t * STAGE;
+        dl_issue<false, TM, NW>(g.A, g.lda, g.M, m0, kb + t * BK, kend, st, junk, wave, lane);
+        dl_issue<BKM, TN, NW>(g.B, g.ldb, g.N, n0, kb + t * BK, kend, st + TM * BK, junk, wave, lane);
+    }
+    floatx4 acc[1][1] = {{floatx4{0.f, 0.f, 0.f, 0.f}}};
+    const int ia = wm * 16 + li, ib = wn * 16 + li;
+    // step s, unrolled (each wait takes a constant count)
+    auto step = [&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        wait_vmcnt<(NSK - 1 - s) * LPT>();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (s < nk) {                                               // uniform
+            const float *st = smem + s * STAGE, *sb = st + TM * BK;
+            floatx4 a[2], b[2];
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                a[q] = *reinterpret_cast<const floatx4 *>(st + (ia * CPI + ((4 * q + lk) ^ kc_swz(ia))) * 4);
+                if constexpr (BKM) {
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const int k = 16 * q + 4 * lk + u;
+                        b[q][u] = sb[k * TN + (ib ^ (((k >> 2) & 1) << 4))];
+                    }
+                } else {
+                    b[q] = *reinterpret_cast<const floatx4 *>(sb + (ib * CPI + ((4 * q + lk) ^ kc_swz(ib))) * 4);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 2; q++)
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[q][u], b[q][u], acc[0][0], 0, 0, 0);
+        }
+    };
+    unrolled(step, std::make_integer_sequence<int, NSK>{});
+    gemm_store<EPI, 1, 1>(g, acc, m0 + wm * 16, n0 + wn * 16, z, li, lk);
+}
+
 // The NT direct-to-LDS tile on v_mfma_f32_32x32x2_f32 (the classifier's
 // forward: both operands k-contiguous, same LDS layout and DMA loads as
 // gemm_tile_dl).  In 8-k block q, lane half h = l/32 of a 32-lane group
@@ -800,6 +872,21 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_dl32(GemmArgs g) {
     gemm_tile_dl32<TM, TN, WM, WN>(g, m * TM, n * TN, z);
 }
 
+// The per-layer panel GEMM (grid and tile order as k_gemm).
+template <bool BKM, int NSK, int EPI>
+__global__ __launch_bounds__(256) void k_gemm_panel(GemmArgs g) {
+    const int gx = gridDim.x, gy = gridDim.y, per_z = gx * gy, total = per_z * gridDim.z;
+    int m = blockIdx.y, n = blockIdx.x, z = blockIdx.z;
+    if (total >= kXcdGrid) {                                        // uniform
+        const int t = xcd_tile(blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z), total);
+        z = t / per_z;
+        const int u = t - z * per_z;
+        if (g.M > g.N) m = u / gx, n = u - m * gx;
+        else n = u / gy, m = u - n * gy;
+    }
+    gemm_tile_panel<BKM, NSK, EPI>(g, m * 32, n * 32, z);
+}
+
 // Grouped TN GEMMs (32x32 tiles, whole K): block b runs tile
 // t = xcd_tile(b) - d.tile0 of the descriptor d whose tile range holds it;
 // tiles run along N first, so neighbours share the A^T tile.  The launch
@@ -955,6 +1042,30 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
         fn = fused_norm[ek == GEMM_EPI_SWIGLU][nk_kind - 1];
     }
     int threads = 256;
+    // Per-layer 32x32 GEMMs with at most 9 K tiles per split: the panel
+    // kernel, every K tile in flight at once.  PTMI_GEMM_PANEL is a bit mask
+    // of the GEMMs that take it: 1 NT, 2 NN with the SwiGLU backward
+    // epilogue, 4 the other NN (default 3).  Measured in the stories15M T=256
+    // training step (kernel µs per step, eager trace): NT Wo + w2 72.8 ->
+    // 70.4, QKV 37.8 -> 37.0, d_sh 45.2 -> 40.2; the split-K NN (w1|w3 and
+    // QKV dX) 82.0 -> 90.9, so those keep the ring.  Graph-mode step
+    // 0.780-0.785 ms against 0.787-0.796 (mask 0) and 0.790-0.795 (mask 7).
+    static const int use_panel = [] { const char *e = getenv("PTMI_GEMM_PANEL"); return e ? atoi(e) & 7 : 3; }();
+    const int nk_split = (plan.k_per_split + BK - 1) / BK;
+    const int panel_bit = op == 2 ? 1 : ek == GEMM_EPI_SWIGLU_BWD ? 2 : 4;
+    if ((use_panel & panel_bit) && !big && vec && !nk_kind && op != 1 && nk_split <= 9) {
+        using PFn = void (*)(GemmArgs);
+        static const PFn panel[2][2][4] = {
+            {{k_gemm_panel<false, 6, GEMM_EPI_NONE>, k_gemm_panel<false, 6, GEMM_EPI_ROPE>,
+              k_gemm_panel<false, 6, GEMM_EPI_SWIGLU>, nullptr},
+             {k_gemm_panel<false, 9, GEMM_EPI_NONE>, k_gemm_panel<false, 9, GEMM_EPI_ROPE>,
+              k_gemm_panel<false, 9, GEMM_EPI_SWIGLU>, nullptr}},
+            {{k_gemm_panel<true, 6, GEMM_EPI_NONE>, nullptr, nullptr, k_gemm_panel<true, 6, GEMM_EPI_SWIGLU_BWD>},
+             {k_gemm_panel<true, 9, GEMM_EPI_NONE>, nullptr, nullptr, k_gemm_panel<true, 9, GEMM_EPI_SWIGLU_BWD>}}};
+        const int ei = ek == GEMM_EPI_NONE ? 0 : ek == GEMM_EPI_ROPE ? 1 : ek == GEMM_EPI_SWIGLU ? 2 : 3;
+        const PFn pf = panel[op == 0][nk_split > 6][ei];
+        if (pf) fn = pf;
+    }
     // The large whole-K GEMMs without a fused epilogue (the classifier's
     // forward and weight gradient) take the direct-to-LDS tiles.
     if (vec && ek == GEMM_EPI_NONE && splits == 1 && (long)M * N >= (4L << 20)) {
