@@ -41,7 +41,12 @@ struct TrainState {
     int desc_T = 0, dw_tiles = 0, n_dw = 0, dw_vec = 0, dw_cls_tiles = 0;   // entry 0: the classifier
     float *ws;
     size_t ws_floats = 0;
-    float *lr;                  // device copy of the step's learning rate
+    float *lr;                  // device copy of the step's learning rate (lr_off floats past tok)
+    // Pinned host staging: the step's tokens and learning rate laid out as
+    // tok .. lr are on the device (one copy in), then the loss (one copy out).
+    float *pin = nullptr;
+    long lr_off = 0;
+    bool pin_busy = false;      // a copy from pin may be in flight (cleared by the step's final synchronisation)
     // Bit t of tok_bits: token t is the input at some position < T-1.  Set by
     // the forward's embedding gather, read by the classifier dW GEMM (which
     // leaves those embedding rows' SGD step to the embedding backward), and
@@ -1185,6 +1190,9 @@ int train_create(ptmi_model *m) {
     e = hipMemsetAsync(ts->mem, 0, total * sizeof(float), lib_stream());
     if (e == hipSuccess) e = hipStreamSynchronize(lib_stream());
     if (e != hipSuccess) { (void)hipFree(ts->mem); delete ts; return hip_check(e, "zero training state"); }
+    ts->lr_off = ts->lr - reinterpret_cast<float *>(ts->tok);
+    e = hipHostMalloc(reinterpret_cast<void **>(&ts->pin), (size_t)(ts->lr_off + 2) * sizeof(float), hipHostMallocDefault);
+    if (e != hipSuccess) { (void)hipFree(ts->mem); delete ts; return hip_check(e, "hipHostMalloc(training staging)"); }
     const char *eager = getenv("PTMI_TRAIN_EAGER");
     ts->eager = eager && eager[0] == '1';
     const char *fuse = getenv("PTMI_TRAIN_FUSE_NORM");
@@ -1198,6 +1206,7 @@ void train_destroy(ptmi_model *m) {
     if (m->train->exec) (void)hipGraphExecDestroy(m->train->exec);
     if (m->train->graph) (void)hipGraphDestroy(m->train->graph);
     (void)hipFree(m->train->mem);
+    (void)hipHostFree(m->train->pin);
     delete m->train;
     m->train = nullptr;
 }
@@ -1606,8 +1615,12 @@ static int train_prepare(ptmi_model_t *m, const int *tokens, int T, float lr) {
         if (tokens[i] < 0 || tokens[i] >= m->c.vocab) return set_error(PTMI_ERR_ARG, "tokens[%d]=%d out of range", i, tokens[i]);
     hipStream_t s = lib_stream();
     TrainState *ts = m->train;
-    PTMI_HIP(hipMemcpyAsync(ts->tok, tokens, (size_t)T * sizeof(int), hipMemcpyHostToDevice, s));
-    PTMI_HIP(hipMemcpyAsync(ts->lr, &lr, sizeof(float), hipMemcpyHostToDevice, s));
+    // a step that returned early may have left its copy in flight
+    if (ts->pin_busy) PTMI_HIP(hipStreamSynchronize(s));
+    memcpy(ts->pin, tokens, (size_t)T * sizeof(int));
+    ts->pin[ts->lr_off] = lr;
+    ts->pin_busy = true;
+    PTMI_HIP(hipMemcpyAsync(ts->tok, ts->pin, (size_t)(ts->lr_off + 1) * sizeof(float), hipMemcpyHostToDevice, s));
     return train_descriptors(m, T);
 }
 
@@ -1640,10 +1653,11 @@ int ptmi_model_train_step(ptmi_model_t *m, const int *tokens, int T, float lr, f
         }
         PTMI_HIP(hipGraphLaunch(ts->exec, s));
     }
-    float l = 0.0f;
-    PTMI_HIP(hipMemcpyAsync(&l, m->train->loss, sizeof(float), hipMemcpyDeviceToHost, s));
+    float *l = ts->pin + ts->lr_off + 1;
+    PTMI_HIP(hipMemcpyAsync(l, ts->loss, sizeof(float), hipMemcpyDeviceToHost, s));
     PTMI_HIP(hipStreamSynchronize(s));
-    if (loss) *loss = l;
+    ts->pin_busy = false;
+    if (loss) *loss = *l;
     return PTMI_OK;
 }
 
@@ -1671,6 +1685,7 @@ int ptmi_model_train_step_trace(ptmi_model_t *m, const int *tokens, int T, float
         if (e != hipSuccess) st = hip_check(e, "loss copy");
     }
     const hipError_t es = hipStreamSynchronize(s);
+    if (es == hipSuccess) m->train->pin_busy = false;
     if (!st && es != hipSuccess) st = hip_check(es, "hipStreamSynchronize(traced train step)");
     if (!st && !tr.open.empty()) st = set_error(PTMI_ERR_STATE, "unclosed trace span %s", tr.open.back().name);
     const TrainTracer::Rec *root = nullptr;
