@@ -218,6 +218,28 @@ def test_gemm_dev_direct_lds_exact(op, M, N, K, acc):
         a.free()
 
 
+# The per-layer NT GEMMs with at most 9 K steps per split take the panel
+# kernel (every K tile of the split in flight): integer-exact at the
+# config-5 forward shapes (K split 4 ways at K = 768, summed by the split-K
+# reduction), with accumulate, and on ragged M, N and K.
+@pytest.mark.parametrize("M,N,K,acc", [(256, 864, 288, 0), (256, 288, 288, 1), (256, 1536, 288, 0),
+                                       (256, 288, 768, 1), (255, 100, 100, 0), (33, 31, 4, 1), (70, 2050, 284, 0)])
+def test_gemm_dev_panel_nt_exact(M, N, K, acc):
+    A, B = ints((M, K), 31), ints((N, K), 32)
+    ref = A.astype(np.float64) @ B.T.astype(np.float64)
+    C0 = ints((M, N), 33) if acc else np.full((M, N), np.nan, np.float32)
+    if acc:
+        ref = ref + C0
+    dA, dB, dC = DeviceArray.from_host(A), DeviceArray.from_host(B), DeviceArray.from_host(C0)
+    L = pa.load_ptmi()
+    assert L.ptmi_gemm_dev(2, dA.ptr, K, dB.ptr, K, dC.ptr, N, M, N, K, acc, None) == 0
+    assert L.ptmi_sync() == 0
+    got = dC.download().reshape(M, N)
+    assert np.array_equal(got, ref.astype(np.float32))
+    for a in (dA, dB, dC):
+        a.free()
+
+
 def test_gemm_errors():
     L = pa.load_ptmi()
     A = np.ones((4, 4), np.float32)
