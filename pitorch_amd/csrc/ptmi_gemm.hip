@@ -606,6 +606,12 @@ __device__ __forceinline__ void gemm_tile_dl(const GemmArgs &g, int m0, int n0, 
     gemm_store<EPI, FM, FN>(g, acc, m0 + wm * (TM / WM), n0 + wn * (TN / WN), z, li, lk);
 }
 
+// f(integral_constant<int, s>) for s = S...
+template <typename F, int... S>
+__device__ __forceinline__ void unrolled(F &f, std::integer_sequence<int, S...>) {
+    (f(std::integral_constant<int, S>{}), ...);
+}
+
 // The per-layer GEMMs' 32x32 tile with every K tile of its split in flight
 // at once: the block issues the DMA loads of all NSK tiles (each into its
 // own LDS stage; tiles past the split's K range load zeros) before its first
@@ -615,12 +621,6 @@ __device__ __forceinline__ void gemm_tile_dl(const GemmArgs &g, int m0, int n0, 
 // for about one.  Operand layout, MFMA k order and epilogue as
 // gemm_tile_dl with 2 x 2 waves of 16 x 16.  NT (B^T k-contiguous) or NN
 // (BKM: B stored [K][N]).
-// f(integral_constant<int, s>) for s = S...
-template <typename F, int... S>
-__device__ __forceinline__ void unrolled(F &f, std::integer_sequence<int, S...>) {
-    (f(std::integral_constant<int, S>{}), ...);
-}
-
 template <bool BKM, int NSK, int EPI>
 __device__ __forceinline__ void gemm_tile_panel(const GemmArgs &g, int m0, int n0, int z) {
     constexpr int TM = 32, TN = 32, WN = 2, NW = 4, CPI = BK / 4;
