@@ -149,6 +149,32 @@ def test_steps_with_changing_tokens_match_oracle(untied):
     om.close()
 
 
+def test_graph_and_eager_steps_give_the_same_bits(monkeypatch):
+    """The captured step (one hipGraph per T, re-captured when T changes)
+    and the eager step (PTMI_TRAIN_EAGER=1, read at model creation) run the
+    same kernels in the same order: over four steps with changing lengths,
+    a rejected call between them, the losses and the trained weights are
+    bit-identical.  Each step stages its tokens and learning rate in one
+    pinned buffer, copied in at the start and holding the loss at the end."""
+    cfg = (64, 160, 2, 4, 4, 512, 32)
+    blob = pa.synth_model(cfg, 17, 0.05)
+    runs = []
+    for eager in ("0", "1"):
+        monkeypatch.setenv("PTMI_TRAIN_EAGER", eager)
+        m = pa.Model(blob, max_T=24)
+        losses = []
+        for step, T in enumerate((24, 16, 24, 9)):
+            if step == 2:
+                with pytest.raises(pa.PtmiError):
+                    m.train_step(np.array([1, 512], np.int32), 0.05)     # token out of range
+            losses.append(m.train_step(pa.seed_tokens(40 + step, T, cfg[5]), 0.05))
+        runs.append((np.array(losses, np.float32), m.read_weights().copy()))
+        m.close()
+    assert np.array_equal(runs[0][0].view(np.uint32), runs[1][0].view(np.uint32))
+    assert np.array_equal(runs[0][1], runs[1][1])
+    assert np.all(np.isfinite(runs[0][0]))
+
+
 def test_trained_weights_drive_decode():
     """After device SGD, decode uses the updated device weights: logits equal
     the oracle's decode on the oracle's own trained blob."""
