@@ -52,6 +52,15 @@ constexpr int kRowsD = 2 * kW;               // rows per block, D-length rows (3
 constexpr int kRowsH = kW;                   // rows per block, H-length rows (64 lanes per row)
 constexpr int kAttRows = 128;                // attention positions per unit (at most)
 constexpr int kMaxChunks = 8;                // units per head
+// Copies of the w1|w3 stage input x_a (Wo's output), in kRepXa regions of
+// L*D tagged words.  Every workgroup polls the whole vector at once, and
+// workgroup b polls copy b % kRepXa: the chip's workgroups are dealt to its 8
+// XCDs in turn, so each copy's lines are read from one XCD.  Same box,
+// stories110M tok/s: one copy 6070-6080, 4 copies 6133-6136, 8 copies
+// 6156-6171, 16 copies 6071-6073.  Copies of x_b (the next QKV and the
+// classifier input) or of the hidden vector were slower: the storing waves
+// wait for their extra stores before their next poll.
+constexpr int kRepXa = 8;
 constexpr int kWriter = kW - 1;              // the wave that issues the workgroup's global stores (not w1|w3's, nor w2's at dim 768)
 constexpr int kPollT = kWriter * 64;         // threads that poll (all other waves)
 constexpr int kMaxHd = 64;                   // head_dim of the instantiated kernels (16 lanes x float4)
@@ -78,7 +87,7 @@ struct StepArgs {
     uint64_t *t_qkv;                         // [L][D + 2KV]
     uint64_t *t_part;                        // [L][NH][n_chunks][hd + 2]  (o[hd], max, sum)
     uint64_t *t_att;                         // [L][D]  merged attention output per head
-    uint64_t *t_xa, *t_xb;                   // [L][D]
+    uint64_t *t_xa, *t_xb;                   // [kRepXa][L][D], [L][D]
     uint64_t *t_hb;                          // [L][H]
     uint64_t *t_cand;                        // [nb][2]  (best logit, its index)
     // optional stage stamps (PTMI_STEP_STAMPS=1): per workgroup, the 100 MHz
@@ -1023,8 +1032,11 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     const int slot = slot_d();
                     if ((lane & 31) == 0) sm.yout[slot] = sm.xres[slot] + acc;
                     __syncthreads();
-                    if (wave == kWriter && lane < kRowsD && rb * kRowsD + lane < D)
-                        tstore(t_xa + rb * kRowsD + lane, sm.yout[lane], tk.tag);
+                    if (wave == kWriter && lane < kRowsD && rb * kRowsD + lane < D) {
+#pragma unroll
+                        for (int r = 0; r < kRepXa; r++)
+                            tstore(t_xa + (long)r * a->L * D + rb * kRowsD + lane, sm.yout[lane], tk.tag);
+                    }
                 }
                 stamp(a, sm.st, 6 + 10 * l);
             }
@@ -1040,7 +1052,8 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             const int blocks_w13 = (2 * H + kRowsD - 1) / kRowsD, blocks_w2 = (D + kRowsH - 1) / kRowsH;
             if (b < blocks_w13) {
                 __syncthreads();                              // xs and xres2 are free again
-                bool ok = tid >= kPollT || poll_pairs<kPD>(a->t_xa + (long)l * D, D, tk.tag, sm.xs, a, tid);
+                bool ok = tid >= kPollT ||
+                          poll_pairs<kPD>(a->t_xa + (long)(b % kRepXa) * a->L * D + (long)l * D, D, tk.tag, sm.xs, a, tid);
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, sm.st, 7 + 10 * l);
                 // the W2 residual rows are rows of this same input
@@ -1380,7 +1393,7 @@ int decode_step_create(ptmi_model *m) {
     const long L = c.n_layers, D = c.dim, H = c.hidden, KV = c.kv_dim, NH = c.n_heads, hd = c.head_dim;
     const int nb = std::min(cus, 512);
     // tagged words, then the argument block (32-byte aligned)
-    const size_t words = L * (D + 2 * KV) + L * nc * NH * (hd + 2) + 3 * L * D + L * H + 2 * (size_t)nb;
+    const size_t words = L * (D + 2 * KV) + L * nc * NH * (hd + 2) + (2 + kRepXa) * L * D + L * H + 2 * (size_t)nb;
     const char *st_env = getenv("PTMI_STEP_STAMPS");
     const int n_stamps = (st_env && st_env[0] == '1') ? (int)(1 + 10 * L + 4) : 0;
     if (n_stamps > kStampSlots)
@@ -1428,7 +1441,7 @@ int decode_step_create(ptmi_model *m) {
     a.t_qkv = p;  p += L * (D + 2 * KV);
     a.t_part = p; p += L * nc * NH * (hd + 2);
     a.t_att = p;  p += L * D;
-    a.t_xa = p;   p += L * D;
+    a.t_xa = p;   p += kRepXa * L * D;
     a.t_xb = p;   p += L * D;
     a.t_hb = p;   p += L * H;
     a.t_cand = p;
