@@ -61,7 +61,13 @@ constexpr int kMaxChunks = 8;                // units per head
 // classifier input) or of the hidden vector were slower: the storing waves
 // wait for their extra stores before their next poll.
 constexpr int kRepXa = 8;
-constexpr int kWriter = kW - 1;              // the wave that issues the workgroup's global stores (not w1|w3's, nor w2's at dim 768)
+// w2's waves store their own rows (no barrier) on the instantiations with
+// 6 float4 per lane of a dim row (dim 768), and the copies of x_b that the
+// other instantiations store after w2's barrier (kernel and host agree
+// through these two functions).
+constexpr bool w2_direct(int itd) { return itd >= 6; }
+constexpr int rep_xb(int itd) { return w2_direct(itd) ? 1 : kW; }
+constexpr int kWriter = kW - 1;              // the wave that issues the workgroup's global stores (not w1|w3's or w2's)
 constexpr int kPollT = kWriter * 64;         // threads that poll (all other waves)
 constexpr int kMaxHd = 64;                   // head_dim of the instantiated kernels (16 lanes x float4)
 constexpr int kPartLds = kMaxChunks * (kMaxHd + 2);  // floats of one head's chunk records
@@ -87,7 +93,7 @@ struct StepArgs {
     uint64_t *t_qkv;                         // [L][D + 2KV]
     uint64_t *t_part;                        // [L][NH][n_chunks][hd + 2]  (o[hd], max, sum)
     uint64_t *t_att;                         // [L][D]  merged attention output per head
-    uint64_t *t_xa, *t_xb;                   // [kRepXa][L][D], [L][D]
+    uint64_t *t_xa, *t_xb;                   // [kRepXa][L][D], [rep_xb(itd)][L][D]
     uint64_t *t_hb;                          // [L][H]
     uint64_t *t_cand;                        // [nb][2]  (best logit, its index)
     // optional stage stamps (PTMI_STEP_STAMPS=1): per workgroup, the 100 MHz
@@ -614,7 +620,15 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
     // writer wave / own stores (w1|w3 storing its own in both): stories110M
     // 6009 / 6075, stories42M 9392 / 8802, stories15M 13043 / 12589.  (A
     // run-time switch between the two cost 0.5-1.2% on every shape.)
-    constexpr bool kW2Direct = ITD >= 6;
+    constexpr bool kW2Direct = w2_direct(ITD);
+    // Copies of each layer's output x_b (the next QKV input, the last one
+    // the classifier's), stored one per wave after the w2 barrier and polled
+    // as copy b % kW, where w2 goes through that barrier (the smaller
+    // instantiations); with w2's direct stores a single copy.  Same box,
+    // tok/s: stories42M 9704-9713 against 9554-9563, stories15M
+    // 13257-13324 against 13200-13245; stories110M with the barrier and
+    // copies 6139-6141 against 6151-6166 with its direct stores.
+    constexpr int kRepXb = rep_xb(ITD);
     // word pairs per polling thread of a dim-length and a hidden-length vector
     constexpr int kPD = (ITD * 64 + kPollT - 1) / kPollT, kPH8 = (ITH * 128 + kT - 1) / kT;
     __shared__ Smem sm;
@@ -714,7 +728,9 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     const float *x = a->emb + (long)tk.token * D;
                     for (int i = tid; i < D; i += kT) sm.xs[i] = gl(x)[i];
                 } else {
-                    ok = tid >= kPollT || poll_pairs<kPD>(a->t_xb + (long)(l - 1) * D, D, tk.tag, sm.xs, a, tid);
+                    const uint64_t *src = a->t_xb + (long)(l - 1) * D;
+                    if constexpr (kRepXb > 1) src += (long)(b % kRepXb) * a->L * D;
+                    ok = tid >= kPollT || poll_pairs<kPD>(src, D, tk.tag, sm.xs, a, tid);
                 }
                 if (!block_ok(ok, &sm.fail, a->ctl)) return;
                 stamp(a, sm.st, 1 + 10 * l);
@@ -1132,8 +1148,9 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
                     } else {
                         if (lane == 0) sm.yout[wave] = sm.xres2[wave] + acc;
                         __syncthreads();
-                        if (wave == kWriter && lane < kRowsH && rb * kRowsH + lane < D)
-                            tstore(t_xb + rb * kRowsH + lane, sm.yout[lane], tk.tag);
+                        // wave r stores copy r of the block's kRowsH values
+                        if (lane < kRowsH && rb * kRowsH + lane < D)
+                            tstore(t_xb + (long)wave * a->L * D + rb * kRowsH + lane, sm.yout[lane], tk.tag);
                     }
                 }
                 stamp(a, sm.st, 10 + 10 * l);
@@ -1186,7 +1203,9 @@ __global__ __launch_bounds__(kT) void k_decode_step(const StepArgs *ap, int g0, 
             float4 wB[ITD], xr[ITD];
             if (b + nb < blocks_cls) load_rows_d(a, wB, a->wcls, a->V, b + nb);
             __syncthreads();
-            bool ok = tid >= kPollT || poll_pairs<kPD>(a->t_xb + (long)(a->L - 1) * a->D, a->D, tk.tag, sm.xs, a, tid);
+            const uint64_t *src = a->t_xb + (long)(a->L - 1) * a->D;
+            if constexpr (kRepXb > 1) src += (long)(b % kRepXb) * a->L * a->D;
+            bool ok = tid >= kPollT || poll_pairs<kPD>(src, a->D, tk.tag, sm.xs, a, tid);
             if (!block_ok(ok, &sm.fail, a->ctl)) return;
             stamp(a, sm.st, 1 + 10 * a->L);
             norm_x_d(a, R, sm.xs, xr);
@@ -1393,7 +1412,8 @@ int decode_step_create(ptmi_model *m) {
     const long L = c.n_layers, D = c.dim, H = c.hidden, KV = c.kv_dim, NH = c.n_heads, hd = c.head_dim;
     const int nb = std::min(cus, 512);
     // tagged words, then the argument block (32-byte aligned)
-    const size_t words = L * (D + 2 * KV) + L * nc * NH * (hd + 2) + (2 + kRepXa) * L * D + L * H + 2 * (size_t)nb;
+    const size_t words = L * (D + 2 * KV) + L * nc * NH * (hd + 2) + (1 + kRepXa + rep_xb(plan.k->itd)) * L * D +
+                         L * H + 2 * (size_t)nb;
     const char *st_env = getenv("PTMI_STEP_STAMPS");
     const int n_stamps = (st_env && st_env[0] == '1') ? (int)(1 + 10 * L + 4) : 0;
     if (n_stamps > kStampSlots)
@@ -1442,7 +1462,7 @@ int decode_step_create(ptmi_model *m) {
     a.t_part = p; p += L * nc * NH * (hd + 2);
     a.t_att = p;  p += L * D;
     a.t_xa = p;   p += kRepXa * L * D;
-    a.t_xb = p;   p += L * D;
+    a.t_xb = p;   p += rep_xb(plan.k->itd) * L * D;
     a.t_hb = p;   p += L * H;
     a.t_cand = p;
     a.stamps = n_stamps ? reinterpret_cast<uint64_t *>(mem + stamps_off) : nullptr;
