@@ -929,7 +929,7 @@ SplitPlan split_plan(int op, int M, int N, int K, size_t ws_floats, int ek) {
     const int nk = (K + BK - 1) / BK;
     int splits = 1;
     if (big && K >= 4096 && blocks < 512) splits = (int)std::min<long>((1024 + blocks - 1) / blocks, nk / 8);
-    else if (!big && blocks < 128 && nk > 9) splits = std::min(8, nk / 6);
+    else if (!big && blocks < 128 && nk > 9) splits = std::min(8, nk / 8);
     while (splits > 1 && (size_t)splits * M * N > ws_floats) splits--;
     const int chosen = std::max(1, splits);
     const int kps = ((K + chosen - 1) / chosen + BK - 1) / BK * BK;
@@ -993,8 +993,11 @@ int launch_gemm(int op, const float *A, long lda, const float *B, long ldb, floa
     // replayed launches): 32x32 tiles win everywhere except long K (>= 4096:
     // 64x64 with K split over >= 512 blocks) and large NT outputs (>= 4M
     // elements: 64x64).  Every small GEMM is bound by the latency of its K
-    // steps, so K is split when a 32x32 grid is small and K long: about six
-    // K steps per split (K=768: 4 splits, 9.3 vs 14.6 us; K=1536: 8 splits).
+    // steps, so K is split when a 32x32 grid is small and K long: about
+    // eight K steps per split (K=768: 3 splits, K=864: 3, K=1536: 6).  With
+    // the panel kernel taking up to 9 K steps at once, eight per split ran
+    // the stories15M T=256 step in 0.769-0.771 ms against 0.778-0.783 with
+    // six (12.9 us less kernel time per step); nine and ten were no faster.
     const bool big = gemm_big_tiles(op, M, N, K);
     const int TM = big ? 64 : 32, TN = TM;
     const int gx = (N + TN - 1) / TN, gy = (M + TM - 1) / TM;
